@@ -1,0 +1,171 @@
+/*
+ * stratakv_amd.h -- C ABI of the MI355X (gfx950) paged KV-cache hot path.
+ *
+ * Plain C types only: bf16 values are `uint16_t` bit patterns, block tables are
+ * `int32_t`, outputs are `float`, a stream is an opaque `void*` (a hipStream_t;
+ * NULL is the default stream).  Every entry point returns an `int` status
+ * (SKV_OK == 0) and never throws; `skv_last_error()` gives the message of the
+ * last failure on the calling thread.  Nothing on the append/decode path
+ * allocates: the caller passes every buffer, including a workspace sized by
+ * `skv_paged_decode_workspace_bytes`.
+ *
+ * KV layout (unchanged from the reference, src/models/transformer_block.cpp:493-499,
+ * src/layers/attention.cpp:137-151): separate K and V pools, each
+ *     [total_blocks][block_size][num_kv_heads][head_dim]   (bf16)
+ * element offset = ((block * block_size + slot) * num_kv_heads + kv_head) * head_dim + d,
+ * computed in 64-bit.  The reference stores FP32; this build stores bf16 in the
+ * same index space.
+ *
+ * Reference interfaces replaced (paths relative to the StrataKV source tree):
+ *   skv_kv_append               <- the two cudaMemcpy D2D of one token's K/V rows,
+ *                                  src/models/transformer_block.cpp:484-509
+ *                                  (CPU twin src/layers/attention.cpp:236-259)
+ *   skv_paged_attention_decode  <- paged_attention_decode_cuda,
+ *                                  include/stratakv/cuda/gemm_cuda.h:40-44,
+ *                                  src/cuda/gemm_cuda.cu:915-935
+ *   skv_paged_decode            <- the same, batched over sequences (the reference
+ *                                  decodes exactly one sequence per call)
+ *   skv_malloc / skv_free / skv_memcpy_*
+ *                               <- the cudaMalloc/cudaFree/cudaMemcpy calls of
+ *                                  BlockPool and PageTable,
+ *                                  src/memory/block_pool.cpp:175-206,
+ *                                  src/memory/page_table.cpp:289-347
+ */
+#ifndef STRATAKV_AMD_H
+#define STRATAKV_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------- */
+#define SKV_OK                   0
+#define SKV_ERR_INVALID_ARGUMENT 1  /* reference: std::invalid_argument        */
+#define SKV_ERR_HIP              2  /* reference: CUDA failure -> runtime_error */
+#define SKV_ERR_WORKSPACE        3  /* workspace missing or too small           */
+#define SKV_ERR_UNSUPPORTED      4  /* shape outside every compiled kernel      */
+
+/* ---- element types ------------------------------------------------------- */
+#define SKV_DTYPE_BF16 0
+#define SKV_DTYPE_FP32 1
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* skv_last_error(void);
+/* ABI version, bumped on any signature change. */
+int skv_abi_version(void);
+
+/* ---- device plumbing (no counterpart on the hot path; used by the C++
+ *      BlockPool/PageTable, the tests and the benchmark) -------------------- */
+int skv_device_count(int* count);
+int skv_set_device(int device);
+int skv_malloc(void** ptr, size_t bytes);
+int skv_free(void* ptr);
+int skv_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int skv_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int skv_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+int skv_memset_d8(void* dst, int value, size_t bytes, void* stream);
+int skv_stream_create(void** stream);
+int skv_stream_destroy(void* stream);
+int skv_stream_synchronize(void* stream);
+int skv_device_synchronize(void);
+/* Events for timing on a given stream. */
+int skv_event_create(void** event);
+int skv_event_destroy(void* event);
+int skv_event_record(void* event, void* stream);
+int skv_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* ---- synthetic data ------------------------------------------------------ */
+/* dst[i] = bf16_rne(N(0,1) sample derived from (seed, first_index + i)) via a
+ * counter hash (no library RNG), so any sub-range can be regenerated alone. */
+int skv_fill_normal_bf16(uint16_t* dst, size_t count, uint64_t seed,
+                         uint64_t first_index, void* stream);
+/* Fill count elements of a bf16 buffer with one 16-bit pattern. */
+int skv_fill_u16(uint16_t* dst, size_t count, uint16_t value, void* stream);
+
+/* ---- KV append ------------------------------------------------------------
+ * Scatter new tokens' K and V rows into the paged pools through the block
+ * tables.  Token j of sequence b (its row is
+ *     k_new[(token_offsets ? token_offsets[b] : b * tokens_per_seq) + j]
+ * a row being num_kv_heads*head_dim elements) lands at logical position
+ * positions[b] + j of that sequence:
+ *     block = block_tables[b * max_blocks_per_seq + pos / block_size],
+ *     slot  = pos % block_size.
+ * Sequence b receives tokens_per_seq tokens, or, when token_offsets is
+ * non-NULL, min(token_offsets[b+1]-token_offsets[b], tokens_per_seq) tokens
+ * (ragged batches pass the longest count as tokens_per_seq).
+ * src_dtype SKV_DTYPE_BF16: the pool receives the input bits unchanged.
+ * src_dtype SKV_DTYPE_FP32: round-to-nearest-even to bf16 with the rule of
+ * Tensor::set_value (src/cpu/tensor.cpp:209-229).
+ * Rows whose table entry falls outside [0, total_blocks) or whose position
+ * falls outside the table are skipped, never written.
+ * Replaces: src/models/transformer_block.cpp:484-509. */
+int skv_kv_append(const void* k_new, const void* v_new, int src_dtype,
+                  uint16_t* k_pool, uint16_t* v_pool, int64_t total_blocks,
+                  const int32_t* block_tables, int max_blocks_per_seq,
+                  const int32_t* positions, const int32_t* token_offsets,
+                  int num_seqs, int tokens_per_seq,
+                  int num_kv_heads, int head_dim, int block_size,
+                  void* stream);
+
+/* ---- paged decode attention ---------------------------------------------
+ * One query token per sequence, grouped-query attention over the paged pools:
+ * q head h reads kv head h / (num_q_heads / num_kv_heads) (reference
+ * src/cuda/gemm_cuda.cu:324-325, src/layers/attention.cpp:270).
+ *   q     [num_seqs][num_q_heads][head_dim], bf16 or fp32 (q_dtype)
+ *   out   [num_seqs][num_q_heads][head_dim], fp32
+ *   out[b,h] = sum_t softmax_t(scale * q[b,h].k_t) v_t over t < context_lens[b]
+ * fp32 accumulation.  Sequences with context_lens[b] <= 0 produce zeros.
+ * Context positions beyond max_blocks_per_seq*block_size and table entries
+ * outside [0, total_blocks) are not read.
+ * workspace: device memory of at least skv_paged_decode_workspace_bytes(...)
+ * bytes for the same arguments; its contents need no initialisation.
+ * Replaces: paged_attention_decode_cuda (include/stratakv/cuda/gemm_cuda.h:40-44). */
+size_t skv_paged_decode_workspace_bytes(int num_seqs, int num_q_heads,
+                                        int num_kv_heads, int head_dim);
+int skv_paged_decode(const void* q, int q_dtype,
+                     const uint16_t* k_pool, const uint16_t* v_pool,
+                     int64_t total_blocks,
+                     const int32_t* block_tables, int max_blocks_per_seq,
+                     const int32_t* context_lens, int num_seqs,
+                     int num_q_heads, int num_kv_heads, int head_dim,
+                     int block_size, float scale, float* out,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Single-sequence decode with the reference's argument list (gemm_cuda.h:41-44)
+ * on bf16 pools, plus the pool size, workspace and stream.  Equivalent to
+ * skv_paged_decode with num_seqs = 1, an fp32 query, max_blocks_per_seq =
+ * ceil(context_len / block_size) and context_lens = {context_len}; the
+ * context length is passed to the kernels by value (no host-device copy).
+ * Invalid arguments (context_len <= 0, num_q_heads % num_kv_heads != 0,
+ * non-finite or non-positive scale, NULL pointers) return
+ * SKV_ERR_INVALID_ARGUMENT like the reference's std::invalid_argument
+ * (src/cuda/gemm_cuda.cu:920-928). */
+size_t skv_paged_attention_decode_workspace_bytes(int num_q_heads,
+                                                  int num_kv_heads,
+                                                  int head_dim);
+int skv_paged_attention_decode(const float* query, const uint16_t* key_cache,
+                               const uint16_t* value_cache,
+                               int64_t total_blocks,
+                               const int32_t* block_table, float* output,
+                               int context_len, int block_size,
+                               int num_q_heads, int num_kv_heads, int head_dim,
+                               float scale, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/* ---- test support --------------------------------------------------------
+ * Copy the blocks listed in table[0..num_blocks) of a pool into a contiguous
+ * device buffer dst[num_blocks][block_elems] (so one sequence can be read back
+ * without copying a whole pool).  Entries outside [0, total_blocks) give
+ * zero-filled blocks. */
+int skv_gather_blocks(const uint16_t* pool, int64_t total_blocks,
+                      const int32_t* table, int num_blocks,
+                      int64_t block_elems, uint16_t* dst, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRATAKV_AMD_H */

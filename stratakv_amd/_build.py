@@ -1,0 +1,88 @@
+"""Build recipes for the native parts of stratakv_amd.
+
+Everything is compiled in-tree so the built files travel with the source tree:
+
+* ``stratakv_amd/libstratakv_amd.so`` -- the gfx950 HIP kernels, the C ABI
+  (``include/stratakv_amd.h``) and the C++17 host layer (``include/stratakv/``),
+  built with ``hipcc --offload-arch=gfx950``.
+* ``build/bin/*`` -- the C++ test programs under ``tests/cpp``.
+* ``oracle/liboracle.so`` and, when the StrataKV sources are present,
+  ``oracle/_ref/libstratakv_ref.so`` -- test infrastructure (``oracle/Makefile``).
+"""
+from __future__ import annotations
+
+import glob
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "stratakv_amd")
+CSRC = os.path.join(PKG, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+LIB = os.path.join(PKG, "libstratakv_amd.so")
+BIN = os.path.join(ROOT, "build", "bin")
+ORACLE = os.path.join(ROOT, "oracle")
+REFERENCE = os.environ.get("STRATAKV_REFERENCE", "/root/reference")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+# Packed fp32 VALU forms are kept out of every kernel (the compiler otherwise
+# forms v_pk_* from float2-shaped code); the host pass ignores the feature.
+NO_PACKED_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall"] + NO_PACKED_FP32
+
+
+def _run(cmd: list[str], cwd: str | None = None) -> None:
+    proc = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in proc.stdout.splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        sys.stderr.write(out + "\n")
+
+
+def build_library() -> str:
+    """Compile the HIP kernels, C ABI and C++ host layer into one shared library."""
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    host = sorted(glob.glob(os.path.join(CSRC, "host", "*.cpp")))
+    cmd = [HIPCC, *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}", *sources]
+    for h in host:
+        cmd += ["-x", "c++", h]
+    cmd += ["-o", LIB + ".tmp"]
+    _run(cmd)
+    os.replace(LIB + ".tmp", LIB)
+    return LIB
+
+
+def build_cpp_tests() -> list[str]:
+    """Compile tests/cpp/*.cpp against the library (and the oracle, for traces)."""
+    os.makedirs(BIN, exist_ok=True)
+    outs = []
+    for src in sorted(glob.glob(os.path.join(ROOT, "tests", "cpp", "*.cpp"))):
+        exe = os.path.join(BIN, os.path.splitext(os.path.basename(src))[0])
+        cmd = [HIPCC, "-O2", "-std=c++17", f"-I{INCLUDE}", f"-I{ORACLE}", "-x", "c++", src,
+               f"-L{PKG}", "-lstratakv_amd", f"-Wl,-rpath,{PKG}",
+               f"-L{ORACLE}", "-loracle", f"-Wl,-rpath,{ORACLE}", "-o", exe]
+        _run(cmd)
+        outs.append(exe)
+    return outs
+
+
+def build_oracle() -> None:
+    """Test infrastructure: the C oracle, plus the reference checker when present."""
+    _run(["make", "-B", "-C", ORACLE, "all"])
+    if os.path.isdir(os.path.join(REFERENCE, "src")):
+        _run(["make", "-B", "-C", ORACLE, "ref", f"REF={REFERENCE}"])
+
+
+def build_all() -> None:
+    build_library()
+    build_oracle()
+    build_cpp_tests()
+
+
+if __name__ == "__main__":
+    build_all()
+    print("built", LIB)

@@ -1,0 +1,248 @@
+// skv_runtime.hip -- error state, device plumbing, synthetic data and test
+// support entry points of the C ABI (include/stratakv_amd.h).
+#include "skv_common.h"
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdlib>
+#include <cstring>
+
+namespace skv {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int set_error(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+bool sync_kernels_enabled() {
+    static const bool enabled = [] {
+        const char* v = std::getenv("STRATAKV_SYNC_KERNELS");
+        return v != nullptr && v[0] == '1';
+    }();
+    return enabled;
+}
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return set_error(SKV_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
+    if (sync_kernels_enabled()) {
+        e = hipDeviceSynchronize();
+        if (e != hipSuccess)
+            return set_error(SKV_ERR_HIP, "%s failed: %s", what, hipGetErrorString(e));
+    }
+    return SKV_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Counter-hash normal generator.  Each element's value depends only on
+// (seed, index), so any slice of a pool can be regenerated independently.
+// splitmix64 finaliser for mixing, Box-Muller for the normal deviate.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ void fill_normal_bf16_kernel(uint16_t* __restrict__ dst, size_t count,
+                                        uint64_t seed, uint64_t first) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+         i < count; i += stride) {
+        const uint64_t h = mix64(seed ^ mix64(first + i));
+        const float u1 = (static_cast<float>(static_cast<uint32_t>(h >> 40)) + 1.0f) *
+                         (1.0f / 16777216.0f);                      // (0, 1]
+        const float u2 = static_cast<float>(static_cast<uint32_t>(h & 0xFFFFFFu)) *
+                         (1.0f / 16777216.0f);                      // [0, 1)
+        const float r = sqrtf(-2.0f * logf(u1));
+        const float z = r * cospif(2.0f * u2);
+        dst[i] = static_cast<uint16_t>(f32_to_bf16_bits(z));
+    }
+}
+
+__global__ void fill_u16_kernel(uint16_t* __restrict__ dst, size_t count, uint16_t value) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+         i < count; i += stride)
+        dst[i] = value;
+}
+
+// Gather whole blocks listed in a table into a contiguous buffer.
+__global__ void gather_blocks_kernel(const uint16_t* __restrict__ pool, int64_t total_blocks,
+                                     const int32_t* __restrict__ table, int num_blocks,
+                                     int64_t block_elems, uint16_t* __restrict__ dst) {
+    const int i = blockIdx.y;
+    const int64_t pb = table[i];
+    const bool ok = pb >= 0 && pb < total_blocks;
+    uint16_t* out = dst + static_cast<int64_t>(i) * block_elems;
+    const uint16_t* in = pool + pb * block_elems;
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+         e < block_elems; e += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        out[e] = ok ? in[e] : uint16_t(0);
+}
+
+}  // namespace skv
+
+using namespace skv;
+
+extern "C" {
+
+const char* skv_last_error(void) { return g_last_error.c_str(); }
+
+int skv_abi_version(void) { return 1; }
+
+int skv_device_count(int* count) {
+    SKV_REQUIRE(count != nullptr, "skv_device_count: count is NULL");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) n = 0;
+    *count = n;
+    return SKV_OK;
+}
+
+int skv_set_device(int device) {
+    SKV_HIP_TRY(hipSetDevice(device));
+    return SKV_OK;
+}
+
+int skv_malloc(void** ptr, size_t bytes) {
+    SKV_REQUIRE(ptr != nullptr, "skv_malloc: ptr is NULL");
+    *ptr = nullptr;
+    if (bytes == 0) return SKV_OK;
+    SKV_HIP_TRY(hipMalloc(ptr, bytes));
+    return SKV_OK;
+}
+
+int skv_free(void* ptr) {
+    if (ptr != nullptr) SKV_HIP_TRY(hipFree(ptr));
+    return SKV_OK;
+}
+
+int skv_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return SKV_OK;
+    SKV_REQUIRE(dst && src, "skv_memcpy_h2d: NULL pointer");
+    SKV_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice,
+                               static_cast<hipStream_t>(stream)));
+    SKV_HIP_TRY(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return SKV_OK;
+}
+
+int skv_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return SKV_OK;
+    SKV_REQUIRE(dst && src, "skv_memcpy_d2h: NULL pointer");
+    SKV_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost,
+                               static_cast<hipStream_t>(stream)));
+    SKV_HIP_TRY(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return SKV_OK;
+}
+
+int skv_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return SKV_OK;
+    SKV_REQUIRE(dst && src, "skv_memcpy_d2d: NULL pointer");
+    SKV_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
+                               static_cast<hipStream_t>(stream)));
+    return SKV_OK;
+}
+
+int skv_memset_d8(void* dst, int value, size_t bytes, void* stream) {
+    if (bytes == 0) return SKV_OK;
+    SKV_REQUIRE(dst != nullptr, "skv_memset_d8: NULL pointer");
+    SKV_HIP_TRY(hipMemsetAsync(dst, value, bytes, static_cast<hipStream_t>(stream)));
+    return SKV_OK;
+}
+
+int skv_stream_create(void** stream) {
+    SKV_REQUIRE(stream != nullptr, "skv_stream_create: NULL out pointer");
+    hipStream_t s = nullptr;
+    SKV_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return SKV_OK;
+}
+
+int skv_stream_destroy(void* stream) {
+    if (stream != nullptr) SKV_HIP_TRY(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+    return SKV_OK;
+}
+
+int skv_stream_synchronize(void* stream) {
+    SKV_HIP_TRY(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return SKV_OK;
+}
+
+int skv_device_synchronize(void) {
+    SKV_HIP_TRY(hipDeviceSynchronize());
+    return SKV_OK;
+}
+
+int skv_event_create(void** event) {
+    SKV_REQUIRE(event != nullptr, "skv_event_create: NULL out pointer");
+    hipEvent_t e = nullptr;
+    SKV_HIP_TRY(hipEventCreate(&e));
+    *event = e;
+    return SKV_OK;
+}
+
+int skv_event_destroy(void* event) {
+    if (event != nullptr) SKV_HIP_TRY(hipEventDestroy(static_cast<hipEvent_t>(event)));
+    return SKV_OK;
+}
+
+int skv_event_record(void* event, void* stream) {
+    SKV_REQUIRE(event != nullptr, "skv_event_record: NULL event");
+    SKV_HIP_TRY(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)));
+    return SKV_OK;
+}
+
+int skv_event_elapsed_ms(float* ms, void* start, void* stop) {
+    SKV_REQUIRE(ms && start && stop, "skv_event_elapsed_ms: NULL argument");
+    SKV_HIP_TRY(hipEventSynchronize(static_cast<hipEvent_t>(stop)));
+    SKV_HIP_TRY(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
+                                    static_cast<hipEvent_t>(stop)));
+    return SKV_OK;
+}
+
+int skv_fill_normal_bf16(uint16_t* dst, size_t count, uint64_t seed, uint64_t first_index,
+                         void* stream) {
+    if (count == 0) return SKV_OK;
+    SKV_REQUIRE(dst != nullptr, "skv_fill_normal_bf16: NULL destination");
+    const unsigned grid = static_cast<unsigned>(std::min<size_t>(cdiv<size_t>(count, 256), 16384));
+    fill_normal_bf16_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+        dst, count, seed, first_index);
+    return check_launch("fill_normal_bf16_kernel");
+}
+
+int skv_fill_u16(uint16_t* dst, size_t count, uint16_t value, void* stream) {
+    if (count == 0) return SKV_OK;
+    SKV_REQUIRE(dst != nullptr, "skv_fill_u16: NULL destination");
+    const unsigned grid = static_cast<unsigned>(std::min<size_t>(cdiv<size_t>(count, 256), 16384));
+    fill_u16_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(dst, count, value);
+    return check_launch("fill_u16_kernel");
+}
+
+int skv_gather_blocks(const uint16_t* pool, int64_t total_blocks, const int32_t* table,
+                      int num_blocks, int64_t block_elems, uint16_t* dst, void* stream) {
+    if (num_blocks == 0) return SKV_OK;
+    SKV_REQUIRE(pool && table && dst, "skv_gather_blocks: NULL pointer");
+    SKV_REQUIRE(num_blocks > 0 && num_blocks <= 65535 && block_elems > 0 && total_blocks > 0,
+                "skv_gather_blocks: invalid sizes (num_blocks=%d, block_elems=%lld)",
+                num_blocks, static_cast<long long>(block_elems));
+    const unsigned gx = static_cast<unsigned>(std::min<int64_t>(cdiv<int64_t>(block_elems, 256), 64));
+    gather_blocks_kernel<<<dim3(gx, num_blocks), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        pool, total_blocks, table, num_blocks, block_elems, dst);
+    return check_launch("gather_blocks_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,70 @@
+"""The C ABI library on the CPU: it loads, exports every symbol the header
+declares, sizes workspaces, and rejects invalid arguments with the
+reference's invalid_argument semantics (src/cuda/gemm_cuda.cu:920-928) before
+touching a device.  No kernel runs here."""
+import ctypes
+import math
+
+import pytest
+
+import stratakv_amd as skv
+
+
+def test_library_exports_every_header_symbol():
+    names = skv.header_symbols()
+    assert len(names) >= 20
+    lib = ctypes.CDLL(skv.LIB_PATH)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    assert skv.lib().skv_abi_version() >= 1
+
+
+def test_workspace_sizes_are_positive_and_monotone():
+    small = skv.decode_workspace_bytes(1, 32, 4, 64)
+    big = skv.decode_workspace_bytes(128, 32, 8, 128)
+    assert 0 < small < big
+    assert skv.decode_workspace_bytes(0, 32, 8, 128) == 0
+    single = skv.lib().skv_paged_attention_decode_workspace_bytes(32, 4, 64)
+    assert single == small
+
+
+FAKE = 0x1000  # never dereferenced: validation rejects before any device work
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(context_len=0), "context"),
+    (dict(num_q_heads=6, num_kv_heads=4), "multiple"),
+    (dict(scale=0.0), "scale"),
+    (dict(scale=math.inf), "scale"),
+    (dict(scale=math.nan), "scale"),
+    (dict(block_size=0), "dimensions"),
+    (dict(query=None), "pointers"),
+])
+def test_single_decode_rejects_invalid_arguments(kw, msg):
+    args = dict(query=FAKE, key_cache=FAKE, value_cache=FAKE, total_blocks=4, block_table=FAKE,
+                output=FAKE, context_len=5, block_size=16, num_q_heads=8, num_kv_heads=4,
+                head_dim=64, scale=0.125, workspace=FAKE, workspace_bytes=1 << 20)
+    args.update(kw)
+    with pytest.raises(skv.SkvInvalidArgument):
+        skv.paged_attention_decode(**args)
+
+
+def test_batched_decode_rejects_invalid_arguments():
+    base = dict(q=FAKE, q_dtype=skv.DTYPE_BF16, k_pool=FAKE, v_pool=FAKE, total_blocks=4,
+                block_tables=FAKE, max_blocks_per_seq=2, context_lens=FAKE, num_seqs=2,
+                num_q_heads=8, num_kv_heads=4, head_dim=64, block_size=16, scale=0.125, out=FAKE,
+                workspace=FAKE, workspace_bytes=1 << 30)
+    for bad in (dict(q_dtype=7), dict(num_seqs=0), dict(num_kv_heads=3), dict(total_blocks=0),
+                dict(context_lens=None)):
+        with pytest.raises(skv.SkvInvalidArgument):
+            skv.paged_decode(**dict(base, **bad))
+
+
+def test_append_rejects_invalid_arguments():
+    base = dict(k_new=FAKE, v_new=FAKE, src_dtype=skv.DTYPE_BF16, k_pool=FAKE, v_pool=FAKE,
+                total_blocks=4, block_tables=FAKE, max_blocks_per_seq=2, positions=FAKE,
+                num_seqs=1, tokens_per_seq=1, num_kv_heads=4, head_dim=64, block_size=16)
+    for bad in (dict(src_dtype=9), dict(block_size=0), dict(k_pool=None), dict(num_seqs=-1)):
+        with pytest.raises(skv.SkvInvalidArgument):
+            skv.kv_append(**dict(base, **bad))
+    skv.kv_append(**dict(base, num_seqs=0))  # empty batch is a no-op
