@@ -1,0 +1,324 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged KV-cache hot path on one MI355X.
+
+A step is one decode step of one layer over a batch of sequences: the KV
+append of one new token per sequence (skv_kv_append) followed by paged decode
+attention over every sequence's whole context (skv_paged_decode).  Inputs are
+synthetic and already resident in HBM when timing starts; the step rewrites
+each sequence's last slot (context stays the same from step to step, as the
+reference's forward_into with append_tokens=false does), so every timed step
+does identical work.
+
+Default workload: config 4 of BASELINE.json (Llama-3-8B geometry: 32 Q heads,
+8 KV heads, head_dim 128, batch 128, context lengths log-normal with median
+8192 and sigma 0.6 clipped to [2048, 32768], 16-token blocks allocated
+round-robin across sequences), the configuration the >= 70 % of HBM peak
+target is quoted on.  --config 2 / 3 select the other single-GPU attention
+configs.
+
+Output: one JSON line on stdout.  value = algorithmic bytes of a whole step
+(append + decode) / device time per step, in GB/s.  roofline = the decode
+call (planner + attention + merge kernels) against 8 TB/s.  cpu_baseline =
+the oracle's restatement of the reference CPU attention timed on this host
+on a bounded sample of sequences of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "paged decode-attn achieved HBM GB/s (% of peak) + decode tokens/sec, 1 GPU"
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD public specification
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# Workloads
+# ---------------------------------------------------------------------------
+def lifo_round_robin_tables(nbs, max_blocks):
+    """Tables as a fresh BlockPool hands blocks out (0, 1, 2, ...) when the
+    sequences take one block each in turn (round-robin, fragmented pool)."""
+    t = np.full((len(nbs), max_blocks), -1, np.int32)
+    nxt = 0
+    for k in range(max(nbs)):
+        for b, nb in enumerate(nbs):
+            if k < nb:
+                t[b, k] = nxt
+                nxt += 1
+    return t, nxt
+
+
+def workload(cfg: int):
+    bs = 16
+    if cfg == 2:
+        rng = np.random.default_rng(0x5EED0002)
+        Hq, Hkv, hd, B = 32, 4, 64, 1
+        lens = np.array([4097], np.int32)            # 4096 cached + the appended token
+        total = 65536
+        perm = rng.permutation(total).astype(np.int32)
+        nb = -(-4097 // bs)
+        tables = perm[:nb].reshape(1, nb)
+        desc = ("cfg2: batch 1, 32 Q / 4 KV heads, head_dim 64, context 4097 (4096 + 1 appended), "
+                "table = first 257 ids of a seeded permutation of a 65536-block pool")
+    elif cfg == 3:
+        rng = np.random.default_rng(0x5EED0003)
+        Hq, Hkv, hd, B = 32, 4, 64, 64
+        lens = rng.integers(512, 8193, size=B).astype(np.int32)
+        total = 1 << 20
+        perm = rng.permutation(total).astype(np.int32)
+        nbs = [-(-int(L) // bs) for L in lens]
+        tables = np.full((B, max(nbs)), -1, np.int32)
+        pos = 0
+        for b, nb in enumerate(nbs):
+            tables[b, :nb] = perm[pos:pos + nb]
+            pos += nb
+        desc = ("cfg3: batch 64, TinyLlama geometry (32 Q / 4 KV heads, head_dim 64), contexts "
+                "U[512, 8192], tables = consecutive slices of a seeded permutation of a 2^20-block pool")
+    elif cfg == 4:
+        rng = np.random.default_rng(0x5EED0004)
+        Hq, Hkv, hd, B = 32, 8, 128, 128
+        z = rng.standard_normal(B)
+        lens = np.clip(np.round(np.exp(math.log(8192) + 0.6 * z)), 2048, 32768).astype(np.int32)
+        nbs = [-(-int(L) // bs) for L in lens]
+        tables, used = lifo_round_robin_tables(nbs, max(nbs))
+        total = used + 1024
+        desc = ("cfg4: Llama-3-8B geometry (32 Q / 8 KV heads, head_dim 128), batch 128, contexts "
+                "log-normal median 8192 sigma 0.6 clipped to [2048, 32768], 16-token blocks "
+                "allocated round-robin across sequences")
+    else:
+        raise SystemExit(f"bench.py: unknown --config {cfg} (single-GPU attention configs: 2, 3, 4)")
+    return dict(cfg=cfg, Hq=Hq, Hkv=Hkv, hd=hd, B=B, bs=bs, lens=lens, tables=tables,
+                total=int(total), desc=desc, seed=0x5EED0000 + cfg)
+
+
+def algorithmic_bytes(w):
+    """Bytes each step must move at least once (K/V counted once per KV head)."""
+    B, Hq, Hkv, hd, bs = w["B"], w["Hq"], w["Hkv"], w["hd"], w["bs"]
+    L = w["lens"].astype(np.int64)
+    kv = int((2 * L * Hkv * hd * 2).sum())
+    tables = int((4 * np.ceil(L / bs)).sum()) + 4 * B
+    qo = B * Hq * hd * 2 + B * Hq * hd * 4
+    decode = kv + tables + qo
+    append = B * 2 * Hkv * hd * 2 * 2
+    flops = 4 * int(L.sum()) * Hq * hd
+    return decode, append, flops
+
+
+# ---------------------------------------------------------------------------
+# GPU run
+# ---------------------------------------------------------------------------
+def run_gpu(w, steps: int, warmup: int):
+    import stratakv_amd as skv
+
+    skv.require_gpu()
+    B, Hq, Hkv, hd, bs, total = w["B"], w["Hq"], w["Hkv"], w["hd"], w["bs"], w["total"]
+    pool_elems = total * bs * Hkv * hd
+    log(f"allocating pools: 2 x {pool_elems * 2 / 2**30:.2f} GiB")
+    stream = skv.Stream()
+    k_pool = skv.DeviceBuffer(pool_elems * 2)
+    v_pool = skv.DeviceBuffer(pool_elems * 2)
+    skv.fill_normal_bf16(k_pool, pool_elems, w["seed"], 0, stream.handle)
+    skv.fill_normal_bf16(v_pool, pool_elems, w["seed"] + 1, 0, stream.handle)
+    q = skv.DeviceBuffer(B * Hq * hd * 2)
+    skv.fill_normal_bf16(q, B * Hq * hd, w["seed"] + 2, 0, stream.handle)
+    k_new = skv.DeviceBuffer(B * Hkv * hd * 2)
+    v_new = skv.DeviceBuffer(B * Hkv * hd * 2)
+    skv.fill_normal_bf16(k_new, B * Hkv * hd, w["seed"] + 3, 0, stream.handle)
+    skv.fill_normal_bf16(v_new, B * Hkv * hd, w["seed"] + 4, 0, stream.handle)
+    tables = skv.DeviceBuffer.from_numpy(w["tables"])
+    lens = skv.DeviceBuffer.from_numpy(w["lens"])
+    positions = skv.DeviceBuffer.from_numpy(w["lens"] - 1)
+    out = skv.DeviceBuffer(B * Hq * hd * 4)
+    wsb = skv.decode_workspace_bytes(B, Hq, Hkv, hd)
+    ws = skv.DeviceBuffer(wsb)
+    max_blocks = w["tables"].shape[1]
+    scale = 1.0 / math.sqrt(hd)
+    stream.synchronize()
+    log("inputs resident; warming up")
+
+    def append():
+        skv.kv_append(k_new, v_new, skv.DTYPE_BF16, k_pool, v_pool, total, tables, max_blocks,
+                      positions, B, 1, Hkv, hd, bs, stream=stream.handle)
+
+    def decode():
+        skv.paged_decode(q, skv.DTYPE_BF16, k_pool, v_pool, total, tables, max_blocks, lens, B,
+                         Hq, Hkv, hd, bs, scale, out, ws, wsb, stream=stream.handle)
+
+    for _ in range(warmup):
+        append()
+        decode()
+    skv.synchronize()
+    log(f"warmup done ({warmup} steps); timing {steps} steps")
+
+    # Events on the launch stream: e[3i] before the append, e[3i+1] between
+    # append and decode, e[3i+2] after the decode of step i.
+    ev = [skv.Event() for _ in range(3 * steps)]
+    skv.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[3 * i].record(stream.handle)
+        append()
+        ev[3 * i + 1].record(stream.handle)
+        decode()
+        ev[3 * i + 2].record(stream.handle)
+    skv.synchronize()
+    wall = time.perf_counter() - t0
+    append_ms = [ev[3 * i].elapsed_ms(ev[3 * i + 1]) for i in range(steps)]
+    decode_ms = [ev[3 * i + 1].elapsed_ms(ev[3 * i + 2]) for i in range(steps)]
+    total_ms = ev[0].elapsed_ms(ev[3 * steps - 1])
+    log(f"timed: device {total_ms:.3f} ms, host wall {wall * 1e3:.3f} ms")
+    return dict(ms_per_step=total_ms / steps, append_ms=float(np.mean(append_ms)),
+                decode_ms=float(np.mean(decode_ms)), decode_ms_median=float(np.median(decode_ms)),
+                decode_ms_min=float(np.min(decode_ms)), wall_ms_per_step=wall * 1e3 / steps)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle (restatement of src/layers/attention.cpp:263-337)
+# ---------------------------------------------------------------------------
+def cpu_baseline(w, budget_s: float = 12.0):
+    import oracle
+
+    rng = np.random.default_rng(w["seed"] + 99)
+    B, Hq, Hkv, hd, bs = w["B"], w["Hq"], w["Hkv"], w["hd"], w["bs"]
+    order = rng.permutation(B)
+    # Estimate: the scalar loop runs ~0.16 GMAC/s on one core at head_dim 128;
+    # take sequences until ~budget_s/2 of single-thread work.
+    macs_budget = 0.16e9 * budget_s / 2
+    chosen, macs = [], 0
+    for b in order:
+        chosen.append(int(b))
+        macs += int(w["lens"][b]) * Hq * hd * 2
+        if macs >= macs_budget:
+            break
+    lens = w["lens"][chosen].astype(np.int32)
+    nbs = [-(-int(L) // bs) for L in lens]
+    tot = sum(nbs)
+    tables = np.full((len(chosen), max(nbs)), -1, np.int32)
+    pos = 0
+    for i, nb in enumerate(nbs):
+        tables[i, :nb] = np.arange(pos, pos + nb)
+        pos += nb
+    # Values do not change the loop's time: tile a 4 Mi-element random bf16 block.
+    base = oracle.f32_to_bf16(rng.standard_normal(1 << 22, dtype=np.float32))
+    kp = np.resize(base, (tot, bs, Hkv, hd))
+    vp = np.resize(base[::-1], (tot, bs, Hkv, hd))
+    q = oracle.bf16_to_f32(oracle.f32_to_bf16(rng.standard_normal((len(chosen), Hq, hd), dtype=np.float32)))
+    scale = 1.0 / math.sqrt(hd)
+    sample_bytes = int((2 * lens.astype(np.int64) * Hkv * hd * 2).sum())
+    results = {}
+    threads_all = min(os.cpu_count() or 1, 16)
+    for threads in (1, threads_all):
+        t0 = time.perf_counter()
+        oracle.paged_decode(q, kp, vp, tables, lens, Hkv, bs, scale, threads=threads)
+        dt = time.perf_counter() - t0
+        results[threads] = dt
+        log(f"cpu baseline: {len(chosen)} sequences, {threads} thread(s): {dt:.2f} s")
+    full_kv = int((2 * w["lens"].astype(np.int64) * Hkv * hd * 2).sum())
+    out = {}
+    for threads, dt in results.items():
+        gbs = sample_bytes / dt / 1e9
+        out[threads] = dict(value=round(gbs, 4), unit="GB/s", cores=threads, kind="port",
+                            tokens_per_s=round(B / (full_kv / (gbs * 1e9)), 6),
+                            sample=(f"oracle two-pass fp32 attention (restatement of "
+                                    f"src/layers/attention.cpp:263-337, gcc -O3 -mavx2 -mfma) over "
+                                    f"{len(chosen)} of {B} sequences ({int(lens.sum())} tokens, "
+                                    f"{sample_bytes / 1e6:.1f} MB of bf16 K/V) in {dt:.2f} s; "
+                                    f"GB/s on the same algorithmic bytes, tokens/s scaled by bytes "
+                                    f"to the full batch; the reference itself caches FP32, so its "
+                                    f"real traffic is twice these bytes"))
+    return out[1], out[threads_all]
+
+
+def profile_traffic(workload_key: str):
+    """HBM bytes per launch of the decode kernel from the committed rocprof
+    counter summary, if one exists for this workload."""
+    path = os.path.join(ROOT, "profiles", f"decode_traffic_{workload_key}.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=4)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}). The paged "
+              f"decode path shards by sequence or KV head with no exchange; the multi-GPU design is "
+              f"described in DESIGN.md but not built or measured.", file=sys.stderr)
+        return 2
+    w = workload(args.config)
+    dec_bytes, app_bytes, flops = algorithmic_bytes(w)
+    log(w["desc"])
+    log(f"algorithmic bytes per step: decode {dec_bytes / 1e9:.3f} GB + append {app_bytes / 1e6:.3f} MB")
+    g = run_gpu(w, args.steps, args.warmup)
+    step_s = g["ms_per_step"] / 1e3
+    value = (dec_bytes + app_bytes) / step_s / 1e9
+    achieved = dec_bytes / (g["decode_ms"] / 1e3) / 1e9
+    key = f"cfg{args.config}"
+    traffic = profile_traffic(key)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (device counter-hash N(0,1) bf16 K/V/Q, seeded)",
+        "config": {
+            "workload": w["desc"],
+            "batch": w["B"], "num_q_heads": w["Hq"], "num_kv_heads": w["Hkv"],
+            "head_dim": w["hd"], "block_size": w["bs"],
+            "context_tokens_total": int(w["lens"].sum()),
+            "context_min": int(w["lens"].min()), "context_max": int(w["lens"].max()),
+            "accumulate": "fp32", "parallelism": "none (1 GPU)",
+        },
+        "tokens_per_s": round(w["B"] / step_s, 1),
+        "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+        "append_ms": round(g["append_ms"], 5),
+        "decode_ms": round(g["decode_ms"], 5),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged decode (planner + attention + merge launches of skv_paged_decode)",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": dec_bytes,
+            "flops": flops,
+        },
+    }
+    if not args.no_cpu_baseline:
+        one, allc = cpu_baseline(w)
+        line["cpu_baseline"] = one
+        line["cpu_baseline_all_cores"] = allc
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
