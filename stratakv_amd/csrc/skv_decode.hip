@@ -3,28 +3,47 @@
 //
 // Replaces paged_attention_decode_kernel / paged_attention_decode_cuda of the
 // reference (src/cuda/gemm_cuda.cu:304-429, 915-935).  The reference runs one
-// 256-thread block per query head over one sequence, so each K/V byte is read
-// by all G = Hq/Hkv query heads of its group, and accumulates P.V in global
-// memory.  Here:
-//   * work unit = (sequence, kv head, partition of blocks).  One wavefront owns
-//     a unit and serves all G query heads of the group from one read of K/V.
-//   * a device-side planner sizes partitions from the actual context lengths
-//     so the grid holds ~16k units whatever the batch / length mix ("split-K",
-//     the flash-decoding scheme), and a merge kernel combines the partial
-//     (max, sum, acc) triples of sequences that span several partitions with
-//     a log-sum-exp rescale.
-//   * a block's rows are read 16 bytes per lane: HD/8 lanes cover one 128 or
-//     256-byte row, so one load instruction moves 64/(HD/8) full rows.
-//   * q.k partial dots are reduced across the lanes of a row with DPP
-//     butterflies (no LDS); every row group keeps its own online-softmax state
-//     and the groups are merged once per unit.
-// Softmax runs in the exp2 domain: q is pre-multiplied by scale*log2(e).
+// 256-thread block per query head of one sequence, so each K/V byte is read by
+// all G = Hq/Hkv query heads of its group, and it accumulates P.V in global
+// memory.  Here the work is organised for CDNA4:
+//
+// * Work = the (sequence, kv head, block) triples, flattened.  A planner kernel
+//   splits them evenly over exactly as many persistent wavefronts as the GPU
+//   holds at once ("stream-K"): no tail of idle CUs, and a wavefront whose
+//   range covers a whole (sequence, kv head) segment writes the final output;
+//   only segments cut by a range boundary leave partial (max, sum, acc)
+//   triples for the merge kernel (log-sum-exp rescale).
+// * A wavefront serves all G query heads of a kv head from one read of K/V.
+//   q.k^T runs on the matrix cores: v_mfma_f32_16x16x32_bf16 with the 16 tokens
+//   of a block as rows and the G heads (zero-padded to 16) as columns; fp32
+//   queries are split into hi + lo bf16 parts (two MFMAs) so the products stay
+//   fp32-accurate.  P.V stays on the VALU in fp32.
+// * K and V rows are read 16 bytes per lane, HD/8 lanes per 128/256-byte row
+//   (fully coalesced).  K goes through a per-wave LDS tile, stored with its
+//   16-byte chunks XOR-swizzled by row, and comes back in the MFMA operand
+//   layout (one 16-byte chunk of one token per lane) without bank conflicts.
+//   The next block is prefetched into registers while the current one is
+//   computed.  K/V are read once per step, so the loads carry the non-temporal
+//   hint (streamed through L2 without displacing reused lines), which on
+//   MI355X raises the achievable rate of this pattern by ~10 %.
+// * Online softmax in the exp2 domain with lazy rescaling: the running max is
+//   only raised (and acc, sum rescaled) when a block's max exceeds it by more
+//   than 2^8, which after the first blocks is rare; the result is exact since
+//   numerator and denominator share the same reference max.
 #include "skv_common.h"
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
+#include <mutex>
+#include <string>
+#include <unordered_map>
 
 namespace skv {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 struct DecodeParams {
     const void* q;
@@ -38,19 +57,19 @@ struct DecodeParams {
     int B, Hq, Hkv, HD, bs;
     float qscale;          // softmax scale * log2(e)
     float* out;            // [B][Hq][HD]
-    int32_t* plan;         // [B + 2]: part_base[0..B], blocks per unit at [B + 1]
-    float* ws_ml;          // [parts_cap][Hq][2]  (running max in log2 units, sum)
-    float* ws_acc;         // [parts_cap][Hq][HD] (unnormalised P.V)
-    int target_parts;
-    int min_bpu;
+    int Hseg;              // segments per sequence: Hkv (MFMA kernel) or Hq (generic kernel)
+    int NH;                // query heads per segment: G or 1
+    int ranges;            // block ranges; the grid is ranges * Hseg wavefronts
+    int min_per;           // minimum blocks per range
+    int32_t* plan;         // [3 + B + 1]: total, per, used ranges, P[0..B]
+    float* ws_ml;          // [2 * ranges * Hseg][NH][2]  (reference max in log2 units, sum)
+    float* ws_acc;         // [2 * ranges * Hseg][NH][HD] (unnormalised P.V)
 };
 
-constexpr int kTargetUnits = 16384;  // ~64 wavefronts of work per CU
 constexpr int kMaxHeadDim = 512;
-
-__host__ __device__ inline int parts_target(int Hkv) {
-    return std::max(1, kTargetUnits / Hkv);
-}
+constexpr int kMaxWaves = 8192;      // bound on persistent wavefronts (workspace sizing)
+constexpr int kMaxBatchPerLaunch = 4096;  // sequences per launch (LDS prefix table)
+constexpr float kLazyRescale = 8.0f;
 
 __device__ __forceinline__ int seq_len(const DecodeParams& p, int b) {
     return p.lens != nullptr ? p.lens[b] : p.single_len;
@@ -63,403 +82,567 @@ __device__ __forceinline__ int seq_blocks(const DecodeParams& p, int b) {
 }
 
 // ---------------------------------------------------------------------------
-// Planner: one workgroup.  blocks per unit = max(min_bpu, ceil(sum_b nb_b /
-// target_parts)); parts_b = ceil(nb_b / bpu); part_base = exclusive scan.
-// Since parts_b <= nb_b/bpu + 1, the total is at most target_parts + B.
+// Work split ("stream-K" over blocks).  Every wavefront builds P[b] = blocks of
+// the sequences before b in LDS (a wave scan over the batch), so no planner
+// launch is needed.  The flattened (sequence, block) space [0, P[B]) is cut
+// into `used` ranges of `per` blocks; wavefront w serves range w / Hseg for
+// head group w % Hseg, so the Hseg wavefronts reading the head slices of the
+// same 16-token blocks run side by side.  A segment = (sequence, head group):
+// it is final when one range holds all of it; otherwise each range touching it
+// leaves a partial in slot (2 * range + tail) * Hseg + group, tail = 1 when
+// the segment starts strictly inside the range (then it is the range's last
+// segment), 0 otherwise (the range's first segment).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void decode_plan_kernel(DecodeParams p) {
-    __shared__ long long s_red[1024];
-    __shared__ int s_scan[1024];
-    const int t = threadIdx.x, nt = blockDim.x;
-    const int per = cdiv(p.B, nt);
-    const int b0 = std::min(t * per, p.B), b1 = std::min(b0 + per, p.B);
+struct WorkSplit {
+    int total, per, used;
+};
 
-    long long mine = 0;
-    for (int b = b0; b < b1; ++b) mine += seq_blocks(p, b);
-    s_red[t] = mine;
+__device__ WorkSplit build_split(const DecodeParams& p, int* P_s) {
+    const int lane = threadIdx.x;
+    int carry = 0;
+    for (int b0 = 0; b0 < p.B; b0 += 64) {
+        const int b = b0 + lane;
+        int v = b < p.B ? seq_blocks(p, b) : 0;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(v, o, 64);
+            if (lane >= o) v += u;
+        }
+        if (b < p.B) P_s[b + 1] = carry + v;
+        carry += __shfl(v, 63, 64);
+    }
+    if (lane == 0) P_s[0] = 0;
     __syncthreads();
-    for (int o = nt / 2; o > 0; o >>= 1) {
-        if (t < o) s_red[t] += s_red[t + o];
-        __syncthreads();
+    WorkSplit ws;
+    ws.total = carry;
+    ws.per = std::max(p.min_per, carry > 0 ? cdiv(carry, p.ranges) : 1);
+    ws.used = carry > 0 ? cdiv(carry, ws.per) : 0;
+    if (blockIdx.x == 0) {  // publish for the merge kernel
+        for (int i = lane; i <= p.B; i += 64) p.plan[3 + i] = P_s[i];
+        if (lane == 0) {
+            p.plan[0] = ws.total;
+            p.plan[1] = ws.per;
+            p.plan[2] = ws.used;
+        }
     }
-    const long long total_blocks = s_red[0];
-    const int bpu = static_cast<int>(
-        std::max<long long>(p.min_bpu, cdiv<long long>(total_blocks, p.target_parts)));
-
-    int parts = 0;
-    for (int b = b0; b < b1; ++b) parts += cdiv(seq_blocks(p, b), bpu);
-    s_scan[t] = parts;
-    __syncthreads();
-    for (int o = 1; o < nt; o <<= 1) {  // inclusive Hillis-Steele scan
-        const int add = t >= o ? s_scan[t - o] : 0;
-        __syncthreads();
-        s_scan[t] += add;
-        __syncthreads();
-    }
-    int base = s_scan[t] - parts;
-    for (int b = b0; b < b1; ++b) {
-        p.plan[b] = base;
-        base += cdiv(seq_blocks(p, b), bpu);
-    }
-    if (t == nt - 1) {
-        p.plan[p.B] = s_scan[t];
-        p.plan[p.B + 1] = bpu;
-    }
+    return ws;
 }
 
-// Locate the sequence owning global partition pg: part_base[b] <= pg < part_base[b+1].
-__device__ __forceinline__ int find_seq(const int32_t* plan, int B, int pg) {
+// Sequence owning flattened block `pos`: P[b] <= pos < P[b+1].
+__device__ __forceinline__ int find_seq(const int* P, int B, int pos) {
     int lo = 0, hi = B;
     while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
-        if (plan[mid] <= pg) lo = mid; else hi = mid;
+        if (P[mid] <= pos) lo = mid; else hi = mid;
     }
     return lo;
 }
 
+__device__ __forceinline__ int64_t partial_row(int range, bool tail, int Hseg, int group) {
+    return (2 * static_cast<int64_t>(range) + (tail ? 1 : 0)) * Hseg + group;
+}
+
 // ---------------------------------------------------------------------------
-// Fast path: block_size 16, head_dim 64 or 128, G in {1,2,4,8}.
-// Lane layout: LPR = HD/8 lanes per K/V row (8 elements = 16 bytes each),
-// RPI = 64/LPR rows per load instruction, TPL = 16/RPI rows per lane per block.
-// Lane (r, c) handles rows r, r+RPI, ... of every block, elements [8c, 8c+8).
+// MFMA path: block_size 16, head_dim 64 or 128, G in {1, 2, 4, 8, 16}.
+// Coalesced (V) layout: lane (r, c) = (lane / CH, lane % CH) holds rows
+//   i*RPI + r (i < TPL) of a block, elements [8c, 8c + 8).
+// MFMA layout: lane (t, j) = (lane % 16, lane / 16); the K operand of MFMA cc
+//   is row t, chunk 4*cc + j, read from the LDS tile; the output holds
+//   S[token 4j + i][head t].
+// LDS tile: row R, chunk c stored at R*CH + (c ^ swz(R)), swz(R) = R for
+//   CH = 16 and (R >> 1) & 7 for CH = 8, so the 16 lanes reading one chunk
+//   column of 16 rows hit 16 distinct bank groups.
 // ---------------------------------------------------------------------------
 template <int HD, int G, bool QF32>
-__global__ __launch_bounds__(64) void decode_fast_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64, (G <= 4 ? 3 : G == 8 ? 2 : 1)) void decode_mfma_kernel(DecodeParams p) {
     constexpr int BS = 16;
-    constexpr int LPR = HD / 8;
-    constexpr int RPI = 64 / LPR;
-    constexpr int TPL = BS / RPI;
-    static_assert(LPR * RPI == 64 && RPI * TPL == BS, "lane layout");
+    constexpr int CH = HD / 8;      // 16-byte chunks per row
+    constexpr int RPI = 64 / CH;    // rows per coalesced load instruction
+    constexpr int TPL = BS / RPI;   // rows per lane per block (coalesced layout)
+    constexpr int NMF = HD / 32;    // MFMAs per block for q.k
+    constexpr int QP = QF32 ? 2 : 1;
+    static_assert(CH * RPI == 64 && RPI * TPL == BS && NMF * 4 == CH, "lane layout");
+    static_assert(G >= 1 && G <= 16, "group size");
+
+    extern __shared__ int P_s[];    // [B + 1] block prefix
+    __shared__ u32x4_t k_s[BS * CH];  // one block of K for this kv head, swizzled
+    __shared__ float p_s[BS * 16];  // probabilities [token][head]
+    __shared__ float h_s[2][16];    // per-head broadcast: rescale factor / (sum, max)
 
     const int lane = threadIdx.x;
-    const int r = lane / LPR, c = lane % LPR;
+    const int r = lane / CH, c = lane % CH;
+    const int t = lane & 15, j = lane >> 4;
+    auto swz = [](int row) { return CH == 16 ? row : ((row >> 1) & 7); };
     const int Hkv = p.Hkv;
-    const int total_parts = p.plan[p.B];
-    const int u = blockIdx.x;
-    if (u >= total_parts * Hkv) return;
-    const int pg = u / Hkv;
-    const int kvh = u - pg * Hkv;
-    const int b = find_seq(p.plan, p.B, pg);
-    const int part = pg - p.plan[b];
-    const int nparts = p.plan[b + 1] - p.plan[b];
-    const int bpu = p.plan[p.B + 1];
-    const int L = seq_len(p, b);
-    const int nb = std::min(cdiv(L, BS), p.max_blocks);
-    const int Leff = std::min(L, nb * BS);
-    const int blk0 = part * bpu;
-    const int blk1 = std::min(blk0 + bpu, nb);
-    const int32_t* table = p.tables + static_cast<int64_t>(b) * p.max_blocks;
+    const int w = blockIdx.x;
+    const int kvh = w % Hkv;
+    const int range = w / Hkv;
+
+    const WorkSplit split = build_split(p, P_s);
+    if (range >= split.used) return;
+    const int per = split.per;
+    const int64_t row_stride = static_cast<int64_t>(Hkv) * HD;
+    const int range_lo = range * per;
+    const int range_hi = range_lo + per;
+    int pos = range_lo;
+    const int end = std::min(range_hi, split.total);
+    int b = find_seq(P_s, p.B, pos);
     const int h0 = kvh * G;
 
-    float qf[G][8];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const int64_t qoff = (static_cast<int64_t>(b) * p.Hq + h0 + g) * HD + 8 * c;
-        if constexpr (QF32) {
-            const float4* qp = reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + qoff);
-            const float4 a0 = qp[0], a1 = qp[1];
-            qf[g][0] = a0.x; qf[g][1] = a0.y; qf[g][2] = a0.z; qf[g][3] = a0.w;
-            qf[g][4] = a1.x; qf[g][5] = a1.y; qf[g][6] = a1.z; qf[g][7] = a1.w;
-        } else {
-            const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.q) + qoff);
-            unpack8(w, qf[g]);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) qf[g][j] *= p.qscale;
-    }
+    while (true) {
+        const int seg_lo = P_s[b], seg_hi = P_s[b + 1];
+        const int nb = seg_hi - seg_lo;
+        const int k0 = pos - seg_lo;
+        const int stop = std::min(end, seg_hi);
+        const int kb1 = stop - seg_lo;
+        const int L = seq_len(p, b);
+        const int Leff = std::min(L, nb * BS);
+        const int32_t* table = p.tables + static_cast<int64_t>(b) * p.max_blocks;
 
-    float m[G], l[G], acc[G][8];
+        // q operand(s): head h0 + t, chunk 4*cc + j; zero for padded heads.
+        bf16x8_t qop[QP][NMF];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -INFINITY;
-        l[g] = 0.0f;
+        for (int cc = 0; cc < NMF; ++cc) {
+            u32x4_t hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
+            if (t < G) {
+                const int64_t qoff =
+                    (static_cast<int64_t>(b) * p.Hq + h0 + t) * HD + (4 * cc + j) * 8;
+                if constexpr (QF32) {
+                    const float4* qp = reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + qoff);
+                    const float4 a0 = qp[0], a1 = qp[1];
+                    const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                    uint32_t hb[8], lb[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
-    }
-
-    const int64_t row_stride = static_cast<int64_t>(Hkv) * HD;
-    const int64_t lane_off = static_cast<int64_t>(kvh) * HD + 8 * c + static_cast<int64_t>(r) * row_stride;
-
-    for (int blk = blk0; blk < blk1; ++blk) {
-        const int64_t pb = table[blk];
-        if (pb < 0 || pb >= p.total_blocks) continue;
-        const uint16_t* kb = p.k + pb * BS * row_stride + lane_off;
-        const uint16_t* vb = p.v + pb * BS * row_stride + lane_off;
-        uint4 kw[TPL], vw[TPL];
-#pragma unroll
-        for (int i = 0; i < TPL; ++i) {
-            kw[i] = *reinterpret_cast<const uint4*>(kb + static_cast<int64_t>(i) * RPI * row_stride);
-            vw[i] = *reinterpret_cast<const uint4*>(vb + static_cast<int64_t>(i) * RPI * row_stride);
-        }
-        float s[TPL][G];
-#pragma unroll
-        for (int i = 0; i < TPL; ++i) {
-            float kf[8];
-            unpack8(kw[i], kf);
-            const bool valid = blk * BS + i * RPI + r < Leff;
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float d = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) d = fmaf(qf[g][j], kf[j], d);
-                d = group_sum<LPR>(d);
-                s[i][g] = valid ? d : -INFINITY;
+                    for (int e = 0; e < 8; ++e) {
+                        hb[e] = f32_to_bf16_bits(x[e]);
+                        lb[e] = f32_to_bf16_bits(x[e] - __uint_as_float(hb[e] << 16));
+                    }
+                    hi = u32x4_t{hb[0] | hb[1] << 16, hb[2] | hb[3] << 16, hb[4] | hb[5] << 16, hb[6] | hb[7] << 16};
+                    lo = u32x4_t{lb[0] | lb[1] << 16, lb[2] | lb[3] << 16, lb[4] | lb[5] << 16, lb[6] | lb[7] << 16};
+                } else {
+                    hi = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.q) + qoff);
+                }
             }
+            qop[0][cc] = __builtin_bit_cast(bf16x8_t, hi);
+            if constexpr (QF32) qop[QP - 1][cc] = __builtin_bit_cast(bf16x8_t, lo);
         }
-        float vf[TPL][8];
+
+        float m = -INFINITY;   // reference max of head t (log2 units), equal across j
+        float lpart = 0.0f;    // sum of this lane's probabilities for head t
+        float acc[G][8];
 #pragma unroll
-        for (int i = 0; i < TPL; ++i) unpack8(vw[i], vf[i]);
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float mb = s[0][g];
-#pragma unroll
-            for (int i = 1; i < TPL; ++i) mb = fmaxf(mb, s[i][g]);
-            const float mn = fmaxf(m[g], mb);
-            const float ms = mn == -INFINITY ? 0.0f : mn;
-            const float alpha = fast_exp2(m[g] - ms);
-            m[g] = mn;
-            l[g] *= alpha;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[g][j] *= alpha;
+            for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+
+        const int64_t lane_off = static_cast<int64_t>(r) * row_stride + static_cast<int64_t>(kvh) * HD + c * 8;
+
+        auto issue = [&](int kb, u32x4_t (&kk)[TPL], u32x4_t (&vv)[TPL]) -> bool {
+            const int64_t pb = table[kb];
+            if (pb < 0 || pb >= p.total_blocks) return false;
+            const int64_t base = pb * BS * row_stride + lane_off;
 #pragma unroll
             for (int i = 0; i < TPL; ++i) {
-                const float pp = fast_exp2(s[i][g] - ms);
-                l[g] += pp;
+                const int64_t off = base + static_cast<int64_t>(i) * RPI * row_stride;
+                kk[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p.k + off));
+                vv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p.v + off));
+            }
+            return true;
+        };
+
+        u32x4_t kcur[TPL], vcur[TPL];
+        bool ok = issue(k0, kcur, vcur);
+        for (int kb = k0; kb < kb1; ++kb) {
+            u32x4_t knext[TPL], vnext[TPL];
+            bool ok_next = false;
+            if (kb + 1 < kb1) ok_next = issue(kb + 1, knext, vnext);
+            if (ok) {
+                // ---- K through the LDS tile into the MFMA operand layout
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(pp, vf[i][j], acc[g][j]);
+                for (int i = 0; i < TPL; ++i) {
+                    const int row = i * RPI + r;
+                    k_s[row * CH + (c ^ swz(row))] = kcur[i];
+                }
+                __syncthreads();
+                // ---- scores S[token 4j+i][head t] on the matrix cores
+                f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int cc = 0; cc < NMF; ++cc) {
+                    const bf16x8_t a = __builtin_bit_cast(bf16x8_t, k_s[t * CH + ((4 * cc + j) ^ swz(t))]);
+#pragma unroll
+                    for (int qp = 0; qp < QP; ++qp)
+                        sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qop[qp][cc], sacc, 0, 0, 0);
+                }
+                const int tok = kb * BS + 4 * j;
+                float s[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[i] = tok + i < Leff ? sacc[i] * p.qscale : -INFINITY;
+                float mb = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+                mb = fmaxf(mb, shfl_xor_f(mb, 16));
+                mb = fmaxf(mb, shfl_xor_f(mb, 32));
+
+                // ---- lazy rescale (wave-uniform branch)
+                const bool need = mb > m + kLazyRescale;
+                if (__any(need)) {
+                    const float mn = need ? mb : m;
+                    // Before the first block m = -inf and acc, sum are 0: factor 0.
+                    const float alpha = m == -INFINITY ? 0.0f : fast_exp2(m - mn);
+                    m = mn;
+                    lpart *= alpha;
+                    if (j == 0) h_s[0][t] = alpha;
+                    __syncthreads();
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        const float a = h_s[0][g];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc[g][e] *= a;
+                    }
+                }
+                const float ms = m == -INFINITY ? 0.0f : m;
+                float pr[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(s[i] - ms);
+                lpart += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+                if (t < G) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) p_s[(4 * j + i) * 16 + t] = pr[i];
+                }
+                __syncthreads();
+
+                // ---- P.V on the VALU (coalesced V layout)
+                const bool tail = kb * BS + BS > Leff;
+#pragma unroll
+                for (int i = 0; i < TPL; ++i) {
+                    const int row = i * RPI + r;
+                    u32x4_t vw = vcur[i];
+                    if (tail && kb * BS + row >= Leff) vw = u32x4_t{0u, 0u, 0u, 0u};
+                    float vf[8];
+                    vf[0] = bf16_lo(vw.x); vf[1] = bf16_hi(vw.x);
+                    vf[2] = bf16_lo(vw.y); vf[3] = bf16_hi(vw.y);
+                    vf[4] = bf16_lo(vw.z); vf[5] = bf16_hi(vw.z);
+                    vf[6] = bf16_lo(vw.w); vf[7] = bf16_hi(vw.w);
+                    float pv[G];
+#pragma unroll
+                    for (int g = 0; g < G; ++g) pv[g] = p_s[row * 16 + g];
+#pragma unroll
+                    for (int g = 0; g < G; ++g)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pv[g], vf[e], acc[g][e]);
+                }
+                __syncthreads();
+            }
+#pragma unroll
+            for (int i = 0; i < TPL; ++i) {
+                kcur[i] = knext[i];
+                vcur[i] = vnext[i];
+            }
+            ok = ok_next;
+        }
+
+        // ---- finalise the segment: combine row groups, broadcast (sum, max)
+#pragma unroll
+        for (int off = CH; off < 64; off <<= 1)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] += shfl_xor_f(acc[g][e], off);
+        float ltot = lpart + shfl_xor_f(lpart, 16);
+        ltot += shfl_xor_f(ltot, 32);
+        if (j == 0) {
+            h_s[0][t] = ltot;
+            h_s[1][t] = m;
+        }
+        __syncthreads();
+        const bool final_out = seg_lo >= range_lo && seg_hi <= range_hi;
+        const int64_t prow = partial_row(range, seg_lo > range_lo, Hkv, kvh);
+        if (r == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float lsum = h_s[0][g];
+                if (final_out) {
+                    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+                    float4* o = reinterpret_cast<float4*>(
+                        p.out + (static_cast<int64_t>(b) * p.Hq + h0 + g) * HD + 8 * c);
+                    o[0] = make_float4(acc[g][0] * inv, acc[g][1] * inv, acc[g][2] * inv, acc[g][3] * inv);
+                    o[1] = make_float4(acc[g][4] * inv, acc[g][5] * inv, acc[g][6] * inv, acc[g][7] * inv);
+                } else {
+                    const int64_t row = prow * G + g;
+                    float4* o = reinterpret_cast<float4*>(p.ws_acc + row * HD + 8 * c);
+                    o[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+                    o[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+                    if (c == 0) {
+                        p.ws_ml[row * 2 + 0] = h_s[1][g];
+                        p.ws_ml[row * 2 + 1] = lsum;
+                    }
+                }
             }
         }
-    }
+        __syncthreads();
 
-    // Merge the RPI row groups (lanes c, c+LPR, ...) into every lane.
-#pragma unroll
-    for (int off = LPR; off < 64; off <<= 1) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float mo = shfl_xor_f(m[g], off);
-            const float lo = shfl_xor_f(l[g], off);
-            const float mn = fmaxf(m[g], mo);
-            const float ms = mn == -INFINITY ? 0.0f : mn;
-            const float sa = fast_exp2(m[g] - ms);
-            const float sb = fast_exp2(mo - ms);
-            l[g] = l[g] * sa + lo * sb;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[g][j] = acc[g][j] * sa + shfl_xor_f(acc[g][j], off) * sb;
-            m[g] = mn;
-        }
-    }
-
-    if (r != 0) return;
-    if (nparts == 1) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float inv = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
-            float4* o = reinterpret_cast<float4*>(
-                p.out + (static_cast<int64_t>(b) * p.Hq + h0 + g) * HD + 8 * c);
-            o[0] = make_float4(acc[g][0] * inv, acc[g][1] * inv, acc[g][2] * inv, acc[g][3] * inv);
-            o[1] = make_float4(acc[g][4] * inv, acc[g][5] * inv, acc[g][6] * inv, acc[g][7] * inv);
-        }
-    } else {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const int64_t row = static_cast<int64_t>(pg) * p.Hq + h0 + g;
-            float4* o = reinterpret_cast<float4*>(p.ws_acc + row * HD + 8 * c);
-            o[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-            o[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
-            if (c == 0) {
-                p.ws_ml[row * 2 + 0] = m[g];
-                p.ws_ml[row * 2 + 1] = l[g];
-            }
-        }
+        pos = stop;
+        if (pos >= end) break;
+        do {
+            ++b;
+        } while (P_s[b + 1] == P_s[b]);
     }
 }
 
 // ---------------------------------------------------------------------------
-// Generic path: any block size, head_dim <= 512, any group size.  One
-// wavefront per (partition, query head): lanes own tokens for q.k (q staged in
-// LDS) and head dimensions for P.V.  Correct for every shape the reference
-// accepts; the fast path covers the benchmark geometries.
+// Generic path: any block size, head_dim <= 512, any group size.  Segments are
+// (sequence, query head); lanes own tokens for q.k (q staged in LDS) and head
+// dimensions for P.V.  Correct for every shape the reference accepts; the
+// MFMA path covers the benchmark geometries.
 // ---------------------------------------------------------------------------
 template <bool QF32>
 __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
     constexpr int DPL = kMaxHeadDim / 64;
+    extern __shared__ int P_s[];    // [B + 1] block prefix
     __shared__ float q_s[kMaxHeadDim];
     __shared__ float p_s[64];
     __shared__ int64_t row_s[64];
 
     const int lane = threadIdx.x;
-    const int total_parts = p.plan[p.B];
-    const int u = blockIdx.x;
-    if (u >= total_parts * p.Hq) return;
-    const int pg = u / p.Hq;
-    const int h = u - pg * p.Hq;
-    const int b = find_seq(p.plan, p.B, pg);
-    const int part = pg - p.plan[b];
-    const int nparts = p.plan[b + 1] - p.plan[b];
-    const int bpu = p.plan[p.B + 1];
-    const int L = seq_len(p, b);
-    const int nb = std::min(cdiv(L, p.bs), p.max_blocks);
-    const int Leff = std::min(L, nb * p.bs);
-    const int tok0 = part * bpu * p.bs;
-    const int tok1 = std::min((part * bpu + bpu) * p.bs, Leff);
-    const int kvh = h / (p.Hq / p.Hkv);
-    const int HD = p.HD;
-    const int32_t* table = p.tables + static_cast<int64_t>(b) * p.max_blocks;
-
-    const int64_t qoff = (static_cast<int64_t>(b) * p.Hq + h) * HD;
-    for (int d = lane; d < HD; d += 64) {
-        const float qv = QF32 ? static_cast<const float*>(p.q)[qoff + d]
-                              : bf16_to_f32(static_cast<const uint16_t*>(p.q)[qoff + d]);
-        q_s[d] = qv * p.qscale;
-    }
-    __syncthreads();
-
-    float m = -INFINITY, l = 0.0f;
-    float acc[DPL];
-#pragma unroll
-    for (int k = 0; k < DPL; ++k) acc[k] = 0.0f;
+    const int Hq = p.Hq, HD = p.HD, bs = p.bs;
+    const int w = blockIdx.x;
+    const int h = w % Hq;
+    const int range = w / Hq;
+    const WorkSplit split = build_split(p, P_s);
+    if (range >= split.used) return;
+    const int per = split.per;
     const int64_t row_elems = static_cast<int64_t>(p.Hkv) * HD;
+    const int range_lo = range * per;
+    const int range_hi = range_lo + per;
+    int pos = range_lo;
+    const int end = std::min(range_hi, split.total);
+    int b = find_seq(P_s, p.B, pos);
+    const int kvh = h / (Hq / p.Hkv);
 
-    for (int t0 = tok0; t0 < tok1; t0 += 64) {
-        const int t = t0 + lane;
-        float score = -INFINITY;
-        int64_t roff = -1;
-        if (t < tok1) {
-            const int64_t pb = table[t / p.bs];
-            if (pb >= 0 && pb < p.total_blocks) {
-                roff = (pb * p.bs + t % p.bs) * row_elems + static_cast<int64_t>(kvh) * HD;
-                const uint16_t* kr = p.k + roff;
-                float dot = 0.0f;
-                for (int d = 0; d < HD; ++d) dot = fmaf(q_s[d], bf16_to_f32(kr[d]), dot);
-                score = dot;
-            }
+    while (true) {
+        const int seg_lo = P_s[b], seg_hi = P_s[b + 1];
+        const int nb = seg_hi - seg_lo;
+        const int k0 = pos - seg_lo;
+        const int stop = std::min(end, seg_hi);
+        const int kb1 = stop - seg_lo;
+        const int L = seq_len(p, b);
+        const int Leff = std::min(L, nb * bs);
+        const int tok0 = k0 * bs;
+        const int tok1 = std::min(kb1 * bs, Leff);
+        const int32_t* table = p.tables + static_cast<int64_t>(b) * p.max_blocks;
+
+        const int64_t qoff = (static_cast<int64_t>(b) * Hq + h) * HD;
+        for (int d = lane; d < HD; d += 64) {
+            const float qv = QF32 ? static_cast<const float*>(p.q)[qoff + d]
+                                  : bf16_to_f32(static_cast<const uint16_t*>(p.q)[qoff + d]);
+            q_s[d] = qv * p.qscale;
         }
-        const float mn = fmaxf(m, wave_max(score));
-        const float ms = mn == -INFINITY ? 0.0f : mn;
-        const float alpha = fast_exp2(m - ms);
-        const float pp = fast_exp2(score - ms);
-        l = l * alpha + wave_sum(pp);
-        m = mn;
-#pragma unroll
-        for (int k = 0; k < DPL; ++k) acc[k] *= alpha;
-        p_s[lane] = pp;
-        row_s[lane] = roff;
         __syncthreads();
-        const int n = std::min(64, tok1 - t0);
-        for (int j = 0; j < n; ++j) {
-            const int64_t vr = row_s[j];
-            if (vr < 0) continue;
-            const float pj = p_s[j];
-            const uint16_t* vrow = p.v + vr;
+
+        float m = -INFINITY, l = 0.0f;
+        float acc[DPL];
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) acc[k] = 0.0f;
+
+        for (int t0 = tok0; t0 < tok1; t0 += 64) {
+            const int tk = t0 + lane;
+            float score = -INFINITY;
+            int64_t roff = -1;
+            if (tk < tok1) {
+                const int64_t pb = table[tk / bs];
+                if (pb >= 0 && pb < p.total_blocks) {
+                    roff = (pb * bs + tk % bs) * row_elems + static_cast<int64_t>(kvh) * HD;
+                    const uint16_t* kr = p.k + roff;
+                    float dot = 0.0f;
+                    for (int d = 0; d < HD; ++d) dot = fmaf(q_s[d], bf16_to_f32(kr[d]), dot);
+                    score = dot;
+                }
+            }
+            const float mn = fmaxf(m, wave_max(score));
+            const float ms = mn == -INFINITY ? 0.0f : mn;
+            const float alpha = fast_exp2(m - ms);
+            const float pp = fast_exp2(score - ms);
+            l = l * alpha + wave_sum(pp);
+            m = mn;
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) acc[k] *= alpha;
+            p_s[lane] = pp;
+            row_s[lane] = roff;
+            __syncthreads();
+            const int n = std::min(64, tok1 - t0);
+            for (int jj = 0; jj < n; ++jj) {
+                const int64_t vr = row_s[jj];
+                if (vr < 0) continue;
+                const float pj = p_s[jj];
+                const uint16_t* vrow = p.v + vr;
+#pragma unroll
+                for (int k = 0; k < DPL; ++k) {
+                    const int d = lane + 64 * k;
+                    if (d < HD) acc[k] = fmaf(pj, bf16_to_f32(vrow[d]), acc[k]);
+                }
+            }
+            __syncthreads();
+        }
+
+        const bool final_out = seg_lo >= range_lo && seg_hi <= range_hi;
+        if (final_out) {
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            float* o = p.out + (static_cast<int64_t>(b) * Hq + h) * HD;
 #pragma unroll
             for (int k = 0; k < DPL; ++k) {
                 const int d = lane + 64 * k;
-                if (d < HD) acc[k] = fmaf(pj, bf16_to_f32(vrow[d]), acc[k]);
+                if (d < HD) o[d] = acc[k] * inv;
+            }
+        } else {
+            const int64_t row = partial_row(range, seg_lo > range_lo, Hq, h);
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) {
+                const int d = lane + 64 * k;
+                if (d < HD) p.ws_acc[row * HD + d] = acc[k];
+            }
+            if (lane == 0) {
+                p.ws_ml[row * 2 + 0] = m;
+                p.ws_ml[row * 2 + 1] = l;
             }
         }
         __syncthreads();
-    }
 
-    if (nparts == 1) {
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        float* o = p.out + (static_cast<int64_t>(b) * p.Hq + h) * HD;
-#pragma unroll
-        for (int k = 0; k < DPL; ++k) {
-            const int d = lane + 64 * k;
-            if (d < HD) o[d] = acc[k] * inv;
-        }
-    } else {
-        const int64_t row = static_cast<int64_t>(pg) * p.Hq + h;
-#pragma unroll
-        for (int k = 0; k < DPL; ++k) {
-            const int d = lane + 64 * k;
-            if (d < HD) p.ws_acc[row * HD + d] = acc[k];
-        }
-        if (lane == 0) {
-            p.ws_ml[row * 2 + 0] = m;
-            p.ws_ml[row * 2 + 1] = l;
-        }
+        pos = stop;
+        if (pos >= end) break;
+        do {
+            ++b;
+        } while (P_s[b + 1] == P_s[b]);
     }
 }
 
 // ---------------------------------------------------------------------------
-// Merge: one workgroup per (sequence, query head).  Sequences with a single
-// partition were finalised by the attention kernel; sequences without context
-// get zeros.  out = sum_p acc_p 2^(m_p - M) / sum_p l_p 2^(m_p - M).
+// Merge: one 256-thread workgroup per segment (sequence, head group).
+// Segments held by a single range were finalised by the attention kernel;
+// sequences without context get zeros.  For each of the NH heads:
+//   out = sum_r acc_r 2^(m_r - M) / sum_r l_r 2^(m_r - M)
+// over the ranges r that touch the segment.  NH divides 256, so thread t only
+// ever sees head t % NH in the (partial, head) loops; the per-thread results
+// are reduced through LDS.  The P.V rows of all partials are loaded
+// independently (no dependent chain), four at a time.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
-    constexpr int kChunk = 2048;
-    __shared__ float w_s[kChunk];
-    __shared__ float red[256];
+    constexpr int kMaxN = 8;   // partials per segment kept in registers (fast path)
+    constexpr int kMaxE = 8;   // output elements per thread (NH * HD <= 2048)
+    __shared__ float red[256], w_s[256];
+    __shared__ float M_s[16], inv_s[16];
     const int t = threadIdx.x;
-    const int b = blockIdx.x / p.Hq;
-    const int h = blockIdx.x - b * p.Hq;
-    const int base = p.plan[b];
-    const int nparts = p.plan[b + 1] - base;
-    if (nparts == 1) return;
-    const int HD = p.HD;
-    float* o = p.out + (static_cast<int64_t>(b) * p.Hq + h) * HD;
-    if (nparts == 0) {
-        for (int d = t; d < HD; d += 256) o[d] = 0.0f;
+    const int s = blockIdx.x;
+    const int b = s / p.Hseg;
+    const int grp = s - b * p.Hseg;
+    const int per = p.plan[1];
+    const int32_t* P = p.plan + 3;
+    const int lo = P[b], hi = P[b + 1];
+    const int HD = p.HD, NH = p.NH;
+    float* out0 = p.out + (static_cast<int64_t>(b) * p.Hq + grp * NH) * HD;
+    if (lo == hi) {
+        for (int e = t; e < NH * HD; e += 256) out0[e] = 0.0f;
         return;
     }
-    auto ml = [&](int i, int which) {
-        return p.ws_ml[(static_cast<int64_t>(base + i) * p.Hq + h) * 2 + which];
+    const int r0 = lo / per, r1 = (hi - 1) / per;
+    if (r0 == r1) return;
+    const int n = r1 - r0 + 1;
+    const bool first_tail = lo > r0 * per;
+    auto row_of = [&](int i, int g) -> int64_t {
+        return partial_row(r0 + i, i == 0 && first_tail, p.Hseg, grp) * NH + g;
     };
+    const int g_t = t % NH;
+    const int elems = NH * HD;
 
-    float mx = -INFINITY;
-    for (int i = t; i < nparts; i += 256) mx = fmaxf(mx, ml(i, 0));
-    red[t] = mx;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (t < s) red[t] = fmaxf(red[t], red[t + s]);
+    if (n <= kMaxN && n * NH <= 256 && elems <= 256 * kMaxE) {
+        // Fast path: every load is issued before any reduction.
+        float m_t = -INFINITY, l_t = 0.0f;
+        if (t < n * NH) {
+            const int64_t row = row_of(t / NH, g_t);
+            m_t = p.ws_ml[row * 2];
+            l_t = p.ws_ml[row * 2 + 1];
+        }
+        float a[kMaxE][kMaxN];
+#pragma unroll
+        for (int k = 0; k < kMaxE; ++k) {
+            const int e = t + 256 * k;
+            const int g = e / HD, d = e - (e / HD) * HD;
+#pragma unroll
+            for (int i = 0; i < kMaxN; ++i)
+                a[k][i] = (e < elems && i < n) ? p.ws_acc[row_of(i, g) * HD + d] : 0.0f;
+        }
+        red[t] = m_t;
         __syncthreads();
-    }
-    const float M = red[0];
-    const float Ms = M == -INFINITY ? 0.0f : M;
-    __syncthreads();
-
-    // Threads split into S slices of HD dims; slice s handles parts i = s mod S.
-    const int S = HD <= 256 ? 256 / HD : 1;
-    const int slice = t / std::min(HD, 256);
-    const int d0 = t % std::min(HD, 256);
-    float acc[2] = {0.0f, 0.0f};  // HD <= 512: at most two dims per thread
-    float lsum = 0.0f;
-    for (int c0 = 0; c0 < nparts; c0 += kChunk) {
-        const int n = std::min(kChunk, nparts - c0);
-        for (int i = t; i < n; i += 256) {
-            const float w = fast_exp2(ml(c0 + i, 0) - Ms);
-            w_s[i] = w;
-            lsum += ml(c0 + i, 1) * w;
+        if (t < NH) {
+            float m = -INFINITY;
+            for (int i = 0; i < n; ++i) m = fmaxf(m, red[i * NH + t]);
+            M_s[t] = m == -INFINITY ? 0.0f : m;
         }
         __syncthreads();
-        if (slice < S) {
-            for (int i = slice; i < n; i += S) {
-                const float w = w_s[i];
-                const float* a = p.ws_acc + (static_cast<int64_t>(base + c0 + i) * p.Hq + h) * HD;
-                acc[0] = fmaf(w, a[d0], acc[0]);
-                if (d0 + 256 < HD) acc[1] = fmaf(w, a[d0 + 256], acc[1]);
+        const float w = t < n * NH ? fast_exp2(m_t - M_s[g_t]) : 0.0f;
+        w_s[t] = w;
+        red[t] = l_t * w;
+        __syncthreads();
+        if (t < NH) {
+            float l = 0.0f;
+            for (int i = 0; i < n; ++i) l += red[i * NH + t];
+            inv_s[t] = l > 0.0f ? 1.0f / l : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kMaxE; ++k) {
+            const int e = t + 256 * k;
+            if (e < elems) {
+                const int g = e / HD;
+                float acc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < kMaxN; ++i)
+                    if (i < n) acc = fmaf(w_s[i * NH + g], a[k][i], acc);
+                out0[e] = acc * inv_s[g];
             }
         }
-        __syncthreads();
+        return;
+    }
+
+    // General path: any number of partials.
+    float mx = -INFINITY;
+    for (int idx = t; idx < n * NH; idx += 256) mx = fmaxf(mx, p.ws_ml[row_of(idx / NH, g_t) * 2]);
+    red[t] = mx;
+    __syncthreads();
+    if (t < NH) {
+        float m = -INFINITY;
+        for (int k = t; k < 256; k += NH) m = fmaxf(m, red[k]);
+        M_s[t] = m == -INFINITY ? 0.0f : m;
+    }
+    __syncthreads();
+    float lsum = 0.0f;
+    for (int idx = t; idx < n * NH; idx += 256) {
+        const int64_t row = row_of(idx / NH, g_t);
+        lsum += p.ws_ml[row * 2 + 1] * fast_exp2(p.ws_ml[row * 2] - M_s[g_t]);
     }
     red[t] = lsum;
     __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (t < s) red[t] += red[t + s];
-        __syncthreads();
+    if (t < NH) {
+        float l = 0.0f;
+        for (int k = t; k < 256; k += NH) l += red[k];
+        inv_s[t] = l > 0.0f ? 1.0f / l : 0.0f;
     }
-    const float total = red[0];
-    const float inv = total > 0.0f ? 1.0f / total : 0.0f;
     __syncthreads();
-    // Reduce the S slices of the first 256 dims through LDS.
-    red[t] = slice < S ? acc[0] : 0.0f;
-    __syncthreads();
-    if (slice == 0) {
-        float sum = red[t];
-        for (int s = 1; s < S; ++s) sum += red[t + s * HD];
-        if (d0 < HD) o[d0] = sum * inv;
-        if (d0 + 256 < HD) o[d0 + 256] = acc[1] * inv;
+
+    for (int e = t; e < elems; e += 256) {
+        const int g = e / HD, d = e - g * HD;
+        const float Mg = M_s[g];
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        int i = 0;
+        for (; i + 4 <= n; i += 4) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t row = row_of(i + u, g);
+                acc[u] = fmaf(fast_exp2(p.ws_ml[row * 2] - Mg), p.ws_acc[row * HD + d], acc[u]);
+            }
+        }
+        for (; i < n; ++i) {
+            const int64_t row = row_of(i, g);
+            acc[0] = fmaf(fast_exp2(p.ws_ml[row * 2] - Mg), p.ws_acc[row * HD + d], acc[0]);
+        }
+        out0[e] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) * inv_s[g];
     }
 }
 
@@ -468,42 +651,98 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
 // ---------------------------------------------------------------------------
 struct WorkspaceLayout {
     size_t plan_off, ml_off, acc_off, total;
-    int parts_cap;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Partial slots: 2 per (range, head group) with ranges * Hseg <= kMaxWaves,
+// each holding NH heads (NH = G for the MFMA kernel, 1 for the generic one).
 WorkspaceLayout workspace_layout(int B, int Hq, int Hkv, int HD) {
     WorkspaceLayout w{};
-    w.parts_cap = parts_target(Hkv) + B;
+    const int G = Hq / std::max(Hkv, 1);
+    const size_t head_slots = 2 * static_cast<size_t>(kMaxWaves) * std::max(G, 1);
+    const size_t plan_ints = 3 + static_cast<size_t>(std::min(B, kMaxBatchPerLaunch)) + 1;
     w.plan_off = 0;
-    w.ml_off = align256(sizeof(int32_t) * (static_cast<size_t>(B) + 2));
-    w.acc_off = w.ml_off + align256(sizeof(float) * 2 * static_cast<size_t>(w.parts_cap) * Hq);
-    w.total = w.acc_off + align256(sizeof(float) * static_cast<size_t>(w.parts_cap) * Hq * HD);
+    w.ml_off = align256(sizeof(int32_t) * plan_ints);
+    w.acc_off = w.ml_off + align256(sizeof(float) * 2 * head_slots);
+    w.total = w.acc_off + align256(sizeof(float) * head_slots * HD);
     return w;
 }
 
-template <bool QF32>
-int launch_fast(const DecodeParams& p, unsigned grid, hipStream_t s) {
-    const int G = p.Hq / p.Hkv;
-#define SKV_FAST(HD_, G_)                                                          \
-    if (p.HD == HD_ && G == G_) {                                                  \
-        decode_fast_kernel<HD_, G_, QF32><<<grid, 64, 0, s>>>(p);                  \
-        return check_launch("decode_fast_kernel");                                 \
-    }
-    SKV_FAST(64, 1) SKV_FAST(64, 2) SKV_FAST(64, 4) SKV_FAST(64, 8)
-    SKV_FAST(128, 1) SKV_FAST(128, 2) SKV_FAST(128, 4) SKV_FAST(128, 8)
-#undef SKV_FAST
-    return set_error(SKV_ERR_UNSUPPORTED, "no fast decode kernel for head_dim %d, group %d", p.HD, G);
+// Wavefronts of `kernel` resident on the device at once (with `lds` bytes of
+// dynamic LDS each), cached per device, kernel and LDS size.
+template <typename K>
+int resident_waves(K kernel, size_t lds) {
+    static std::mutex mu;
+    static std::unordered_map<std::string, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    char key[96];
+    std::snprintf(key, sizeof(key), "%d:%p:%zu", dev, reinterpret_cast<const void*>(kernel), lds);
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64, lds) != hipSuccess ||
+        per_cu <= 0)
+        per_cu = 4;
+    const int waves = std::min(kMaxWaves, cus * per_cu);
+    cache.emplace(key, waves);
+    return waves;
 }
 
-bool fast_path_ok(const DecodeParams& p, int q_dtype) {
+// Attention kernel over `ranges * Hseg` persistent wavefronts, then the merge.
+template <typename K>
+int launch_pair(K kern, DecodeParams p, hipStream_t s, const char* name) {
+    const size_t lds = sizeof(int) * (static_cast<size_t>(p.B) + 1);
+    const int waves = resident_waves(kern, lds);
+    p.ranges = std::max(1, waves / p.Hseg);
+    kern<<<static_cast<unsigned>(p.ranges) * p.Hseg, 64, lds, s>>>(p);
+    if (int rc = check_launch(name)) return rc;
+    decode_merge_kernel<<<static_cast<unsigned>(p.B) * p.Hseg, 256, 0, s>>>(p);
+    return check_launch("decode_merge_kernel");
+}
+
+template <bool QF32>
+int launch_mfma(const DecodeParams& p, hipStream_t s) {
     const int G = p.Hq / p.Hkv;
-    return p.bs == 16 && (p.HD == 64 || p.HD == 128) && (G == 1 || G == 2 || G == 4 || G == 8) &&
-           aligned16(p.k) && aligned16(p.v) && aligned16(p.q) && aligned16(p.out) &&
+#define SKV_MFMA(HD_, G_)                                                          \
+    if (p.HD == HD_ && G == G_) return launch_pair(decode_mfma_kernel<HD_, G_, QF32>, p, s, "decode_mfma_kernel");
+    SKV_MFMA(64, 1) SKV_MFMA(64, 2) SKV_MFMA(64, 4) SKV_MFMA(64, 8) SKV_MFMA(64, 16)
+    SKV_MFMA(128, 1) SKV_MFMA(128, 2) SKV_MFMA(128, 4) SKV_MFMA(128, 8) SKV_MFMA(128, 16)
+#undef SKV_MFMA
+    return set_error(SKV_ERR_UNSUPPORTED, "no MFMA decode kernel for head_dim %d, group %d", p.HD, G);
+}
+
+bool mfma_path_ok(const DecodeParams& p, int q_dtype) {
+    const int G = p.Hq / p.Hkv;
+    return p.bs == 16 && (p.HD == 64 || p.HD == 128) &&
+           (G == 1 || G == 2 || G == 4 || G == 8 || G == 16) && aligned16(p.k) && aligned16(p.v) &&
+           aligned16(p.q) && aligned16(p.out) &&
            (q_dtype == SKV_DTYPE_BF16 || q_dtype == SKV_DTYPE_FP32);
 }
 
+int run_decode_chunk(DecodeParams p, int q_dtype, char* ws, const WorkspaceLayout& w, hipStream_t s) {
+    p.plan = reinterpret_cast<int32_t*>(ws + w.plan_off);
+    p.ws_ml = reinterpret_cast<float*>(ws + w.ml_off);
+    p.ws_acc = reinterpret_cast<float*>(ws + w.acc_off);
+    if (mfma_path_ok(p, q_dtype)) {
+        p.Hseg = p.Hkv;
+        p.NH = p.Hq / p.Hkv;
+        p.min_per = 4;
+        return q_dtype == SKV_DTYPE_FP32 ? launch_mfma<true>(p, s) : launch_mfma<false>(p, s);
+    }
+    p.Hseg = p.Hq;
+    p.NH = 1;
+    p.min_per = std::max(1, cdiv(64, p.bs));
+    return q_dtype == SKV_DTYPE_FP32 ? launch_pair(decode_generic_kernel<true>, p, s, "decode_generic_kernel")
+                                     : launch_pair(decode_generic_kernel<false>, p, s, "decode_generic_kernel");
+}
+
+// Batches larger than kMaxBatchPerLaunch run as consecutive launches on the
+// same stream (sequences are independent), reusing the workspace.
 int run_decode(DecodeParams p, int q_dtype, void* workspace, size_t workspace_bytes,
                hipStream_t s) {
     const WorkspaceLayout w = workspace_layout(p.B, p.Hq, p.Hkv, p.HD);
@@ -511,32 +750,24 @@ int run_decode(DecodeParams p, int q_dtype, void* workspace, size_t workspace_by
         return set_error(SKV_ERR_WORKSPACE,
                          "decode workspace of %zu bytes is smaller than the %zu required",
                          workspace_bytes, w.total);
-    char* ws = static_cast<char*>(workspace);
-    p.plan = reinterpret_cast<int32_t*>(ws + w.plan_off);
-    p.ws_ml = reinterpret_cast<float*>(ws + w.ml_off);
-    p.ws_acc = reinterpret_cast<float*>(ws + w.acc_off);
-    p.target_parts = parts_target(p.Hkv);
-    p.min_bpu = std::max(1, cdiv(64, p.bs));
-
-    decode_plan_kernel<<<1, 1024, 0, s>>>(p);
-    if (int rc = check_launch("decode_plan_kernel")) return rc;
-
-    int rc;
-    if (fast_path_ok(p, q_dtype)) {
-        const unsigned grid = static_cast<unsigned>(w.parts_cap) * p.Hkv;
-        rc = q_dtype == SKV_DTYPE_FP32 ? launch_fast<true>(p, grid, s) : launch_fast<false>(p, grid, s);
-    } else {
-        const unsigned grid = static_cast<unsigned>(w.parts_cap) * p.Hq;
-        if (q_dtype == SKV_DTYPE_FP32)
-            decode_generic_kernel<true><<<grid, 64, 0, s>>>(p);
-        else
-            decode_generic_kernel<false><<<grid, 64, 0, s>>>(p);
-        rc = check_launch("decode_generic_kernel");
+    // Flattened (sequence, block) indices are int32 on the device.
+    const long long flat_bound = static_cast<long long>(std::min(p.B, kMaxBatchPerLaunch)) * p.max_blocks;
+    if (flat_bound >= (1ll << 30))
+        return set_error(SKV_ERR_UNSUPPORTED,
+                         "batch x table width = %lld exceeds the 2^30 work index range", flat_bound);
+    const size_t q_elem = q_dtype == SKV_DTYPE_FP32 ? 4 : 2;
+    const int B = p.B;
+    for (int b0 = 0; b0 < B; b0 += kMaxBatchPerLaunch) {
+        DecodeParams c = p;
+        c.B = std::min(kMaxBatchPerLaunch, B - b0);
+        const size_t head_rows = static_cast<size_t>(b0) * p.Hq * p.HD;
+        c.q = static_cast<const char*>(p.q) + head_rows * q_elem;
+        c.out = p.out + head_rows;
+        c.tables = p.tables + static_cast<int64_t>(b0) * p.max_blocks;
+        if (p.lens != nullptr) c.lens = p.lens + b0;
+        if (int rc = run_decode_chunk(c, q_dtype, static_cast<char*>(workspace), w, s)) return rc;
     }
-    if (rc) return rc;
-
-    decode_merge_kernel<<<static_cast<unsigned>(p.B) * p.Hq, 256, 0, s>>>(p);
-    return check_launch("decode_merge_kernel");
+    return SKV_OK;
 }
 
 int validate_geometry(const char* fn, int B, int Hq, int Hkv, int HD, int bs, float scale) {

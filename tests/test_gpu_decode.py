@@ -124,3 +124,21 @@ def test_long_context_split_merge(gpu):
     Hq, Hkv, hd = L3
     case = make_case(1, Hq, Hkv, hd, 16, [32768], layout="random", seed=21)
     _check(gpu, case, "L3 32k")
+
+
+@pytest.mark.parametrize("geom", [TL, L3, (8, 1, 256)], ids=["tl", "l3", "generic"])
+def test_unused_slots_holding_nan_are_never_used(gpu, geom):
+    """Slots past a context in its last block may hold anything (freed data,
+    uninitialised memory); NaN bit patterns there must not reach the output."""
+    Hq, Hkv, hd = geom
+    lens = [17, 40, 1, 250]
+    case = make_case(len(lens), Hq, Hkv, hd, 16, lens, layout="random", seed=13)
+    for b, L in enumerate(lens):
+        last = case["tables"][b, (L - 1) // 16]
+        case["k_pool"][last, L % 16 or 16:] = 0xFFFF
+        case["v_pool"][last, L % 16 or 16:] = 0xFFFF
+    unused = np.ones(case["total_blocks"], bool)
+    unused[case["tables"][case["tables"] >= 0]] = False
+    case["k_pool"][unused] = 0xFFFF
+    case["v_pool"][unused] = 0xFFFF
+    _check(gpu, case, f"nan slots {geom}")
