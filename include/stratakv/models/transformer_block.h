@@ -1,0 +1,105 @@
+// transformer_block.h -- one Llama decoder layer; forward_into is the GPU
+// decode step of one token of one sequence, the drop-in boundary of the paged
+// KV-cache path.
+//
+// Interface of the reference's stratakv::models::TransformerBlock
+// (include/stratakv/models/transformer_block.h:13-103).  to(Device::GPU)
+// moves the parameters and allocates the persistent scratchpads once (the
+// reference's 11 FP32 workspaces plus the decode workspace); forward_into
+// never allocates.  Sub-steps (src/models/transformer_block.cpp:334-613):
+// rmsnorm, q/k/v projections, split-half RoPE at the token's position,
+// PageTable::append_token, the KV append of the rotated K and V rows into the
+// bf16 pools (skv_kv_append_token), the device block table, paged decode
+// attention (skv_paged_attention_decode), o_proj + residual, rmsnorm,
+// gate/up, SwiGLU, down + residual, and the final copy that keeps
+// hidden_states/output aliasing safe.  All device work is queued on one
+// stream (the null stream by default, as the reference's legacy stream).
+#pragma once
+
+#include <cstddef>
+#include <optional>
+
+#include "stratakv/layers/attention.h"
+#include "stratakv/layers/linear.h"
+#include "stratakv/layers/rmsnorm.h"
+
+namespace stratakv {
+namespace models {
+
+class TransformerBlock {
+public:
+    TransformerBlock(std::size_t hidden_dim, std::size_t intermediate_dim, std::size_t num_heads,
+                     int total_blocks, int block_size, Device device = Device::CPU);
+    TransformerBlock(std::size_t hidden_dim, std::size_t intermediate_dim, std::size_t num_heads,
+                     std::size_t num_kv_heads, int total_blocks, int block_size,
+                     Device device = Device::CPU);
+
+    TransformerBlock(const TransformerBlock&) = delete;
+    TransformerBlock& operator=(const TransformerBlock&) = delete;
+    TransformerBlock(TransformerBlock&&) noexcept = default;
+    TransformerBlock& operator=(TransformerBlock&&) noexcept = default;
+    ~TransformerBlock() = default;
+
+    void to(Device device);
+    void set_parity_diagnostic(bool enabled) noexcept { parity_diagnostic_ = enabled; }
+    // Stream for the device work of forward_into (a hipStream_t; nullptr =
+    // the default stream).
+    void set_stream(void* stream) noexcept { stream_ = stream; }
+
+    // GPU tensors: allocates the result and runs forward_into.  CPU tensors:
+    // the reference's CPU path, not provided by this build (throws).
+    Tensor forward(const Tensor& hidden_states, int seq_id, memory::PageTable& page_table,
+                   memory::BlockPool& block_pool, bool append_tokens = true);
+    void forward_into(const Tensor& hidden_states, Tensor& output, int seq_id,
+                      memory::PageTable& page_table, memory::BlockPool& block_pool,
+                      bool append_tokens = true);
+
+    std::size_t last_attention_blocks_visited() const noexcept {
+        return attention_.last_blocks_visited();
+    }
+
+    layers::RMSNorm& input_norm() noexcept { return norm1_; }
+    const layers::RMSNorm& input_norm() const noexcept { return norm1_; }
+    layers::PagedAttention& attention() noexcept { return attention_; }
+    const layers::PagedAttention& attention() const noexcept { return attention_; }
+    layers::RMSNorm& post_attention_norm() noexcept { return norm2_; }
+    const layers::RMSNorm& post_attention_norm() const noexcept { return norm2_; }
+    layers::Linear& gate_projection() noexcept { return gate_proj_; }
+    const layers::Linear& gate_projection() const noexcept { return gate_proj_; }
+    layers::Linear& up_projection() noexcept { return up_proj_; }
+    const layers::Linear& up_projection() const noexcept { return up_proj_; }
+    layers::Linear& down_projection() noexcept { return down_proj_; }
+    const layers::Linear& down_projection() const noexcept { return down_proj_; }
+    layers::Linear& gate_proj() noexcept { return gate_proj_; }
+    const layers::Linear& gate_proj() const noexcept { return gate_proj_; }
+    layers::Linear& up_proj() noexcept { return up_proj_; }
+    const layers::Linear& up_proj() const noexcept { return up_proj_; }
+    layers::Linear& down_proj() noexcept { return down_proj_; }
+    const layers::Linear& down_proj() const noexcept { return down_proj_; }
+
+private:
+    std::size_t hidden_dim_;
+    layers::RMSNorm norm1_;
+    layers::PagedAttention attention_;
+    layers::RMSNorm norm2_;
+    layers::Linear gate_proj_;
+    layers::Linear up_proj_;
+    layers::Linear down_proj_;
+    bool parity_diagnostic_ = false;
+    void* stream_ = nullptr;
+    // Persistent GPU scratchpads, allocated by to(Device::GPU) and reused by
+    // every forward_into; a block serves one request at a time.
+    std::optional<Tensor> normalized_input_workspace_;
+    std::optional<Tensor> query_workspace_;
+    std::optional<Tensor> key_workspace_;
+    std::optional<Tensor> value_workspace_;
+    std::optional<Tensor> context_workspace_;
+    std::optional<Tensor> normalized_residual_workspace_;
+    std::optional<Tensor> gate_workspace_;
+    std::optional<Tensor> up_workspace_;
+    std::optional<Tensor> down_workspace_;
+    std::optional<Tensor> decode_workspace_;  // skv_paged_attention_decode scratch
+};
+
+}  // namespace models
+}  // namespace stratakv

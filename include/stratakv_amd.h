@@ -71,11 +71,21 @@ int skv_stream_create(void** stream);
 int skv_stream_destroy(void* stream);
 int skv_stream_synchronize(void* stream);
 int skv_device_synchronize(void);
-/* Events for timing on a given stream. */
+/* Events for timing and ordering on a given stream. */
 int skv_event_create(void** event);
 int skv_event_destroy(void* event);
 int skv_event_record(void* event, void* stream);
+int skv_event_synchronize(void* event);
 int skv_event_elapsed_ms(float* ms, void* start, void* stop);
+/* Page-locked host memory, so host-to-device copies can run asynchronously. */
+int skv_host_alloc(void** ptr, size_t bytes);
+int skv_host_free(void* ptr);
+/* Asynchronous copy on `stream` (src should be page-locked; the call returns
+ * before the copy completes). */
+int skv_memcpy_h2d_async(void* dst, const void* src, size_t bytes, void* stream);
+/* dst[pairs[2i]] = pairs[2i+1] for i < n: applies a batch of (index, value)
+ * updates to a device int32 array (incremental block-table upload). */
+int skv_scatter_i32(int32_t* dst, const int32_t* pairs, int n, void* stream);
 
 /* ---- synthetic data ------------------------------------------------------ */
 /* dst[i] = bf16_rne(N(0,1) sample derived from (seed, first_index + i)) via a
@@ -109,6 +119,16 @@ int skv_kv_append(const void* k_new, const void* v_new, int src_dtype,
                   int num_seqs, int tokens_per_seq,
                   int num_kv_heads, int head_dim, int block_size,
                   void* stream);
+
+/* Single-token append with the position passed by value: the exact
+ * replacement for the two per-token cudaMemcpy of one K row and one V row
+ * (src/models/transformer_block.cpp:484-509).  block_table is the
+ * sequence's device table of table_len entries. */
+int skv_kv_append_token(const void* k_row, const void* v_row, int src_dtype,
+                        uint16_t* k_pool, uint16_t* v_pool, int64_t total_blocks,
+                        const int32_t* block_table, int table_len, int position,
+                        int num_kv_heads, int head_dim, int block_size,
+                        void* stream);
 
 /* ---- paged decode attention ---------------------------------------------
  * One query token per sequence, grouped-query attention over the paged pools:
@@ -154,6 +174,29 @@ int skv_paged_attention_decode(const float* query, const uint16_t* key_cache,
                                int num_q_heads, int num_kv_heads, int head_dim,
                                float scale, void* workspace,
                                size_t workspace_bytes, void* stream);
+
+/* ---- decoder-layer sub-steps around the path -----------------------------
+ * Used by TransformerBlock::forward_into (include/stratakv/models/) for the
+ * steps before and after the KV append and decode; fp32 activations.
+ * Reference kernels replaced: rmsnorm_cuda, matmul_cuda_tiled's M=1 GEMV,
+ * rope_split_half_cuda + generate_rope_frequencies_cuda, swiglu_inplace_cuda,
+ * add_inplace_cuda (include/stratakv/cuda/gemm_cuda.h:13-38). */
+/* out[r] = in[r] / sqrt(mean(in[r]^2) + epsilon) * gamma, rows of `hidden`. */
+int skv_rmsnorm_f32(const float* input, float* output, const float* gamma,
+                    int rows, int hidden, float epsilon, void* stream);
+/* y[r][n] = sum_k x[r][k] * W[k][n] (+ bias[n]); W element (k, n) lives at
+ * weight[k * stride_k + n * stride_n], bf16 or fp32 (weight_dtype); either
+ * stride_k == 1 (output-major rows) or stride_n == 1 (GEMM-ready). */
+int skv_linear_f32(const float* x, int rows, const void* weight, int weight_dtype,
+                   int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
+                   const float* bias, float* y, void* stream);
+/* In-place split-half rotary embedding of `heads` contiguous head vectors at
+ * `position` (src/layers/attention.cpp:96-135). */
+int skv_rope_f32(float* x, int heads, int head_dim, int position, void* stream);
+/* gate[i] = gate[i] * sigmoid(gate[i]) * up[i]. */
+int skv_swiglu_f32(float* gate, const float* up, int n, void* stream);
+/* target[i] += source[i]. */
+int skv_add_f32(float* target, const float* source, int n, void* stream);
 
 /* ---- test support --------------------------------------------------------
  * Copy the blocks listed in table[0..num_blocks) of a pool into a contiguous

@@ -61,11 +61,18 @@ _PROTOS = {
     "skv_event_create": (_i32, [_c.POINTER(_vp)]),
     "skv_event_destroy": (_i32, [_vp]),
     "skv_event_record": (_i32, [_vp, _vp]),
+    "skv_event_synchronize": (_i32, [_vp]),
     "skv_event_elapsed_ms": (_i32, [_c.POINTER(_f32), _vp, _vp]),
+    "skv_host_alloc": (_i32, [_c.POINTER(_vp), _sz]),
+    "skv_host_free": (_i32, [_vp]),
+    "skv_memcpy_h2d_async": (_i32, [_vp, _vp, _sz, _vp]),
+    "skv_scatter_i32": (_i32, [_vp, _vp, _i32, _vp]),
     "skv_fill_normal_bf16": (_i32, [_vp, _sz, _u64, _u64, _vp]),
     "skv_fill_u16": (_i32, [_vp, _sz, _c.c_uint16, _vp]),
     "skv_kv_append": (_i32, [_vp, _vp, _i32, _vp, _vp, _i64, _vp, _i32, _vp, _vp,
                              _i32, _i32, _i32, _i32, _i32, _vp]),
+    "skv_kv_append_token": (_i32, [_vp, _vp, _i32, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32,
+                                   _i32, _vp]),
     "skv_paged_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "skv_paged_decode": (_i32, [_vp, _i32, _vp, _vp, _i64, _vp, _i32, _vp, _i32, _i32, _i32,
                                 _i32, _i32, _f32, _vp, _vp, _sz, _vp]),
@@ -73,6 +80,11 @@ _PROTOS = {
     "skv_paged_attention_decode": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32,
                                           _i32, _f32, _vp, _sz, _vp]),
     "skv_gather_blocks": (_i32, [_vp, _i64, _vp, _i32, _i64, _vp, _vp]),
+    "skv_rmsnorm_f32": (_i32, [_vp, _vp, _vp, _i32, _i32, _f32, _vp]),
+    "skv_linear_f32": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "skv_rope_f32": (_i32, [_vp, _i32, _i32, _i32, _vp]),
+    "skv_swiglu_f32": (_i32, [_vp, _vp, _i32, _vp]),
+    "skv_add_f32": (_i32, [_vp, _vp, _i32, _vp]),
 }
 
 _lib = None

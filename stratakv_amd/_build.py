@@ -43,15 +43,26 @@ def _run(cmd: list[str], cwd: str | None = None) -> None:
         sys.stderr.write(out + "\n")
 
 
+OBJ = os.path.join(ROOT, "build", "obj")
+CXX = os.environ.get("CXX", "g++")
+
+
 def build_library() -> str:
-    """Compile the HIP kernels, C ABI and C++ host layer into one shared library."""
-    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    host = sorted(glob.glob(os.path.join(CSRC, "host", "*.cpp")))
-    cmd = [HIPCC, *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}", *sources]
-    for h in host:
-        cmd += ["-x", "c++", h]
-    cmd += ["-o", LIB + ".tmp"]
-    _run(cmd)
+    """Compile the HIP kernels and C ABI (hipcc, gfx950) and the C++ host
+    layer (plain C++17; it reaches the GPU only through the C ABI) into one
+    shared library."""
+    os.makedirs(OBJ, exist_ok=True)
+    objs = []
+    for src in sorted(glob.glob(os.path.join(CSRC, "host", "*.cpp"))):
+        obj = os.path.join(OBJ, os.path.basename(src) + ".o")
+        _run([CXX, "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", f"-I{INCLUDE}", "-c", src,
+              "-o", obj])
+        objs.append(obj)
+    for src in sorted(glob.glob(os.path.join(CSRC, "*.hip"))):
+        obj = os.path.join(OBJ, os.path.basename(src) + ".o")
+        _run([HIPCC, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj])
+        objs.append(obj)
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", *objs, "-o", LIB + ".tmp"])
     os.replace(LIB + ".tmp", LIB)
     return LIB
 

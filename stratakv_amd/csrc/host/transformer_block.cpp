@@ -1,0 +1,210 @@
+// transformer_block.cpp -- TransformerBlock::to / forward / forward_into.
+// The GPU decode step follows src/models/transformer_block.cpp:334-613 of the
+// reference sub-step for sub-step; the KV append and the paged decode are the
+// hot path (skv_kv_append_token, skv_paged_attention_decode); the other
+// sub-steps use the simple kernels of skv_layer_ops.hip.
+#include "stratakv/models/transformer_block.h"
+
+#include <cmath>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "abi_check.h"
+
+namespace stratakv {
+namespace models {
+
+TransformerBlock::TransformerBlock(std::size_t hidden_dim, std::size_t intermediate_dim,
+                                   std::size_t num_heads, int total_blocks, int block_size,
+                                   Device device)
+    : TransformerBlock(hidden_dim, intermediate_dim, num_heads, 0, total_blocks, block_size, device) {}
+
+TransformerBlock::TransformerBlock(std::size_t hidden_dim, std::size_t intermediate_dim,
+                                   std::size_t num_heads, std::size_t num_kv_heads, int total_blocks,
+                                   int block_size, Device device)
+    : hidden_dim_(hidden_dim),
+      norm1_(hidden_dim == 0 ? 1 : hidden_dim),
+      attention_(hidden_dim, num_heads, num_kv_heads, total_blocks, block_size, device),
+      norm2_(hidden_dim == 0 ? 1 : hidden_dim),
+      gate_proj_(hidden_dim, intermediate_dim == 0 ? 1 : intermediate_dim),
+      up_proj_(hidden_dim, intermediate_dim == 0 ? 1 : intermediate_dim),
+      down_proj_(intermediate_dim == 0 ? 1 : intermediate_dim, hidden_dim) {
+    if (hidden_dim == 0 || intermediate_dim == 0)
+        throw std::invalid_argument("TransformerBlock: feature dimensions must be non-zero");
+}
+
+void TransformerBlock::to(Device device) {
+    norm1_.to(device);
+    attention_.query_projection().to(device);
+    attention_.key_projection().to(device);
+    attention_.value_projection().to(device);
+    attention_.output_projection().to(device);
+    norm2_.to(device);
+    gate_proj_.to(device);
+    up_proj_.to(device);
+    down_proj_.to(device);
+    if (device == Device::GPU) {
+        const std::size_t kv_dim = attention_.num_kv_heads() * attention_.head_dim();
+        const std::size_t inter = gate_proj_.output_dim();
+        normalized_input_workspace_.emplace(std::vector<std::size_t>{1, hidden_dim_}, DataType::FP32, device);
+        query_workspace_.emplace(std::vector<std::size_t>{1, hidden_dim_}, DataType::FP32, device);
+        key_workspace_.emplace(std::vector<std::size_t>{1, kv_dim}, DataType::FP32, device);
+        value_workspace_.emplace(std::vector<std::size_t>{1, kv_dim}, DataType::FP32, device);
+        context_workspace_.emplace(std::vector<std::size_t>{1, hidden_dim_}, DataType::FP32, device);
+        normalized_residual_workspace_.emplace(std::vector<std::size_t>{1, hidden_dim_}, DataType::FP32, device);
+        gate_workspace_.emplace(std::vector<std::size_t>{1, inter}, DataType::FP32, device);
+        up_workspace_.emplace(std::vector<std::size_t>{1, inter}, DataType::FP32, device);
+        down_workspace_.emplace(std::vector<std::size_t>{1, hidden_dim_}, DataType::FP32, device);
+        const std::size_t ws = skv_paged_attention_decode_workspace_bytes(
+            static_cast<int>(attention_.num_heads()), static_cast<int>(attention_.num_kv_heads()),
+            static_cast<int>(attention_.head_dim()));
+        decode_workspace_.emplace(std::vector<std::size_t>{ws}, DataType::FP32, device);
+    } else {
+        normalized_input_workspace_.reset();
+        query_workspace_.reset();
+        key_workspace_.reset();
+        value_workspace_.reset();
+        context_workspace_.reset();
+        normalized_residual_workspace_.reset();
+        gate_workspace_.reset();
+        up_workspace_.reset();
+        down_workspace_.reset();
+        decode_workspace_.reset();
+    }
+}
+
+Tensor TransformerBlock::forward(const Tensor& hidden_states, int seq_id, memory::PageTable& page_table,
+                                 memory::BlockPool& block_pool, bool append_tokens) {
+    if (hidden_states.ndim() != 2 || hidden_states.shape()[1] != hidden_dim_)
+        throw std::invalid_argument("TransformerBlock::forward: hidden_states must be [tokens, hidden_dim]");
+    if (hidden_states.device() == Device::GPU) {
+        Tensor result({1, hidden_dim_}, DataType::FP32, Device::GPU);
+        forward_into(hidden_states, result, seq_id, page_table, block_pool, append_tokens);
+        return result;
+    }
+    throw std::runtime_error(
+        "TransformerBlock::forward: the CPU path is not part of this build; move the block and "
+        "the hidden states to Device::GPU");
+}
+
+void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output, int seq_id,
+                                    memory::PageTable& page_table, memory::BlockPool& block_pool,
+                                    bool append_tokens) {
+    // Validation in the order and with the messages of
+    // src/models/transformer_block.cpp:338-394.
+    if (hidden_states.ndim() != 2 || hidden_states.shape()[1] != hidden_dim_ ||
+        output.device() != hidden_states.device() || output.shape() != hidden_states.shape() ||
+        output.dtype() != DataType::FP32)
+        throw std::invalid_argument("TransformerBlock::forward_into: output shape or device mismatch");
+    if (output.device() != Device::GPU)
+        throw std::runtime_error(
+            "TransformerBlock::forward_into: the CPU path is not part of this build; use GPU tensors");
+    if (hidden_states.shape()[0] != 1)
+        throw std::invalid_argument("TransformerBlock::forward_into: GPU decode requires one token");
+    if (hidden_states.dtype() != DataType::FP32)
+        throw std::runtime_error("TransformerBlock::forward_into: hidden_states is not FP32");
+    if (norm1_.gamma().dtype() != DataType::FP32 || norm2_.gamma().dtype() != DataType::FP32 ||
+        norm1_.gamma().device() != Device::GPU || norm2_.gamma().device() != Device::GPU)
+        throw std::runtime_error("TransformerBlock::forward_into: RMSNorm weights are not on GPU");
+    if (attention_.query_projection().weight().device() != Device::GPU ||
+        attention_.key_projection().weight().device() != Device::GPU ||
+        attention_.value_projection().weight().device() != Device::GPU ||
+        attention_.output_projection().weight().device() != Device::GPU ||
+        gate_proj_.weight().device() != Device::GPU || up_proj_.weight().device() != Device::GPU ||
+        down_proj_.weight().device() != Device::GPU)
+        throw std::runtime_error("TransformerBlock::forward_into: projection weights are not on GPU");
+    if (block_pool.device() != Device::GPU || block_pool.key_cache() == nullptr ||
+        block_pool.value_cache() == nullptr ||
+        block_pool.num_kv_heads() != static_cast<int>(attention_.num_kv_heads()) ||
+        block_pool.head_dim() != static_cast<int>(attention_.head_dim()))
+        throw std::invalid_argument(
+            "TransformerBlock::forward_into: GPU BlockPool configuration does not match attention");
+    if (!page_table.has_sequence(seq_id))
+        throw std::runtime_error("TransformerBlock::forward_into: seq_id is not registered");
+    if (!normalized_input_workspace_ || !query_workspace_ || !key_workspace_ || !value_workspace_ ||
+        !context_workspace_ || !normalized_residual_workspace_ || !gate_workspace_ ||
+        !up_workspace_ || !down_workspace_ || !decode_workspace_)
+        throw std::runtime_error("TransformerBlock::forward_into: GPU workspace is not initialized");
+
+    const memory::SequenceState& initial_state = page_table.get_state(seq_id);
+    if (initial_state.sequence_length <= 0 && !append_tokens)
+        throw std::invalid_argument("TransformerBlock::forward_into: cannot decode without context");
+    const int logical_position = initial_state.sequence_length;
+    if (append_tokens) page_table.append_token(seq_id, block_pool);
+    const memory::SequenceState& state = page_table.get_state(seq_id);
+    const int context_len = state.sequence_length;
+    const int position = append_tokens ? logical_position : context_len - 1;
+    const int block_size = block_pool.block_size();
+    const int head_dim = static_cast<int>(attention_.head_dim());
+    const int num_heads = static_cast<int>(attention_.num_heads());
+    const int num_kv_heads = static_cast<int>(attention_.num_kv_heads());
+    const int hidden = static_cast<int>(hidden_dim_);
+    const int inter = static_cast<int>(gate_proj_.output_dim());
+    if (position / block_size >= static_cast<int>(state.physical_blocks.size()))
+        throw std::runtime_error("TransformerBlock::forward_into: no KV page for decode position");
+    void* s = stream_;
+
+    auto fp = [](Tensor& t) { return static_cast<float*>(t.raw_data()); };
+    auto cfp = [](const Tensor& t) { return static_cast<const float*>(t.raw_data()); };
+    auto linear = [&](const layers::Linear& layer, const Tensor& x, Tensor& y, const char* what) {
+        const Tensor& w = layer.weight();
+        detail::check(skv_linear_f32(cfp(x), 1, w.raw_data(),
+                                     w.dtype() == DataType::BF16 ? SKV_DTYPE_BF16 : SKV_DTYPE_FP32,
+                                     static_cast<int64_t>(w.strides()[0]), static_cast<int64_t>(w.strides()[1]),
+                                     static_cast<int>(layer.input_dim()), static_cast<int>(layer.output_dim()),
+                                     layer.bias() ? cfp(*layer.bias()) : nullptr, fp(y), s),
+                      what);
+    };
+    Tensor& normalized_input = *normalized_input_workspace_;
+    Tensor& queries = *query_workspace_;
+    Tensor& keys = *key_workspace_;
+    Tensor& values = *value_workspace_;
+    Tensor& context = *context_workspace_;
+    Tensor& normalized_residual = *normalized_residual_workspace_;
+    Tensor& gate = *gate_workspace_;
+    Tensor& up = *up_workspace_;
+    Tensor& down = *down_workspace_;
+
+    detail::check(skv_rmsnorm_f32(cfp(hidden_states), fp(normalized_input), cfp(norm1_.gamma()), 1, hidden,
+                                  norm1_.epsilon(), s),
+                  "forward_into: input rmsnorm");
+    linear(attention_.query_projection(), normalized_input, queries, "forward_into: q_proj");
+    linear(attention_.key_projection(), normalized_input, keys, "forward_into: k_proj");
+    linear(attention_.value_projection(), normalized_input, values, "forward_into: v_proj");
+    detail::check(skv_rope_f32(fp(queries), num_heads, head_dim, position, s), "forward_into: rope q");
+    detail::check(skv_rope_f32(fp(keys), num_kv_heads, head_dim, position, s), "forward_into: rope k");
+
+    // The paged-KV hot path: device block table (only new block ids are
+    // uploaded), the K/V append of this token, then the decode.
+    const int* table = page_table.get_device_block_table(seq_id);
+    const int table_len = static_cast<int>(state.physical_blocks.size());
+    detail::check(skv_kv_append_token(cfp(keys), cfp(values), SKV_DTYPE_FP32, block_pool.key_cache(),
+                                      block_pool.value_cache(), block_pool.total_blocks(), table,
+                                      table_len, position, num_kv_heads, head_dim, block_size, s),
+                  "forward_into: KV append");
+    Tensor& ws = *decode_workspace_;
+    detail::check(skv_paged_attention_decode(cfp(queries), block_pool.key_cache(), block_pool.value_cache(),
+                                             block_pool.total_blocks(), table, fp(context), context_len,
+                                             block_size, num_heads, num_kv_heads, head_dim,
+                                             1.0f / std::sqrt(static_cast<float>(head_dim)), ws.raw_data(),
+                                             ws.num_elements() * ws.element_size(), s),
+                  "forward_into: paged attention");
+
+    linear(attention_.output_projection(), context, down, "forward_into: o_proj");
+    // Residual: reads hidden_states before output is written (aliasing-safe).
+    detail::check(skv_add_f32(fp(down), cfp(hidden_states), hidden, s), "forward_into: residual");
+    detail::check(skv_rmsnorm_f32(cfp(down), fp(normalized_residual), cfp(norm2_.gamma()), 1, hidden,
+                                  norm2_.epsilon(), s),
+                  "forward_into: post-attention rmsnorm");
+    linear(gate_proj_, normalized_residual, gate, "forward_into: gate_proj");
+    linear(up_proj_, normalized_residual, up, "forward_into: up_proj");
+    detail::check(skv_swiglu_f32(fp(gate), cfp(up), inter, s), "forward_into: swiglu");
+    linear(down_proj_, gate, context, "forward_into: down_proj");
+    detail::check(skv_add_f32(fp(down), cfp(context), hidden, s), "forward_into: residual");
+    detail::check(skv_memcpy_d2d(output.raw_data(), down.raw_data(), hidden_dim_ * sizeof(float), s),
+                  "forward_into: output copy");
+}
+
+}  // namespace models
+}  // namespace stratakv

@@ -24,7 +24,8 @@ struct AppendParams {
     int64_t total_blocks;
     const int32_t* tables;
     int max_blocks;
-    const int32_t* positions;
+    const int32_t* positions; // [num_seqs], or nullptr -> single_position
+    int single_position;
     const int32_t* offsets;   // [num_seqs + 1] or nullptr
     int num_seqs;
     int tokens_per_seq;       // tokens per sequence (upper bound when offsets != nullptr)
@@ -44,7 +45,7 @@ __device__ __forceinline__ bool resolve_row(const AppendParams& p, int b, int j,
     } else {
         src_row = static_cast<int64_t>(b) * p.tokens_per_seq + j;
     }
-    const int pos = p.positions[b] + j;
+    const int pos = (p.positions != nullptr ? p.positions[b] : p.single_position) + j;
     if (pos < 0) return false;
     const int blk = pos / p.block_size;
     if (blk >= p.max_blocks) return false;
@@ -113,6 +114,8 @@ __global__ __launch_bounds__(256) void kv_append_scalar_kernel(AppendParams p) {
     }
 }
 
+int launch_append(const AppendParams& p, int src_dtype, hipStream_t s);
+
 }  // namespace skv
 
 using namespace skv;
@@ -138,13 +141,43 @@ extern "C" int skv_kv_append(const void* k_new, const void* v_new, int src_dtype
                 static_cast<long long>(row));
 
     AppendParams p{k_new, v_new, k_pool, v_pool, total_blocks, block_tables, max_blocks_per_seq,
-                   positions, token_offsets, num_seqs, tokens_per_seq, static_cast<int>(row),
+                   positions, 0, token_offsets, num_seqs, tokens_per_seq, static_cast<int>(row),
                    block_size};
+    return launch_append(p, src_dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int skv_kv_append_token(const void* k_row, const void* v_row, int src_dtype,
+                                   uint16_t* k_pool, uint16_t* v_pool, int64_t total_blocks,
+                                   const int32_t* block_table, int table_len, int position,
+                                   int num_kv_heads, int head_dim, int block_size, void* stream) {
+    SKV_REQUIRE(k_row && v_row && k_pool && v_pool && block_table,
+                "skv_kv_append_token: NULL pointer");
+    SKV_REQUIRE(src_dtype == SKV_DTYPE_BF16 || src_dtype == SKV_DTYPE_FP32,
+                "skv_kv_append_token: unknown source dtype %d", src_dtype);
+    SKV_REQUIRE(total_blocks > 0 && table_len > 0 && num_kv_heads > 0 && head_dim > 0 &&
+                    block_size > 0 && position >= 0,
+                "skv_kv_append_token: invalid dimensions or position");
+    SKV_REQUIRE(position / block_size < table_len,
+                "skv_kv_append_token: no KV page for position %d", position);
+    const int64_t row = static_cast<int64_t>(num_kv_heads) * head_dim;
+    SKV_REQUIRE(row <= (1 << 24), "skv_kv_append_token: row too large");
+    AppendParams p{k_row, v_row, k_pool, v_pool, total_blocks, block_table, table_len, nullptr,
+                   position, nullptr, 1, 1, static_cast<int>(row), block_size};
+    return launch_append(p, src_dtype, static_cast<hipStream_t>(stream));
+}
+
+namespace skv {
+int launch_append(const AppendParams& p, int src_dtype, hipStream_t s) {
+    const int64_t row = p.row_elems;
+    const int num_seqs = p.num_seqs, tokens_per_seq = p.tokens_per_seq;
+    const void* k_new = p.k_new;
+    const void* v_new = p.v_new;
+    const uint16_t* k_pool = p.k_pool;
+    const uint16_t* v_pool = p.v_pool;
     const bool vec = (row % 8) == 0 && aligned16(k_new) && aligned16(v_new) &&
                      aligned16(k_pool) && aligned16(v_pool);
     const int64_t items = static_cast<int64_t>(num_seqs) * tokens_per_seq * (vec ? row / 8 : row);
     const unsigned grid = static_cast<unsigned>(std::min<int64_t>(cdiv<int64_t>(items, 256), 8192));
-    hipStream_t s = static_cast<hipStream_t>(stream);
     if (vec) {
         if (src_dtype == SKV_DTYPE_FP32)
             kv_append_vec_kernel<true><<<grid, 256, 0, s>>>(p);
@@ -158,3 +191,4 @@ extern "C" int skv_kv_append(const void* k_new, const void* v_new, int src_dtype
     }
     return check_launch("kv_append_kernel");
 }
+}  // namespace skv

@@ -94,6 +94,12 @@ __global__ void gather_blocks_kernel(const uint16_t* __restrict__ pool, int64_t 
         out[e] = ok ? in[e] : uint16_t(0);
 }
 
+__global__ void scatter_i32_kernel(int32_t* __restrict__ dst, const int32_t* __restrict__ pairs,
+                                   int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[pairs[2 * i]] = pairs[2 * i + 1];
+}
+
 }  // namespace skv
 
 using namespace skv;
@@ -204,6 +210,40 @@ int skv_event_record(void* event, void* stream) {
     SKV_REQUIRE(event != nullptr, "skv_event_record: NULL event");
     SKV_HIP_TRY(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)));
     return SKV_OK;
+}
+
+int skv_event_synchronize(void* event) {
+    SKV_REQUIRE(event != nullptr, "skv_event_synchronize: NULL event");
+    SKV_HIP_TRY(hipEventSynchronize(static_cast<hipEvent_t>(event)));
+    return SKV_OK;
+}
+
+int skv_host_alloc(void** ptr, size_t bytes) {
+    SKV_REQUIRE(ptr != nullptr, "skv_host_alloc: ptr is NULL");
+    *ptr = nullptr;
+    if (bytes == 0) return SKV_OK;
+    SKV_HIP_TRY(hipHostMalloc(ptr, bytes, hipHostMallocDefault));
+    return SKV_OK;
+}
+
+int skv_host_free(void* ptr) {
+    if (ptr != nullptr) SKV_HIP_TRY(hipHostFree(ptr));
+    return SKV_OK;
+}
+
+int skv_memcpy_h2d_async(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return SKV_OK;
+    SKV_REQUIRE(dst && src, "skv_memcpy_h2d_async: NULL pointer");
+    SKV_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice,
+                               static_cast<hipStream_t>(stream)));
+    return SKV_OK;
+}
+
+int skv_scatter_i32(int32_t* dst, const int32_t* pairs, int n, void* stream) {
+    if (n == 0) return SKV_OK;
+    SKV_REQUIRE(dst && pairs && n > 0, "skv_scatter_i32: invalid arguments");
+    scatter_i32_kernel<<<cdiv(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(dst, pairs, n);
+    return check_launch("scatter_i32_kernel");
 }
 
 int skv_event_elapsed_ms(float* ms, void* start, void* stop) {
