@@ -98,14 +98,81 @@ def workload(cfg: int):
         desc = ("cfg4: Llama-3-8B geometry (32 Q / 8 KV heads, head_dim 128), batch 128, contexts "
                 "log-normal median 8192 sigma 0.6 clipped to [2048, 32768], 16-token blocks "
                 "allocated round-robin across sequences")
+    elif cfg == 5:
+        return churn_workload()
     else:
-        raise SystemExit(f"bench.py: unknown --config {cfg} (single-GPU attention configs: 2, 3, 4)")
+        raise SystemExit(f"bench.py: unknown --config {cfg} (single-GPU attention configs: 2, 3, 4, 5)")
     return dict(cfg=cfg, Hq=Hq, Hkv=Hkv, hd=hd, B=B, bs=bs, lens=lens, tables=tables,
                 total=int(total), desc=desc, seed=0x5EED0000 + cfg)
 
 
+class LifoPool:
+    """Block ids in BlockPool order: the constructor's stack holds total-1 ... 0
+    (block 0 on top) and freed ids are pushed in table order, so the last block
+    of a freed sequence is handed out first (src/memory/block_pool.cpp:72-76,
+    193-207; src/memory/page_table.cpp:152-160)."""
+
+    def __init__(self, total: int):
+        self.stack = list(range(total - 1, -1, -1))
+
+    def alloc(self) -> int:
+        if not self.stack:
+            raise RuntimeError("OOM")
+        return self.stack.pop()
+
+    def free(self, ids) -> None:
+        self.stack.extend(ids)
+
+
+CHURN_LONG, CHURN_NEW, CHURN_L, CHURN_CHUNK = 32, 4, 131072, 2048
+
+
+def churn_workload(steps: int = 64):
+    """cfg5: 64 Q / 8 KV heads, head_dim 128.  32 sequences of 131,072 tokens
+    (blocks allocated round-robin) plus 4 churn slots.  Before the first step
+    4 further long sequences are evicted, so their 4 x 8,192 blocks sit on top
+    of the free stack.  Step s: free the 4 churn sequences of step s-1, allocate
+    4 new ones and chunk-append one 2,048-token prefill chunk to each (128
+    blocks each, taken LIFO, i.e. freed blocks in reverse: non-monotone
+    tables), append one decode token to all 36 sequences, decode all 36.
+    Returns the table state for every step (precomputed on the host)."""
+    bs, Hq, Hkv, hd = 16, 64, 8, 128
+    nbl = CHURN_L // bs
+    n_live = CHURN_LONG + CHURN_NEW
+    total = (CHURN_LONG + CHURN_NEW) * nbl + 64
+    pool = LifoPool(total)
+    long_tables = np.zeros((n_live, nbl), np.int32)
+    for k in range(nbl):                      # 36 long sequences, round-robin
+        for i in range(n_live):
+            long_tables[i, k] = pool.alloc()
+    for i in range(CHURN_LONG, n_live):       # evict 4 of them
+        pool.free(long_tables[i].tolist())
+    new_blocks = CHURN_CHUNK // bs + 1        # the chunk plus the decode token's block
+    churn = np.zeros((steps, CHURN_NEW, new_blocks), np.int32)
+    prev = None
+    for st in range(steps):
+        if prev is not None:
+            for row in prev:
+                pool.free(row.tolist())
+        for j in range(CHURN_NEW):
+            churn[st, j] = [pool.alloc() for _ in range(new_blocks)]
+        prev = churn[st]
+    tables = np.full((n_live, nbl), -1, np.int32)
+    tables[:CHURN_LONG] = long_tables[:CHURN_LONG]
+    tables[CHURN_LONG:, :new_blocks] = churn[0]
+    lens = np.array([CHURN_L] * CHURN_LONG + [CHURN_CHUNK + 1] * CHURN_NEW, np.int32)
+    desc = ("cfg5: 64 Q / 8 KV heads, head_dim 128; 32 sequences at 131,072 tokens + 4 churn slots; "
+            "each step frees the previous 4 churn sequences, chunk-appends one 2,048-token prefill "
+            "chunk to 4 new ones (LIFO-reused blocks, non-monotone tables), appends one decode token "
+            "to all 36 and decodes all 36")
+    return dict(cfg=5, Hq=Hq, Hkv=Hkv, hd=hd, B=n_live, bs=bs, lens=lens, tables=tables,
+                total=int(total), desc=desc, seed=0x5EED0005, churn=churn)
+
+
 def algorithmic_bytes(w):
-    """Bytes each step must move at least once (K/V counted once per KV head)."""
+    """Bytes each step must move at least once (K/V counted once per KV head).
+    Returns (decode bytes, append bytes, flops); for cfg5 the append bytes
+    include the 4 x 2,048-token chunk append and the table patch."""
     B, Hq, Hkv, hd, bs = w["B"], w["Hq"], w["Hkv"], w["hd"], w["bs"]
     L = w["lens"].astype(np.int64)
     kv = int((2 * L * Hkv * hd * 2).sum())
@@ -113,6 +180,8 @@ def algorithmic_bytes(w):
     qo = B * Hq * hd * 2 + B * Hq * hd * 4
     decode = kv + tables + qo
     append = B * 2 * Hkv * hd * 2 * 2
+    if "churn" in w:
+        append += CHURN_NEW * CHURN_CHUNK * 2 * Hkv * hd * 2 * 2 + 2 * 4 * w["churn"][0].size
     flops = 4 * int(L.sum()) * Hq * hd
     return decode, append, flops
 
@@ -149,7 +218,31 @@ def run_gpu(w, steps: int, warmup: int):
     stream.synchronize()
     log("inputs resident; warming up")
 
+    churn = w.get("churn")
+    if churn is not None:
+        assert churn.shape[0] >= warmup + steps, "churn history shorter than the run"
+        churn_dev = skv.DeviceBuffer.from_numpy(churn)
+        n_chunk = CHURN_NEW * CHURN_CHUNK * Hkv * hd
+        chunk_k = skv.DeviceBuffer(n_chunk * 2)
+        chunk_v = skv.DeviceBuffer(n_chunk * 2)
+        skv.fill_normal_bf16(chunk_k, n_chunk, w["seed"] + 5, 0, stream.handle)
+        skv.fill_normal_bf16(chunk_v, n_chunk, w["seed"] + 6, 0, stream.handle)
+        zero_pos = skv.DeviceBuffer.from_numpy(np.zeros(CHURN_NEW, np.int32))
+        row_bytes = churn.shape[2] * 4
+        step_counter = [0]
+
     def append():
+        if churn is not None:
+            # New churn sequences: their block-table rows, then the prefill chunk.
+            st = step_counter[0]
+            step_counter[0] += 1
+            for j in range(CHURN_NEW):
+                src = churn_dev.ptr + (st * CHURN_NEW + j) * row_bytes
+                dst = tables.ptr + ((CHURN_LONG + j) * max_blocks) * 4
+                skv._check(skv.lib().skv_memcpy_d2d(dst, src, row_bytes, stream.handle))
+            skv.kv_append(chunk_k, chunk_v, skv.DTYPE_BF16, k_pool, v_pool, total,
+                          tables.ptr + CHURN_LONG * max_blocks * 4, max_blocks, zero_pos,
+                          CHURN_NEW, CHURN_CHUNK, Hkv, hd, bs, stream=stream.handle)
         skv.kv_append(k_new, v_new, skv.DTYPE_BF16, k_pool, v_pool, total, tables, max_blocks,
                       positions, B, 1, Hkv, hd, bs, stream=stream.handle)
 
@@ -257,7 +350,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=4)
+    ap.add_argument("--config", type=int, default=4, help="BASELINE.json config (2, 3, 4 or 5)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -265,7 +358,7 @@ def main() -> int:
               f"decode path shards by sequence or KV head with no exchange; the multi-GPU design is "
               f"described in DESIGN.md but not built or measured.", file=sys.stderr)
         return 2
-    w = workload(args.config)
+    w = churn_workload(args.warmup + args.steps) if args.config == 5 else workload(args.config)
     dec_bytes, app_bytes, flops = algorithmic_bytes(w)
     log(w["desc"])
     log(f"algorithmic bytes per step: decode {dec_bytes / 1e9:.3f} GB + append {app_bytes / 1e6:.3f} MB")
