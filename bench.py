@@ -345,6 +345,26 @@ def profile_traffic(workload_key: str):
     return float(m.group(1)) if m else None
 
 
+def copy_calibration(mib: int) -> int:
+    """Copy `mib` MiB with the block-gather kernel (identity table, 1 MiB
+    blocks): a plain copy of known size (reads and writes `mib` MiB once per
+    launch), to scale the FETCH_SIZE / WRITE_SIZE counters."""
+    import stratakv_amd as skv
+
+    skv.require_gpu()
+    block = 1 << 19  # bf16 elements = 1 MiB
+    src = skv.DeviceBuffer(mib << 20)
+    dst = skv.DeviceBuffer(mib << 20)
+    skv.fill_normal_bf16(src, mib * block, 1)
+    table = skv.DeviceBuffer.from_numpy(np.arange(mib, dtype=np.int32))
+    for _ in range(5):
+        skv.gather_blocks(src, mib, table, mib, block, dst)
+    skv.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": mib << 20, "bytes_written": mib << 20,
+                      "launches": 5}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -352,7 +372,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=4, help="BASELINE.json config (2, 3, 4 or 5)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
+                    help="only run a plain copy of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}). The paged "
               f"decode path shards by sequence or KV head with no exchange; the multi-GPU design is "
