@@ -18,7 +18,7 @@ configs.
 
 Output: one JSON line on stdout.  value = algorithmic bytes of a whole step
 (append + decode) / device time per step, in GB/s.  roofline = the decode
-call (planner + attention + merge kernels) against 8 TB/s.  cpu_baseline =
+call (attention + merge kernels) against 8 TB/s.  cpu_baseline =
 the oracle's restatement of the reference CPU attention timed on this host
 on a bounded sample of sequences of the same workload.
 """
@@ -419,7 +419,7 @@ def main() -> int:
         "decode_ms": round(g["decode_ms"], 5),
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged decode (planner + attention + merge launches of skv_paged_decode)",
+            "kernel": "paged decode (attention + merge launches of skv_paged_decode)",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -125,4 +125,19 @@ __device__ __forceinline__ float fast_exp2(float x) {
     return __builtin_amdgcn_exp2f(x);
 }
 
+// LDS hand-off between the lanes of ONE wavefront (not between wavefronts).
+// The LDS instructions of a wavefront execute in issue order, so a ds_read
+// issued after a ds_write of the same wavefront sees it without s_barrier; the
+// fences only stop the compiler from moving LDS accesses across this point.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Value of lane `src` (a compile-time or wave-uniform index), as a scalar.
+__device__ __forceinline__ float lane_value(float x, int src) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), src));
+}
+
 }  // namespace skv

@@ -7,12 +7,14 @@
 // all G = Hq/Hkv query heads of its group, and it accumulates P.V in global
 // memory.  Here the work is organised for CDNA4:
 //
-// * Work = the (sequence, kv head, block) triples, flattened.  A planner kernel
-//   splits them evenly over exactly as many persistent wavefronts as the GPU
-//   holds at once ("stream-K"): no tail of idle CUs, and a wavefront whose
-//   range covers a whole (sequence, kv head) segment writes the final output;
-//   only segments cut by a range boundary leave partial (max, sum, acc)
-//   triples for the merge kernel (log-sum-exp rescale).
+// * Work = the (sequence, kv head, block) triples, flattened, and split evenly
+//   over a fixed set of persistent wavefronts ("stream-K"; each wavefront
+//   derives the split itself from a scan of the context lengths): no tail of
+//   idle CUs, and a wavefront whose range covers a whole (sequence, kv head)
+//   segment writes the final output; only segments cut by a range boundary
+//   leave partial (max, sum, acc) triples for the merge kernel (log-sum-exp
+//   rescale).  The wavefronts of one workgroup take neighbouring kv heads of
+//   the same range, so one CU reads adjacent slices of every block row.
 // * A wavefront serves all G query heads of a kv head from one read of K/V.
 //   q.k^T runs on the matrix cores: v_mfma_f32_16x16x32_bf16 with the 16 tokens
 //   of a block as rows and the G heads (zero-padded to 16) as columns; fp32
@@ -22,8 +24,10 @@
 //   (fully coalesced).  K goes through a per-wave LDS tile, stored with its
 //   16-byte chunks XOR-swizzled by row, and comes back in the MFMA operand
 //   layout (one 16-byte chunk of one token per lane) without bank conflicts.
-//   The next block is prefetched into registers while the current one is
-//   computed.  K/V are read once per step, so the loads carry the non-temporal
+//   Each wavefront keeps a ring of NBUF blocks in registers: while one is
+//   computed the next NBUF - 1 are in flight, and the block addresses come
+//   from table entries preloaded 64 at a time (no dependent table load per
+//   block).  K/V are read once per step, so the loads carry the non-temporal
 //   hint (streamed through L2 without displacing reused lines), which on
 //   MI355X raises the achievable rate of this pattern by ~10 %.
 // * Online softmax in the exp2 domain with lazy rescaling: the running max is
@@ -99,25 +103,27 @@ struct WorkSplit {
 
 __device__ WorkSplit build_split(const DecodeParams& p, int* P_s) {
     const int lane = threadIdx.x;
-    int carry = 0;
-    for (int b0 = 0; b0 < p.B; b0 += 64) {
-        const int b = b0 + lane;
-        int v = b < p.B ? seq_blocks(p, b) : 0;
+    if (lane < 64) {  // wavefront 0 of the workgroup scans
+        int carry = 0;
+        for (int b0 = 0; b0 < p.B; b0 += 64) {
+            const int b = b0 + lane;
+            int v = b < p.B ? seq_blocks(p, b) : 0;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int u = __shfl_up(v, o, 64);
-            if (lane >= o) v += u;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int u = __shfl_up(v, o, 64);
+                if (lane >= o) v += u;
+            }
+            if (b < p.B) P_s[b + 1] = carry + v;
+            carry += __shfl(v, 63, 64);
         }
-        if (b < p.B) P_s[b + 1] = carry + v;
-        carry += __shfl(v, 63, 64);
+        if (lane == 0) P_s[0] = 0;
     }
-    if (lane == 0) P_s[0] = 0;
     __syncthreads();
     WorkSplit ws;
-    ws.total = carry;
-    ws.per = std::max(p.min_per, carry > 0 ? cdiv(carry, p.ranges) : 1);
-    ws.used = carry > 0 ? cdiv(carry, ws.per) : 0;
-    if (blockIdx.x == 0) {  // publish for the merge kernel
+    ws.total = P_s[p.B];
+    ws.per = std::max(p.min_per, ws.total > 0 ? cdiv(ws.total, p.ranges) : 1);
+    ws.used = ws.total > 0 ? cdiv(ws.total, ws.per) : 0;
+    if (blockIdx.x == 0 && lane < 64) {  // publish for the merge kernel
         for (int i = lane; i <= p.B; i += 64) p.plan[3 + i] = P_s[i];
         if (lane == 0) {
             p.plan[0] = ws.total;
@@ -152,9 +158,19 @@ __device__ __forceinline__ int64_t partial_row(int range, bool tail, int Hseg, i
 // LDS tile: row R, chunk c stored at R*CH + (c ^ swz(R)), swz(R) = R for
 //   CH = 16 and (R >> 1) & 7 for CH = 8, so the 16 lanes reading one chunk
 //   column of 16 rows hit 16 distinct bank groups.
+// Each wavefront owns its LDS tiles and synchronises only with itself
+// (wave_lds_sync); the WPW wavefronts of a workgroup meet once, at the split.
 // ---------------------------------------------------------------------------
-template <int HD, int G, bool QF32>
-__global__ __launch_bounds__(64, (G <= 4 ? 3 : G == 8 ? 2 : 1)) void decode_mfma_kernel(DecodeParams p) {
+// Wavefronts per SIMD the register budget of decode_mfma_kernel allows: about
+// G*8 accumulators + NBUF * HD/4 buffer registers + 70 for the rest.
+constexpr int mfma_occupancy(int HD, int G, int NBUF) {
+    return G * 8 + NBUF * HD / 4 + 70 <= 128 ? 4
+         : G * 8 + NBUF * HD / 4 + 70 <= 168 ? 3
+         : G * 8 + NBUF * HD / 4 + 70 <= 256 ? 2 : 1;
+}
+
+template <int HD, int G, bool QF32, int WPW, int NBUF>
+__global__ __launch_bounds__(64 * WPW, mfma_occupancy(HD, G, NBUF)) void decode_mfma_kernel(DecodeParams p) {
     constexpr int BS = 16;
     constexpr int CH = HD / 8;      // 16-byte chunks per row
     constexpr int RPI = 64 / CH;    // rows per coalesced load instruction
@@ -164,17 +180,23 @@ __global__ __launch_bounds__(64, (G <= 4 ? 3 : G == 8 ? 2 : 1)) void decode_mfma
     static_assert(CH * RPI == 64 && RPI * TPL == BS && NMF * 4 == CH, "lane layout");
     static_assert(G >= 1 && G <= 16, "group size");
 
-    extern __shared__ int P_s[];    // [B + 1] block prefix
-    __shared__ u32x4_t k_s[BS * CH];  // one block of K for this kv head, swizzled
-    __shared__ float p_s[BS * 16];  // probabilities [token][head]
-    __shared__ float h_s[2][16];    // per-head broadcast: rescale factor / (sum, max)
+    // Per-wavefront LDS: the WPW wavefronts of a workgroup serve the same
+    // range for WPW consecutive kv heads and only meet at the work split.
+    extern __shared__ int P_s[];            // [B + 1] block prefix
+    __shared__ u32x4_t k_all[WPW][BS * CH];  // one block of K for this kv head, swizzled
+    __shared__ float p_all[WPW][BS * 16];    // probabilities [token][head]
+    __shared__ float h_all[WPW][2][16];      // per-head (sum, max) at the end of a segment
 
-    const int lane = threadIdx.x;
+    const int wv = WPW == 1 ? 0 : __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    u32x4_t* k_s = k_all[wv];
+    float* p_s = p_all[wv];
+    float (*h_s)[16] = h_all[wv];
     const int r = lane / CH, c = lane % CH;
     const int t = lane & 15, j = lane >> 4;
     auto swz = [](int row) { return CH == 16 ? row : ((row >> 1) & 7); };
     const int Hkv = p.Hkv;
-    const int w = blockIdx.x;
+    const int w = blockIdx.x * WPW + wv;    // Hkv % WPW == 0: one range per workgroup
     const int kvh = w % Hkv;
     const int range = w / Hkv;
 
@@ -237,9 +259,29 @@ __global__ __launch_bounds__(64, (G <= 4 ? 3 : G == 8 ? 2 : 1)) void decode_mfma
 
         const int64_t lane_off = static_cast<int64_t>(r) * row_stride + static_cast<int64_t>(kvh) * HD + c * 8;
 
+        // Table entries of the segment, 64 at a time: lane i holds entry tb + i
+        // (tv) and tb + 64 + i (tvn, loaded one chunk ahead), so the block
+        // addresses never wait on a dependent table load.
+        auto table_entry = [&](int k) -> int { return table[k < kb1 ? k : kb1 - 1]; };
+        int tb = k0;
+        int tv = table_entry(tb + lane);
+        int tvn = table_entry(tb + 64 + lane);
+
+        // Loads of block kb into one register buffer.  Every call issues the
+        // same loads (a position past the segment reloads its last block, an
+        // entry outside the pool reads block 0), so the compiler's wait counts
+        // stay exact; the return value says whether the block is real.
         auto issue = [&](int kb, u32x4_t (&kk)[TPL], u32x4_t (&vv)[TPL]) -> bool {
-            const int64_t pb = table[kb];
-            if (pb < 0 || pb >= p.total_blocks) return false;
+            const bool in_seg = kb < kb1;
+            kb = in_seg ? kb : kb1 - 1;
+            if (kb - tb >= 64) {  // blocks are issued in order: advance one chunk
+                tb += 64;
+                tv = tvn;
+                tvn = table_entry(tb + 64 + lane);
+            }
+            const int64_t e = __builtin_amdgcn_readlane(tv, kb - tb);
+            const bool valid = in_seg && e >= 0 && e < p.total_blocks;
+            const int64_t pb = e >= 0 && e < p.total_blocks ? e : 0;
             const int64_t base = pb * BS * row_stride + lane_off;
 #pragma unroll
             for (int i = 0; i < TPL; ++i) {
@@ -247,96 +289,96 @@ __global__ __launch_bounds__(64, (G <= 4 ? 3 : G == 8 ? 2 : 1)) void decode_mfma
                 kk[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p.k + off));
                 vv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p.v + off));
             }
-            return true;
+            return valid;
         };
 
-        u32x4_t kcur[TPL], vcur[TPL];
-        bool ok = issue(k0, kcur, vcur);
-        for (int kb = k0; kb < kb1; ++kb) {
-            u32x4_t knext[TPL], vnext[TPL];
-            bool ok_next = false;
-            if (kb + 1 < kb1) ok_next = issue(kb + 1, knext, vnext);
-            if (ok) {
-                // ---- K through the LDS tile into the MFMA operand layout
-#pragma unroll
-                for (int i = 0; i < TPL; ++i) {
-                    const int row = i * RPI + r;
-                    k_s[row * CH + (c ^ swz(row))] = kcur[i];
-                }
-                __syncthreads();
-                // ---- scores S[token 4j+i][head t] on the matrix cores
-                f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int cc = 0; cc < NMF; ++cc) {
-                    const bf16x8_t a = __builtin_bit_cast(bf16x8_t, k_s[t * CH + ((4 * cc + j) ^ swz(t))]);
-#pragma unroll
-                    for (int qp = 0; qp < QP; ++qp)
-                        sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qop[qp][cc], sacc, 0, 0, 0);
-                }
-                const int tok = kb * BS + 4 * j;
-                float s[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) s[i] = tok + i < Leff ? sacc[i] * p.qscale : -INFINITY;
-                float mb = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-                mb = fmaxf(mb, shfl_xor_f(mb, 16));
-                mb = fmaxf(mb, shfl_xor_f(mb, 32));
-
-                // ---- lazy rescale (wave-uniform branch)
-                const bool need = mb > m + kLazyRescale;
-                if (__any(need)) {
-                    const float mn = need ? mb : m;
-                    // Before the first block m = -inf and acc, sum are 0: factor 0.
-                    const float alpha = m == -INFINITY ? 0.0f : fast_exp2(m - mn);
-                    m = mn;
-                    lpart *= alpha;
-                    if (j == 0) h_s[0][t] = alpha;
-                    __syncthreads();
-#pragma unroll
-                    for (int g = 0; g < G; ++g) {
-                        const float a = h_s[0][g];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) acc[g][e] *= a;
-                    }
-                }
-                const float ms = m == -INFINITY ? 0.0f : m;
-                float pr[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(s[i] - ms);
-                lpart += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-                if (t < G) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) p_s[(4 * j + i) * 16 + t] = pr[i];
-                }
-                __syncthreads();
-
-                // ---- P.V on the VALU (coalesced V layout)
-                const bool tail = kb * BS + BS > Leff;
-#pragma unroll
-                for (int i = 0; i < TPL; ++i) {
-                    const int row = i * RPI + r;
-                    u32x4_t vw = vcur[i];
-                    if (tail && kb * BS + row >= Leff) vw = u32x4_t{0u, 0u, 0u, 0u};
-                    float vf[8];
-                    vf[0] = bf16_lo(vw.x); vf[1] = bf16_hi(vw.x);
-                    vf[2] = bf16_lo(vw.y); vf[3] = bf16_hi(vw.y);
-                    vf[4] = bf16_lo(vw.z); vf[5] = bf16_hi(vw.z);
-                    vf[6] = bf16_lo(vw.w); vf[7] = bf16_hi(vw.w);
-                    float pv[G];
-#pragma unroll
-                    for (int g = 0; g < G; ++g) pv[g] = p_s[row * 16 + g];
-#pragma unroll
-                    for (int g = 0; g < G; ++g)
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pv[g], vf[e], acc[g][e]);
-                }
-                __syncthreads();
-            }
+        auto consume = [&](int kb, const u32x4_t (&kk)[TPL], const u32x4_t (&vv)[TPL]) {
+            // ---- K through the LDS tile into the MFMA operand layout
 #pragma unroll
             for (int i = 0; i < TPL; ++i) {
-                kcur[i] = knext[i];
-                vcur[i] = vnext[i];
+                const int row = i * RPI + r;
+                k_s[row * CH + (c ^ swz(row))] = kk[i];
             }
-            ok = ok_next;
+            wave_lds_sync();
+            // ---- scores S[token 4j+i][head t] on the matrix cores
+            f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int cc = 0; cc < NMF; ++cc) {
+                const bf16x8_t a = __builtin_bit_cast(bf16x8_t, k_s[t * CH + ((4 * cc + j) ^ swz(t))]);
+#pragma unroll
+                for (int qp = 0; qp < QP; ++qp)
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qop[qp][cc], sacc, 0, 0, 0);
+            }
+            const int tok = kb * BS + 4 * j;
+            float s[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[i] = tok + i < Leff ? sacc[i] * p.qscale : -INFINITY;
+            float mb = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+            mb = fmaxf(mb, shfl_xor_f(mb, 16));
+            mb = fmaxf(mb, shfl_xor_f(mb, 32));
+
+            // ---- lazy rescale (wave-uniform branch)
+            const bool need = mb > m + kLazyRescale;
+            if (__any(need)) {
+                const float mn = need ? mb : m;
+                // Before the first block m = -inf and acc, sum are 0: factor 0.
+                const float alpha = m == -INFINITY ? 0.0f : fast_exp2(m - mn);
+                m = mn;
+                lpart *= alpha;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float a = lane_value(alpha, g);  // lane g holds head g
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[g][e] *= a;
+                }
+            }
+            const float ms = m == -INFINITY ? 0.0f : m;
+            float pr[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(s[i] - ms);
+            lpart += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+            if (t < G) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) p_s[(4 * j + i) * 16 + t] = pr[i];
+            }
+            wave_lds_sync();
+
+            // ---- P.V on the VALU (coalesced V layout)
+            const bool tail = kb * BS + BS > Leff;
+#pragma unroll
+            for (int i = 0; i < TPL; ++i) {
+                const int row = i * RPI + r;
+                u32x4_t vw = vv[i];
+                if (tail && kb * BS + row >= Leff) vw = u32x4_t{0u, 0u, 0u, 0u};
+                float vf[8];
+                vf[0] = bf16_lo(vw.x); vf[1] = bf16_hi(vw.x);
+                vf[2] = bf16_lo(vw.y); vf[3] = bf16_hi(vw.y);
+                vf[4] = bf16_lo(vw.z); vf[5] = bf16_hi(vw.z);
+                vf[6] = bf16_lo(vw.w); vf[7] = bf16_hi(vw.w);
+                float pv[G];
+#pragma unroll
+                for (int g = 0; g < G; ++g) pv[g] = p_s[row * 16 + g];
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pv[g], vf[e], acc[g][e]);
+            }
+            wave_lds_sync();
+        };
+
+        // Ring of NBUF register buffers, unrolled so that buffer u always
+        // holds block kb + u: while one block is consumed the next NBUF - 1
+        // are in flight, and no register copy forces an early wait.
+        u32x4_t kbuf[NBUF][TPL], vbuf[NBUF][TPL];
+        bool okb[NBUF];
+#pragma unroll
+        for (int u = 0; u < NBUF; ++u) okb[u] = issue(k0 + u, kbuf[u], vbuf[u]);
+        for (int kb = k0; kb < kb1; kb += NBUF) {
+#pragma unroll
+            for (int u = 0; u < NBUF; ++u) {
+                if (okb[u]) consume(kb + u, kbuf[u], vbuf[u]);
+                okb[u] = issue(kb + u + NBUF, kbuf[u], vbuf[u]);
+            }
         }
 
         // ---- finalise the segment: combine row groups, broadcast (sum, max)
@@ -352,7 +394,7 @@ __global__ __launch_bounds__(64, (G <= 4 ? 3 : G == 8 ? 2 : 1)) void decode_mfma
             h_s[0][t] = ltot;
             h_s[1][t] = m;
         }
-        __syncthreads();
+        wave_lds_sync();
         const bool final_out = seg_lo >= range_lo && seg_hi <= range_hi;
         const int64_t prow = partial_row(range, seg_lo > range_lo, Hkv, kvh);
         if (r == 0) {
@@ -377,7 +419,7 @@ __global__ __launch_bounds__(64, (G <= 4 ? 3 : G == 8 ? 2 : 1)) void decode_mfma
                 }
             }
         }
-        __syncthreads();
+        wave_lds_sync();
 
         pos = stop;
         if (pos >= end) break;
@@ -669,10 +711,11 @@ WorkspaceLayout workspace_layout(int B, int Hq, int Hkv, int HD) {
     return w;
 }
 
-// Wavefronts of `kernel` resident on the device at once (with `lds` bytes of
-// dynamic LDS each), cached per device, kernel and LDS size.
+// Wavefronts of `kernel` resident on the device at once, in workgroups of
+// `wpw` wavefronts with `lds` bytes of dynamic LDS each, at most
+// `max_per_simd` per SIMD (0 = no cap); cached per device, kernel and LDS size.
 template <typename K>
-int resident_waves(K kernel, size_t lds) {
+int resident_waves(K kernel, int wpw, size_t lds, int max_per_simd) {
     static std::mutex mu;
     static std::unordered_map<std::string, int> cache;
     int dev = 0;
@@ -685,31 +728,55 @@ int resident_waves(K kernel, size_t lds) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64, lds) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64 * wpw, lds) != hipSuccess ||
         per_cu <= 0)
-        per_cu = 4;
-    const int waves = std::min(kMaxWaves, cus * per_cu);
+        per_cu = std::max(1, 4 / wpw);
+    int waves = std::min(kMaxWaves, cus * per_cu * wpw);
+    if (max_per_simd > 0) waves = std::min(waves, std::max(wpw, cus * 4 * max_per_simd));
     cache.emplace(key, waves);
     return waves;
 }
 
-// Attention kernel over `ranges * Hseg` persistent wavefronts, then the merge.
+// Attention kernel over `ranges * Hseg` persistent wavefronts (workgroups of
+// `wpw` of them, wpw dividing Hseg), then the merge.
 template <typename K>
-int launch_pair(K kern, DecodeParams p, hipStream_t s, const char* name) {
+int launch_pair(K kern, int wpw, int max_per_simd, DecodeParams p, hipStream_t s, const char* name) {
     const size_t lds = sizeof(int) * (static_cast<size_t>(p.B) + 1);
-    const int waves = resident_waves(kern, lds);
+    const int waves = resident_waves(kern, wpw, lds, max_per_simd);
     p.ranges = std::max(1, waves / p.Hseg);
-    kern<<<static_cast<unsigned>(p.ranges) * p.Hseg, 64, lds, s>>>(p);
+    const unsigned groups = static_cast<unsigned>(p.ranges) * (p.Hseg / wpw);
+    kern<<<groups, 64 * wpw, lds, s>>>(p);
     if (int rc = check_launch(name)) return rc;
     decode_merge_kernel<<<static_cast<unsigned>(p.B) * p.Hseg, 256, 0, s>>>(p);
     return check_launch("decode_merge_kernel");
 }
 
+// Wavefronts per workgroup of the MFMA kernel: neighbouring kv heads of the
+// same blocks read side by side from one CU (adjacent 256-byte row slices)
+// stream faster than when their wavefronts are spread over CUs.
+// Launch shape of the MFMA kernel, chosen by measurement on MI355X:
+// * 4 wavefronts per workgroup (when Hkv allows): neighbouring kv heads of
+//   the same blocks are read side by side from one CU, adjacent 256-byte
+//   slices of each row, which streams ~5 % faster than spreading them;
+// * a ring of NBUF blocks in flight per wavefront and few wavefronts per
+//   SIMD: about 16-24 KiB of K/V requested per SIMD (head_dim 128: 2 blocks
+//   of 8 KiB, 1 wavefront per SIMD; head_dim 64: 3 blocks of 4 KiB, 2 per
+//   SIMD).  More requests in flight than that lowers the achieved rate.
+template <int HD, int G, bool QF32>
+int launch_mfma_shape(const DecodeParams& p, hipStream_t s) {
+    constexpr int NB = HD == 64 ? 3 : 2;
+    constexpr int PER_SIMD = HD == 64 ? 2 : 1;
+    const char* name = "decode_mfma_kernel";
+    if (p.Hkv % 4 == 0) return launch_pair(decode_mfma_kernel<HD, G, QF32, 4, NB>, 4, PER_SIMD, p, s, name);
+    if (p.Hkv % 2 == 0) return launch_pair(decode_mfma_kernel<HD, G, QF32, 2, NB>, 2, PER_SIMD, p, s, name);
+    return launch_pair(decode_mfma_kernel<HD, G, QF32, 1, NB>, 1, PER_SIMD, p, s, name);
+}
+
 template <bool QF32>
 int launch_mfma(const DecodeParams& p, hipStream_t s) {
     const int G = p.Hq / p.Hkv;
-#define SKV_MFMA(HD_, G_)                                                          \
-    if (p.HD == HD_ && G == G_) return launch_pair(decode_mfma_kernel<HD_, G_, QF32>, p, s, "decode_mfma_kernel");
+#define SKV_MFMA(HD_, G_) \
+    if (p.HD == HD_ && G == G_) return launch_mfma_shape<HD_, G_, QF32>(p, s);
     SKV_MFMA(64, 1) SKV_MFMA(64, 2) SKV_MFMA(64, 4) SKV_MFMA(64, 8) SKV_MFMA(64, 16)
     SKV_MFMA(128, 1) SKV_MFMA(128, 2) SKV_MFMA(128, 4) SKV_MFMA(128, 8) SKV_MFMA(128, 16)
 #undef SKV_MFMA
@@ -737,8 +804,8 @@ int run_decode_chunk(DecodeParams p, int q_dtype, char* ws, const WorkspaceLayou
     p.Hseg = p.Hq;
     p.NH = 1;
     p.min_per = std::max(1, cdiv(64, p.bs));
-    return q_dtype == SKV_DTYPE_FP32 ? launch_pair(decode_generic_kernel<true>, p, s, "decode_generic_kernel")
-                                     : launch_pair(decode_generic_kernel<false>, p, s, "decode_generic_kernel");
+    return q_dtype == SKV_DTYPE_FP32 ? launch_pair(decode_generic_kernel<true>, 1, 0, p, s, "decode_generic_kernel")
+                                     : launch_pair(decode_generic_kernel<false>, 1, 0, p, s, "decode_generic_kernel");
 }
 
 // Batches larger than kMaxBatchPerLaunch run as consecutive launches on the
