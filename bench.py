@@ -2,25 +2,28 @@
 """Benchmark of the paged KV-cache hot path on one MI355X.
 
 A step is one decode step of one layer over a batch of sequences: the KV
-append of one new token per sequence (skv_kv_append) followed by paged decode
-attention over every sequence's whole context (skv_paged_decode).  Inputs are
-synthetic and already resident in HBM when timing starts; the step rewrites
-each sequence's last slot (context stays the same from step to step, as the
-reference's forward_into with append_tokens=false does), so every timed step
-does identical work.
+append of one new token per sequence and paged decode attention over every
+sequence's whole context, in one fused call (skv_paged_decode_append; with
+--separate: skv_kv_append then skv_paged_decode).  Inputs are synthetic and
+already resident in HBM when timing starts; the step rewrites each sequence's
+last slot (context stays the same from step to step, as the reference's
+forward_into with append_tokens=false does), so every timed step does
+identical work.  Config 5 adds the churn work of its definition before the
+decode step (block-table rows of the 4 new sequences, their 2,048-token
+prefill chunks appended through the tables).
 
 Default workload: config 4 of BASELINE.json (Llama-3-8B geometry: 32 Q heads,
 8 KV heads, head_dim 128, batch 128, context lengths log-normal with median
 8192 and sigma 0.6 clipped to [2048, 32768], 16-token blocks allocated
 round-robin across sequences), the configuration the >= 70 % of HBM peak
-target is quoted on.  --config 2 / 3 select the other single-GPU attention
-configs.
+target is quoted on.  --config 2 / 3 / 5 select the other single-GPU
+attention configs.
 
 Output: one JSON line on stdout.  value = algorithmic bytes of a whole step
-(append + decode) / device time per step, in GB/s.  roofline = the decode
-call (attention + merge kernels) against 8 TB/s.  cpu_baseline =
-the oracle's restatement of the reference CPU attention timed on this host
-on a bounded sample of sequences of the same workload.
+/ device time per step, in GB/s.  roofline = the decode call (fused append +
+attention kernel, then the merge kernel) against 8 TB/s.  cpu_baseline = the
+oracle's restatement of the reference CPU attention timed on this host on a
+bounded sample of sequences of the same workload.
 """
 from __future__ import annotations
 
@@ -179,17 +182,23 @@ def algorithmic_bytes(w):
     tables = int((4 * np.ceil(L / bs)).sum()) + 4 * B
     qo = B * Hq * hd * 2 + B * Hq * hd * 4
     decode = kv + tables + qo
-    append = B * 2 * Hkv * hd * 2 * 2
+    token_append = B * 2 * Hkv * hd * 2 * 2
+    churn_append = 0
     if "churn" in w:
-        append += CHURN_NEW * CHURN_CHUNK * 2 * Hkv * hd * 2 * 2 + 2 * 4 * w["churn"][0].size
+        churn_append = CHURN_NEW * CHURN_CHUNK * 2 * Hkv * hd * 2 * 2 + 2 * 4 * w["churn"][0].size
     flops = 4 * int(L.sum()) * Hq * hd
-    return decode, append, flops
+    return decode, token_append, churn_append, flops
 
 
 # ---------------------------------------------------------------------------
 # GPU run
 # ---------------------------------------------------------------------------
-def run_gpu(w, steps: int, warmup: int):
+def run_gpu(w, steps: int, warmup: int, fused: bool = True):
+    """Times `steps` decode steps.  A step is [pre] + [main]: with fused=True,
+    pre = the cfg5 churn work (table patch + prefill-chunk append; nothing for
+    the other configs) and main = one skv_paged_decode_append call (decode-token
+    append + attention); with fused=False, pre also holds the decode-token
+    skv_kv_append and main is skv_paged_decode alone."""
     import stratakv_amd as skv
 
     skv.require_gpu()
@@ -231,7 +240,7 @@ def run_gpu(w, steps: int, warmup: int):
         row_bytes = churn.shape[2] * 4
         step_counter = [0]
 
-    def append():
+    def pre():
         if churn is not None:
             # New churn sequences: their block-table rows, then the prefill chunk.
             st = step_counter[0]
@@ -243,39 +252,50 @@ def run_gpu(w, steps: int, warmup: int):
             skv.kv_append(chunk_k, chunk_v, skv.DTYPE_BF16, k_pool, v_pool, total,
                           tables.ptr + CHURN_LONG * max_blocks * 4, max_blocks, zero_pos,
                           CHURN_NEW, CHURN_CHUNK, Hkv, hd, bs, stream=stream.handle)
-        skv.kv_append(k_new, v_new, skv.DTYPE_BF16, k_pool, v_pool, total, tables, max_blocks,
-                      positions, B, 1, Hkv, hd, bs, stream=stream.handle)
+        if not fused:
+            skv.kv_append(k_new, v_new, skv.DTYPE_BF16, k_pool, v_pool, total, tables, max_blocks,
+                          positions, B, 1, Hkv, hd, bs, stream=stream.handle)
 
-    def decode():
-        skv.paged_decode(q, skv.DTYPE_BF16, k_pool, v_pool, total, tables, max_blocks, lens, B,
-                         Hq, Hkv, hd, bs, scale, out, ws, wsb, stream=stream.handle)
+    def main():
+        if fused:
+            skv.paged_decode_append(q, skv.DTYPE_BF16, k_new, v_new, skv.DTYPE_BF16, k_pool, v_pool,
+                                    total, tables, max_blocks, lens, B, Hq, Hkv, hd, bs, scale, out,
+                                    ws, wsb, stream=stream.handle)
+        else:
+            skv.paged_decode(q, skv.DTYPE_BF16, k_pool, v_pool, total, tables, max_blocks, lens, B,
+                             Hq, Hkv, hd, bs, scale, out, ws, wsb, stream=stream.handle)
 
     for _ in range(warmup):
-        append()
-        decode()
+        pre()
+        main()
     skv.synchronize()
     log(f"warmup done ({warmup} steps); timing {steps} steps")
 
-    # Events on the launch stream: e[3i] before the append, e[3i+1] between
-    # append and decode, e[3i+2] after the decode of step i.
-    ev = [skv.Event() for _ in range(3 * steps)]
+    # Events on the launch stream, per step i: a before pre, b between pre and
+    # main, c after main.  When pre is empty (fused step, no churn) a is b: an
+    # extra event between two back-to-back records would itself cost ~5 us.
+    has_pre = churn is not None or not fused
+    ev_a = [skv.Event() for _ in range(steps)]
+    ev_b = [skv.Event() for _ in range(steps)] if has_pre else ev_a
+    ev_c = [skv.Event() for _ in range(steps)]
     skv.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        ev[3 * i].record(stream.handle)
-        append()
-        ev[3 * i + 1].record(stream.handle)
-        decode()
-        ev[3 * i + 2].record(stream.handle)
+        ev_a[i].record(stream.handle)
+        if has_pre:
+            pre()
+            ev_b[i].record(stream.handle)
+        main()
+        ev_c[i].record(stream.handle)
     skv.synchronize()
     wall = time.perf_counter() - t0
-    append_ms = [ev[3 * i].elapsed_ms(ev[3 * i + 1]) for i in range(steps)]
-    decode_ms = [ev[3 * i + 1].elapsed_ms(ev[3 * i + 2]) for i in range(steps)]
-    total_ms = ev[0].elapsed_ms(ev[3 * steps - 1])
+    pre_ms = [ev_a[i].elapsed_ms(ev_b[i]) if has_pre else 0.0 for i in range(steps)]
+    main_ms = [ev_b[i].elapsed_ms(ev_c[i]) for i in range(steps)]
+    total_ms = ev_a[0].elapsed_ms(ev_c[steps - 1])
     log(f"timed: device {total_ms:.3f} ms, host wall {wall * 1e3:.3f} ms")
-    return dict(ms_per_step=total_ms / steps, append_ms=float(np.mean(append_ms)),
-                decode_ms=float(np.mean(decode_ms)), decode_ms_median=float(np.median(decode_ms)),
-                decode_ms_min=float(np.min(decode_ms)), wall_ms_per_step=wall * 1e3 / steps)
+    return dict(ms_per_step=total_ms / steps, pre_ms=float(np.mean(pre_ms)),
+                main_ms=float(np.mean(main_ms)), main_ms_median=float(np.median(main_ms)),
+                main_ms_min=float(np.min(main_ms)), wall_ms_per_step=wall * 1e3 / steps)
 
 
 # ---------------------------------------------------------------------------
@@ -372,6 +392,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=4, help="BASELINE.json config (2, 3, 4 or 5)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--separate", action="store_true",
+                    help="time the decode-token append and the decode as two calls "
+                         "(skv_kv_append + skv_paged_decode) instead of the fused call")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                     help="only run a plain copy of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -383,14 +406,17 @@ def main() -> int:
               f"described in DESIGN.md but not built or measured.", file=sys.stderr)
         return 2
     w = churn_workload(args.warmup + args.steps) if args.config == 5 else workload(args.config)
-    dec_bytes, app_bytes, flops = algorithmic_bytes(w)
+    dec_bytes, tok_bytes, churn_bytes, flops = algorithmic_bytes(w)
     log(w["desc"])
-    log(f"algorithmic bytes per step: decode {dec_bytes / 1e9:.3f} GB + append {app_bytes / 1e6:.3f} MB")
-    g = run_gpu(w, args.steps, args.warmup)
+    log(f"algorithmic bytes per step: decode {dec_bytes / 1e9:.3f} GB + decode-token append "
+        f"{tok_bytes / 1e6:.3f} MB + churn {churn_bytes / 1e6:.3f} MB")
+    fused = not args.separate
+    g = run_gpu(w, args.steps, args.warmup, fused=fused)
     step_s = g["ms_per_step"] / 1e3
-    value = (dec_bytes + app_bytes) / step_s / 1e9
-    achieved = dec_bytes / (g["decode_ms"] / 1e3) / 1e9
-    key = f"cfg{args.config}"
+    value = (dec_bytes + tok_bytes + churn_bytes) / step_s / 1e9
+    main_bytes = dec_bytes + (tok_bytes if fused else 0)
+    achieved = main_bytes / (g["main_ms"] / 1e3) / 1e9
+    key = f"cfg{args.config}" + ("" if fused else "_separate")
     traffic = profile_traffic(key)
     line = {
         "metric": METRIC,
@@ -415,17 +441,22 @@ def main() -> int:
         },
         "tokens_per_s": round(w["B"] / step_s, 1),
         "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
-        "append_ms": round(g["append_ms"], 5),
-        "decode_ms": round(g["decode_ms"], 5),
+        "step": ("fused: skv_paged_decode_append (decode-token append + attention + merge)"
+                 if fused else "separate: skv_kv_append, then skv_paged_decode")
+                + ("; before it the churn table patch and 4 x 2,048-token chunk append"
+                   if "churn" in w else ""),
+        "pre_ms": round(g["pre_ms"], 5),
+        "decode_ms": round(g["main_ms"], 5),
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged decode (attention + merge launches of skv_paged_decode)",
+            "kernel": ("skv_paged_decode_append: fused append + attention kernel, then merge"
+                       if fused else "skv_paged_decode: attention kernel, then merge"),
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "algorithmic_bytes": dec_bytes,
+            "algorithmic_bytes": main_bytes,
             "flops": flops,
         },
     }

@@ -154,6 +154,28 @@ int skv_paged_decode(const void* q, int q_dtype,
                      int block_size, float scale, float* out,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* Fused decode step: appends each sequence's new token at position
+ * context_lens[b] - 1 and decodes over context_lens[b] tokens, in one launch.
+ * k_new / v_new: [num_seqs][num_kv_heads][head_dim] in kv_dtype (bf16 bits are
+ * stored as given, fp32 is rounded to nearest-even like skv_kv_append).  The
+ * pools and `out` end up bit-identical to skv_kv_append(k_new, v_new, ...,
+ * positions = context_lens - 1, tokens_per_seq = 1) followed by
+ * skv_paged_decode(...) on the same stream; the same positions are skipped
+ * (beyond the table, or a block outside the pool).  Workspace as for
+ * skv_paged_decode.
+ * Replaces: the per-token K/V copy followed by paged_attention_decode_cuda in
+ * forward_into (src/models/transformer_block.cpp:484-509 then 511-518), for a
+ * batch of sequences. */
+int skv_paged_decode_append(const void* q, int q_dtype,
+                            const void* k_new, const void* v_new, int kv_dtype,
+                            uint16_t* k_pool, uint16_t* v_pool,
+                            int64_t total_blocks,
+                            const int32_t* block_tables, int max_blocks_per_seq,
+                            const int32_t* context_lens, int num_seqs,
+                            int num_q_heads, int num_kv_heads, int head_dim,
+                            int block_size, float scale, float* out,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
 /* Single-sequence decode with the reference's argument list (gemm_cuda.h:41-44)
  * on bf16 pools, plus the pool size, workspace and stream.  Equivalent to
  * skv_paged_decode with num_seqs = 1, an fp32 query, max_blocks_per_seq =
@@ -174,6 +196,23 @@ int skv_paged_attention_decode(const float* query, const uint16_t* key_cache,
                                int num_q_heads, int num_kv_heads, int head_dim,
                                float scale, void* workspace,
                                size_t workspace_bytes, void* stream);
+
+/* skv_paged_attention_decode that first appends one token's K/V rows
+ * ([num_kv_heads][head_dim], kv_dtype) at position context_len - 1, in the same
+ * launch; equal to skv_kv_append_token(key_row, value_row, kv_dtype, ...,
+ * table_len = ceil(context_len / block_size), position = context_len - 1)
+ * followed by skv_paged_attention_decode.
+ * Replaces: transformer_block.cpp:484-509 (the K/V cudaMemcpy pair) plus the
+ * paged_attention_decode_cuda call that follows it (:511-518). */
+int skv_paged_attention_decode_append(const float* query, const void* key_row,
+                                      const void* value_row, int kv_dtype,
+                                      uint16_t* key_cache, uint16_t* value_cache,
+                                      int64_t total_blocks,
+                                      const int32_t* block_table, float* output,
+                                      int context_len, int block_size,
+                                      int num_q_heads, int num_kv_heads,
+                                      int head_dim, float scale, void* workspace,
+                                      size_t workspace_bytes, void* stream);
 
 /* ---- decoder-layer sub-steps around the path -----------------------------
  * Used by TransformerBlock::forward_into (include/stratakv/models/) for the

@@ -76,6 +76,11 @@ _PROTOS = {
     "skv_paged_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "skv_paged_decode": (_i32, [_vp, _i32, _vp, _vp, _i64, _vp, _i32, _vp, _i32, _i32, _i32,
                                 _i32, _i32, _f32, _vp, _vp, _sz, _vp]),
+    "skv_paged_decode_append": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _i32, _vp,
+                                       _i32, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _sz, _vp]),
+    "skv_paged_attention_decode_append": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _vp,
+                                                 _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz,
+                                                 _vp]),
     "skv_paged_attention_decode_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "skv_paged_attention_decode": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32,
                                           _i32, _f32, _vp, _sz, _vp]),
@@ -215,6 +220,31 @@ def paged_decode(q, q_dtype: int, k_pool, v_pool, total_blocks: int, block_table
                                   _ptr(block_tables), max_blocks_per_seq, _ptr(context_lens),
                                   num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
                                   scale, _ptr(out), _ptr(workspace), workspace_bytes, stream))
+
+
+def paged_decode_append(q, q_dtype: int, k_new, v_new, kv_dtype: int, k_pool, v_pool,
+                        total_blocks: int, block_tables, max_blocks_per_seq: int, context_lens,
+                        num_seqs: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                        block_size: int, scale: float, out, workspace, workspace_bytes: int,
+                        stream=None) -> None:
+    """Append each sequence's new token at context_lens[b] - 1, then decode (one launch)."""
+    _check(lib().skv_paged_decode_append(_ptr(q), q_dtype, _ptr(k_new), _ptr(v_new), kv_dtype,
+                                         _ptr(k_pool), _ptr(v_pool), total_blocks,
+                                         _ptr(block_tables), max_blocks_per_seq,
+                                         _ptr(context_lens), num_seqs, num_q_heads, num_kv_heads,
+                                         head_dim, block_size, scale, _ptr(out), _ptr(workspace),
+                                         workspace_bytes, stream))
+
+
+def paged_attention_decode_append(query, key_row, value_row, kv_dtype: int, key_cache,
+                                  value_cache, total_blocks: int, block_table, output,
+                                  context_len: int, block_size: int, num_q_heads: int,
+                                  num_kv_heads: int, head_dim: int, scale: float, workspace,
+                                  workspace_bytes: int, stream=None) -> None:
+    _check(lib().skv_paged_attention_decode_append(
+        _ptr(query), _ptr(key_row), _ptr(value_row), kv_dtype, _ptr(key_cache), _ptr(value_cache),
+        total_blocks, _ptr(block_table), _ptr(output), context_len, block_size, num_q_heads,
+        num_kv_heads, head_dim, scale, _ptr(workspace), workspace_bytes, stream))
 
 
 def paged_attention_decode(query, key_cache, value_cache, total_blocks: int, block_table, output,

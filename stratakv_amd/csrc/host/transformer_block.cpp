@@ -1,7 +1,7 @@
 // transformer_block.cpp -- TransformerBlock::to / forward / forward_into.
 // The GPU decode step follows src/models/transformer_block.cpp:334-613 of the
 // reference sub-step for sub-step; the KV append and the paged decode are the
-// hot path (skv_kv_append_token, skv_paged_attention_decode); the other
+// hot path (skv_paged_attention_decode_append: append + decode in one launch); the other
 // sub-steps use the simple kernels of skv_layer_ops.hip.
 #include "stratakv/models/transformer_block.h"
 
@@ -176,20 +176,17 @@ void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output,
     detail::check(skv_rope_f32(fp(keys), num_kv_heads, head_dim, position, s), "forward_into: rope k");
 
     // The paged-KV hot path: device block table (only new block ids are
-    // uploaded), the K/V append of this token, then the decode.
+    // uploaded), then one launch that appends this token's K/V rows at
+    // `position` (= context_len - 1) and decodes over the whole context.
     const int* table = page_table.get_device_block_table(seq_id);
-    const int table_len = static_cast<int>(state.physical_blocks.size());
-    detail::check(skv_kv_append_token(cfp(keys), cfp(values), SKV_DTYPE_FP32, block_pool.key_cache(),
-                                      block_pool.value_cache(), block_pool.total_blocks(), table,
-                                      table_len, position, num_kv_heads, head_dim, block_size, s),
-                  "forward_into: KV append");
     Tensor& ws = *decode_workspace_;
-    detail::check(skv_paged_attention_decode(cfp(queries), block_pool.key_cache(), block_pool.value_cache(),
-                                             block_pool.total_blocks(), table, fp(context), context_len,
-                                             block_size, num_heads, num_kv_heads, head_dim,
-                                             1.0f / std::sqrt(static_cast<float>(head_dim)), ws.raw_data(),
-                                             ws.num_elements() * ws.element_size(), s),
-                  "forward_into: paged attention");
+    detail::check(skv_paged_attention_decode_append(
+                      cfp(queries), cfp(keys), cfp(values), SKV_DTYPE_FP32, block_pool.key_cache(),
+                      block_pool.value_cache(), block_pool.total_blocks(), table, fp(context),
+                      context_len, block_size, num_heads, num_kv_heads, head_dim,
+                      1.0f / std::sqrt(static_cast<float>(head_dim)), ws.raw_data(),
+                      ws.num_elements() * ws.element_size(), s),
+                  "forward_into: KV append + paged attention");
 
     linear(attention_.output_projection(), context, down, "forward_into: o_proj");
     // Residual: reads hidden_states before output is written (aliasing-safe).

@@ -10,28 +10,11 @@
 // consecutive lanes on consecutive bytes of a row, so a row is written with
 // full-width coalesced stores.  bf16 input is copied bit for bit; fp32 input is
 // narrowed with the reference's round-to-nearest-even rule.
-#include "skv_common.h"
+#include "skv_append.h"
 
 #include <algorithm>
 
 namespace skv {
-
-struct AppendParams {
-    const void* k_new;
-    const void* v_new;
-    uint16_t* k_pool;
-    uint16_t* v_pool;
-    int64_t total_blocks;
-    const int32_t* tables;
-    int max_blocks;
-    const int32_t* positions; // [num_seqs], or nullptr -> single_position
-    int single_position;
-    const int32_t* offsets;   // [num_seqs + 1] or nullptr
-    int num_seqs;
-    int tokens_per_seq;       // tokens per sequence (upper bound when offsets != nullptr)
-    int row_elems;            // num_kv_heads * head_dim
-    int block_size;
-};
 
 // Resolve work item (sequence b, token j) to its source row and destination
 // element offset; returns false when the token does not exist or its block is
@@ -45,7 +28,7 @@ __device__ __forceinline__ bool resolve_row(const AppendParams& p, int b, int j,
     } else {
         src_row = static_cast<int64_t>(b) * p.tokens_per_seq + j;
     }
-    const int pos = (p.positions != nullptr ? p.positions[b] : p.single_position) + j;
+    const int pos = (p.positions != nullptr ? p.positions[b] + p.position_bias : p.single_position) + j;
     if (pos < 0) return false;
     const int blk = pos / p.block_size;
     if (blk >= p.max_blocks) return false;
@@ -114,8 +97,6 @@ __global__ __launch_bounds__(256) void kv_append_scalar_kernel(AppendParams p) {
     }
 }
 
-int launch_append(const AppendParams& p, int src_dtype, hipStream_t s);
-
 }  // namespace skv
 
 using namespace skv;
@@ -141,7 +122,7 @@ extern "C" int skv_kv_append(const void* k_new, const void* v_new, int src_dtype
                 static_cast<long long>(row));
 
     AppendParams p{k_new, v_new, k_pool, v_pool, total_blocks, block_tables, max_blocks_per_seq,
-                   positions, 0, token_offsets, num_seqs, tokens_per_seq, static_cast<int>(row),
+                   positions, 0, 0, token_offsets, num_seqs, tokens_per_seq, static_cast<int>(row),
                    block_size};
     return launch_append(p, src_dtype, static_cast<hipStream_t>(stream));
 }
@@ -161,7 +142,7 @@ extern "C" int skv_kv_append_token(const void* k_row, const void* v_row, int src
                 "skv_kv_append_token: no KV page for position %d", position);
     const int64_t row = static_cast<int64_t>(num_kv_heads) * head_dim;
     SKV_REQUIRE(row <= (1 << 24), "skv_kv_append_token: row too large");
-    AppendParams p{k_row, v_row, k_pool, v_pool, total_blocks, block_table, table_len, nullptr,
+    AppendParams p{k_row, v_row, k_pool, v_pool, total_blocks, block_table, table_len, nullptr, 0,
                    position, nullptr, 1, 1, static_cast<int>(row), block_size};
     return launch_append(p, src_dtype, static_cast<hipStream_t>(stream));
 }

@@ -34,7 +34,7 @@
 //   only raised (and acc, sum rescaled) when a block's max exceeds it by more
 //   than 2^8, which after the first blocks is rare; the result is exact since
 //   numerator and denominator share the same reference max.
-#include "skv_common.h"
+#include "skv_append.h"
 
 #include <algorithm>
 #include <cmath>
@@ -68,6 +68,13 @@ struct DecodeParams {
     int32_t* plan;         // [3 + B + 1]: total, per, used ranges, P[0..B]
     float* ws_ml;          // [2 * ranges * Hseg][NH][2]  (reference max in log2 units, sum)
     float* ws_acc;         // [2 * ranges * Hseg][NH][HD] (unnormalised P.V)
+    // Fused append (MFMA kernel only): the new token of sequence b, at position
+    // lens[b] - 1, rows [B][Hkv][HD]; nullptr = no append.
+    const void* k_new;
+    const void* v_new;
+    int kv_new_fp32;       // 1: fp32 rows, rounded to nearest-even; 0: bf16 bits
+    uint16_t* k_pool_w;    // the pools again, writable (the new rows are stored)
+    uint16_t* v_pool_w;
 };
 
 constexpr int kMaxHeadDim = 512;
@@ -161,16 +168,12 @@ __device__ __forceinline__ int64_t partial_row(int range, bool tail, int Hseg, i
 // Each wavefront owns its LDS tiles and synchronises only with itself
 // (wave_lds_sync); the WPW wavefronts of a workgroup meet once, at the split.
 // ---------------------------------------------------------------------------
-// Wavefronts per SIMD the register budget of decode_mfma_kernel allows: about
-// G*8 accumulators + NBUF * HD/4 buffer registers + 70 for the rest.
-constexpr int mfma_occupancy(int HD, int G, int NBUF) {
-    return G * 8 + NBUF * HD / 4 + 70 <= 128 ? 4
-         : G * 8 + NBUF * HD / 4 + 70 <= 168 ? 3
-         : G * 8 + NBUF * HD / 4 + 70 <= 256 ? 2 : 1;
-}
+// Wavefronts per SIMD the MFMA kernel is launched with (see launch_mfma_shape);
+// also its register budget (launch bound).
+constexpr int mfma_waves_per_simd(int HD, int G) { return HD == 64 && G < 16 ? 2 : 1; }
 
 template <int HD, int G, bool QF32, int WPW, int NBUF>
-__global__ __launch_bounds__(64 * WPW, mfma_occupancy(HD, G, NBUF)) void decode_mfma_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_mfma_kernel(DecodeParams p) {
     constexpr int BS = 16;
     constexpr int CH = HD / 8;      // 16-byte chunks per row
     constexpr int RPI = 64 / CH;    // rows per coalesced load instruction
@@ -220,6 +223,41 @@ __global__ __launch_bounds__(64 * WPW, mfma_occupancy(HD, G, NBUF)) void decode_
         const int L = seq_len(p, b);
         const int Leff = std::min(L, nb * BS);
         const int32_t* table = p.tables + static_cast<int64_t>(b) * p.max_blocks;
+
+        // Fused append: the wavefront whose range holds the segment's last block
+        // takes the new token's K/V row (position L - 1, slot = row i_new * RPI
+        // + r_new of that block): it replaces the pool's row in registers when
+        // the block is consumed and is stored into the pool after the segment.
+        // Skipped, like skv_kv_append, when the position is beyond the table or
+        // its block is outside the pool.
+        int kb_new = -1, i_new = 0, r_new = 0;
+        int64_t new_dst = 0;
+        u32x4_t knew = {0u, 0u, 0u, 0u}, vnew = {0u, 0u, 0u, 0u};
+        if (p.k_new != nullptr && kb1 == nb && L >= 1 && L <= nb * BS) {
+            const int64_t e = table[nb - 1];
+            if (e >= 0 && e < p.total_blocks) {
+                const int slot = (L - 1) - (nb - 1) * BS;
+                kb_new = nb - 1;
+                i_new = slot / RPI;
+                r_new = slot % RPI;
+                new_dst = (e * BS + slot) * row_stride + static_cast<int64_t>(kvh) * HD + c * 8;
+                if (r == r_new) {
+                    const int64_t src = (static_cast<int64_t>(b) * Hkv + kvh) * HD + c * 8;
+                    if (p.kv_new_fp32) {
+                        const float4* ks = reinterpret_cast<const float4*>(static_cast<const float*>(p.k_new) + src);
+                        const float4* vs = reinterpret_cast<const float4*>(static_cast<const float*>(p.v_new) + src);
+                        const float4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
+                        knew = u32x4_t{pack_bf16x2(k0.x, k0.y), pack_bf16x2(k0.z, k0.w),
+                                       pack_bf16x2(k1.x, k1.y), pack_bf16x2(k1.z, k1.w)};
+                        vnew = u32x4_t{pack_bf16x2(v0.x, v0.y), pack_bf16x2(v0.z, v0.w),
+                                       pack_bf16x2(v1.x, v1.y), pack_bf16x2(v1.z, v1.w)};
+                    } else {
+                        knew = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.k_new) + src);
+                        vnew = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.v_new) + src);
+                    }
+                }
+            }
+        }
 
         // q operand(s): head h0 + t, chunk 4*cc + j; zero for padded heads.
         bf16x8_t qop[QP][NMF];
@@ -292,7 +330,16 @@ __global__ __launch_bounds__(64 * WPW, mfma_occupancy(HD, G, NBUF)) void decode_
             return valid;
         };
 
-        auto consume = [&](int kb, const u32x4_t (&kk)[TPL], const u32x4_t (&vv)[TPL]) {
+        auto consume = [&](int kb, u32x4_t (&kk)[TPL], u32x4_t (&vv)[TPL]) {
+            if (kb == kb_new) {  // the block that receives the appended token
+#pragma unroll
+                for (int i = 0; i < TPL; ++i) {
+                    if (i == i_new && r == r_new) {
+                        kk[i] = knew;
+                        vv[i] = vnew;
+                    }
+                }
+            }
             // ---- K through the LDS tile into the MFMA operand layout
 #pragma unroll
             for (int i = 0; i < TPL; ++i) {
@@ -379,6 +426,11 @@ __global__ __launch_bounds__(64 * WPW, mfma_occupancy(HD, G, NBUF)) void decode_
                 if (okb[u]) consume(kb + u, kbuf[u], vbuf[u]);
                 okb[u] = issue(kb + u + NBUF, kbuf[u], vbuf[u]);
             }
+        }
+
+        if (kb_new >= 0 && r == r_new) {  // fused append: store the new row
+            *reinterpret_cast<u32x4_t*>(p.k_pool_w + new_dst) = knew;
+            *reinterpret_cast<u32x4_t*>(p.v_pool_w + new_dst) = vnew;
         }
 
         // ---- finalise the segment: combine row groups, broadcast (sum, max)
@@ -765,7 +817,7 @@ int launch_pair(K kern, int wpw, int max_per_simd, DecodeParams p, hipStream_t s
 template <int HD, int G, bool QF32>
 int launch_mfma_shape(const DecodeParams& p, hipStream_t s) {
     constexpr int NB = HD == 64 ? 3 : 2;
-    constexpr int PER_SIMD = HD == 64 ? 2 : 1;
+    constexpr int PER_SIMD = mfma_waves_per_simd(HD, G);
     const char* name = "decode_mfma_kernel";
     if (p.Hkv % 4 == 0) return launch_pair(decode_mfma_kernel<HD, G, QF32, 4, NB>, 4, PER_SIMD, p, s, name);
     if (p.Hkv % 2 == 0) return launch_pair(decode_mfma_kernel<HD, G, QF32, 2, NB>, 2, PER_SIMD, p, s, name);
@@ -791,11 +843,25 @@ bool mfma_path_ok(const DecodeParams& p, int q_dtype) {
            (q_dtype == SKV_DTYPE_BF16 || q_dtype == SKV_DTYPE_FP32);
 }
 
+// The appended rows go through the MFMA kernel when it runs and its 16-byte
+// accesses to them are aligned; otherwise the append kernel runs first (same
+// result: it writes position lens[b] - 1 of every sequence, then the decode
+// reads it from the pool).
+int append_before_decode(DecodeParams& p, hipStream_t s) {
+    AppendParams a{p.k_new, p.v_new, p.k_pool_w, p.v_pool_w, p.total_blocks, p.tables,
+                   p.max_blocks, p.lens, -1, p.single_len - 1, nullptr, p.B, 1, p.Hkv * p.HD, p.bs};
+    p.k_new = p.v_new = nullptr;
+    return launch_append(a, p.kv_new_fp32 ? SKV_DTYPE_FP32 : SKV_DTYPE_BF16, s);
+}
+
 int run_decode_chunk(DecodeParams p, int q_dtype, char* ws, const WorkspaceLayout& w, hipStream_t s) {
     p.plan = reinterpret_cast<int32_t*>(ws + w.plan_off);
     p.ws_ml = reinterpret_cast<float*>(ws + w.ml_off);
     p.ws_acc = reinterpret_cast<float*>(ws + w.acc_off);
-    if (mfma_path_ok(p, q_dtype)) {
+    const bool mfma = mfma_path_ok(p, q_dtype);
+    if (p.k_new != nullptr && !(mfma && aligned16(p.k_new) && aligned16(p.v_new)))
+        if (int rc = append_before_decode(p, s)) return rc;
+    if (mfma) {
         p.Hseg = p.Hkv;
         p.NH = p.Hq / p.Hkv;
         p.min_per = 4;
@@ -832,6 +898,11 @@ int run_decode(DecodeParams p, int q_dtype, void* workspace, size_t workspace_by
         c.out = p.out + head_rows;
         c.tables = p.tables + static_cast<int64_t>(b0) * p.max_blocks;
         if (p.lens != nullptr) c.lens = p.lens + b0;
+        if (p.k_new != nullptr) {
+            const size_t rows = static_cast<size_t>(b0) * p.Hkv * p.HD * (p.kv_new_fp32 ? 4 : 2);
+            c.k_new = static_cast<const char*>(p.k_new) + rows;
+            c.v_new = static_cast<const char*>(p.v_new) + rows;
+        }
         if (int rc = run_decode_chunk(c, q_dtype, static_cast<char*>(workspace), w, s)) return rc;
     }
     return SKV_OK;
@@ -893,6 +964,49 @@ extern "C" int skv_paged_decode(const void* q, int q_dtype, const uint16_t* k_po
     return run_decode(p, q_dtype, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int skv_paged_decode_append(const void* q, int q_dtype, const void* k_new,
+                                       const void* v_new, int kv_dtype, uint16_t* k_pool,
+                                       uint16_t* v_pool, int64_t total_blocks,
+                                       const int32_t* block_tables, int max_blocks_per_seq,
+                                       const int32_t* context_lens, int num_seqs, int num_q_heads,
+                                       int num_kv_heads, int head_dim, int block_size, float scale,
+                                       float* out, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+    SKV_REQUIRE(q && k_new && v_new && k_pool && v_pool && block_tables && context_lens && out,
+                "skv_paged_decode_append: invalid device pointers or attention dimensions");
+    SKV_REQUIRE(q_dtype == SKV_DTYPE_BF16 || q_dtype == SKV_DTYPE_FP32,
+                "skv_paged_decode_append: unknown query dtype %d", q_dtype);
+    SKV_REQUIRE(kv_dtype == SKV_DTYPE_BF16 || kv_dtype == SKV_DTYPE_FP32,
+                "skv_paged_decode_append: unknown K/V dtype %d", kv_dtype);
+    SKV_REQUIRE(total_blocks > 0 && max_blocks_per_seq > 0,
+                "skv_paged_decode_append: pool and table sizes must be positive");
+    if (int rc = validate_geometry("skv_paged_decode_append", num_seqs, num_q_heads, num_kv_heads,
+                                   head_dim, block_size, scale))
+        return rc;
+    DecodeParams p{};
+    p.q = q;
+    p.k = k_pool;
+    p.v = v_pool;
+    p.total_blocks = total_blocks;
+    p.tables = block_tables;
+    p.max_blocks = max_blocks_per_seq;
+    p.lens = context_lens;
+    p.single_len = 0;
+    p.B = num_seqs;
+    p.Hq = num_q_heads;
+    p.Hkv = num_kv_heads;
+    p.HD = head_dim;
+    p.bs = block_size;
+    p.qscale = scale * 1.4426950408889634f;
+    p.out = out;
+    p.k_new = k_new;
+    p.v_new = v_new;
+    p.kv_new_fp32 = kv_dtype == SKV_DTYPE_FP32 ? 1 : 0;
+    p.k_pool_w = k_pool;
+    p.v_pool_w = v_pool;
+    return run_decode(p, q_dtype, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
 extern "C" size_t skv_paged_attention_decode_workspace_bytes(int num_q_heads, int num_kv_heads,
                                                              int head_dim) {
     return skv_paged_decode_workspace_bytes(1, num_q_heads, num_kv_heads, head_dim);
@@ -927,6 +1041,47 @@ extern "C" int skv_paged_attention_decode(const float* query, const uint16_t* ke
     p.bs = block_size;
     p.qscale = scale * 1.4426950408889634f;
     p.out = output;
+    return run_decode(p, SKV_DTYPE_FP32, workspace, workspace_bytes,
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" int skv_paged_attention_decode_append(const float* query, const void* key_row,
+                                                 const void* value_row, int kv_dtype,
+                                                 uint16_t* key_cache, uint16_t* value_cache,
+                                                 int64_t total_blocks, const int32_t* block_table,
+                                                 float* output, int context_len, int block_size,
+                                                 int num_q_heads, int num_kv_heads, int head_dim,
+                                                 float scale, void* workspace,
+                                                 size_t workspace_bytes, void* stream) {
+    SKV_REQUIRE(query && key_row && value_row && key_cache && value_cache && block_table &&
+                    output && context_len > 0 && total_blocks > 0,
+                "paged_attention_decode_append: invalid device pointers or attention dimensions");
+    SKV_REQUIRE(kv_dtype == SKV_DTYPE_BF16 || kv_dtype == SKV_DTYPE_FP32,
+                "paged_attention_decode_append: unknown K/V dtype %d", kv_dtype);
+    if (int rc = validate_geometry("paged_attention_decode_append", 1, num_q_heads, num_kv_heads,
+                                   head_dim, block_size, scale))
+        return rc;
+    DecodeParams p{};
+    p.q = query;
+    p.k = key_cache;
+    p.v = value_cache;
+    p.total_blocks = total_blocks;
+    p.tables = block_table;
+    p.max_blocks = cdiv(context_len, block_size);
+    p.lens = nullptr;
+    p.single_len = context_len;
+    p.B = 1;
+    p.Hq = num_q_heads;
+    p.Hkv = num_kv_heads;
+    p.HD = head_dim;
+    p.bs = block_size;
+    p.qscale = scale * 1.4426950408889634f;
+    p.out = output;
+    p.k_new = key_row;
+    p.v_new = value_row;
+    p.kv_new_fp32 = kv_dtype == SKV_DTYPE_FP32 ? 1 : 0;
+    p.k_pool_w = key_cache;
+    p.v_pool_w = value_cache;
     return run_decode(p, SKV_DTYPE_FP32, workspace, workspace_bytes,
                       static_cast<hipStream_t>(stream));
 }

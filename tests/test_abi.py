@@ -71,3 +71,21 @@ def test_append_rejects_invalid_arguments():
         with pytest.raises(skv.SkvInvalidArgument):
             skv.kv_append(**dict(base, **bad))
     skv.kv_append(**dict(base, num_seqs=0))  # empty batch is a no-op
+
+
+def test_fused_decode_append_rejects_invalid_arguments():
+    base = dict(q=FAKE, q_dtype=skv.DTYPE_BF16, k_new=FAKE, v_new=FAKE, kv_dtype=skv.DTYPE_BF16,
+                k_pool=FAKE, v_pool=FAKE, total_blocks=4, block_tables=FAKE, max_blocks_per_seq=2,
+                context_lens=FAKE, num_seqs=2, num_q_heads=8, num_kv_heads=4, head_dim=64,
+                block_size=16, scale=0.125, out=FAKE, workspace=FAKE, workspace_bytes=1 << 30)
+    for bad in (dict(kv_dtype=5), dict(q_dtype=7), dict(k_new=None), dict(num_seqs=0),
+                dict(num_kv_heads=3), dict(scale=float("nan"))):
+        with pytest.raises(skv.SkvInvalidArgument):
+            skv.paged_decode_append(**dict(base, **bad))
+    single = dict(query=FAKE, key_row=FAKE, value_row=FAKE, kv_dtype=skv.DTYPE_FP32,
+                  key_cache=FAKE, value_cache=FAKE, total_blocks=4, block_table=FAKE, output=FAKE,
+                  context_len=5, block_size=16, num_q_heads=8, num_kv_heads=4, head_dim=64,
+                  scale=0.125, workspace=FAKE, workspace_bytes=1 << 20)
+    for bad in (dict(context_len=0), dict(key_row=None), dict(kv_dtype=3), dict(num_q_heads=6)):
+        with pytest.raises(skv.SkvInvalidArgument):
+            skv.paged_attention_decode_append(**dict(single, **bad))

@@ -3,7 +3,9 @@
 The pools are generated on the GPU (counter-hash N(0,1) bf16) with the same
 tables bench.py times.  After one bench step (append of one token per sequence
 at its last slot, then decode):
-* every output is finite and a second identical decode gives identical bits;
+* the step is the fused call bench.py times (append at lens - 1, then decode);
+  every output is finite, and a plain decode of the appended pools afterwards
+  gives identical bits;
 * the appended rows hold exactly the new K/V bits;
 * a seeded sample of sequences plus the shortest and longest is checked against
   the oracle: their blocks are gathered on the GPU into a compact pool, read
@@ -45,13 +47,18 @@ def _step(skv, w, seed):
     wsb = skv.decode_workspace_bytes(B, Hq, Hkv, hd)
     d["ws"] = skv.DeviceBuffer(wsb)
     mb = w["tables"].shape[1]
-    skv.kv_append(d["kn"], d["vn"], skv.DTYPE_BF16, d["k"], d["v"], total, d["t"], mb, d["p"], B, 1,
-                  Hkv, hd, bs)
 
-    def decode():
+    def decode(fused=False):
+        """fused: the bench step (skv_paged_decode_append: append the new rows
+        at lens - 1, then attend); otherwise a plain decode of the pools."""
         out = skv.DeviceBuffer(B * Hq * hd * 4)
-        skv.paged_decode(d["q"], skv.DTYPE_BF16, d["k"], d["v"], total, d["t"], mb, d["l"], B, Hq,
-                         Hkv, hd, bs, 1.0 / math.sqrt(hd), out, d["ws"], wsb)
+        if fused:
+            skv.paged_decode_append(d["q"], skv.DTYPE_BF16, d["kn"], d["vn"], skv.DTYPE_BF16,
+                                    d["k"], d["v"], total, d["t"], mb, d["l"], B, Hq, Hkv, hd, bs,
+                                    1.0 / math.sqrt(hd), out, d["ws"], wsb)
+        else:
+            skv.paged_decode(d["q"], skv.DTYPE_BF16, d["k"], d["v"], total, d["t"], mb, d["l"], B,
+                             Hq, Hkv, hd, bs, 1.0 / math.sqrt(hd), out, d["ws"], wsb)
         skv.synchronize()
         return out.download(np.float32, (B, Hq, hd))
 
@@ -73,9 +80,12 @@ def test_full_size_config(gpu, cfg, n_sample):
     B, Hq, Hkv, hd, bs, total = w["B"], w["Hq"], w["Hkv"], w["hd"], w["bs"], w["total"]
     print(f"cfg{cfg}: B={B} contexts {int(w['lens'].min())}..{int(w['lens'].max())}", flush=True)
     d, decode = _step(gpu, w, seed=0x5EED0000 + 17 * cfg)
-    out = decode()
+    out = decode(fused=True)
     assert np.isfinite(out).all()
-    assert np.array_equal(out, decode()), "decode is not deterministic"
+    # A plain decode of the appended pools gives the same bits: the fused
+    # append stored exactly the rows it attended to, and the kernel is
+    # deterministic.
+    assert np.array_equal(out, decode()), "fused step and plain decode differ"
 
     rng = np.random.default_rng(cfg)
     lens = w["lens"]
@@ -112,8 +122,9 @@ def test_full_size_churn_config5(gpu):
     t_new = w["tables"][nl:]
     assert any(np.any(np.diff(r[: chunk // bs]) < 0) for r in t_new), "churn tables are monotone"
     d, decode = _step(gpu, dict(w, lens=w["lens"]), seed=0x5EED0055)
-    # _step appended one decode token per sequence at lens-1 (the churn rows'
-    # position 2,048); now the prefill chunks at positions 0..2,047.
+    # The prefill chunks at positions 0..2,047 of the new sequences first, then
+    # the fused step appends one decode token per sequence at lens - 1 (the
+    # churn rows' position 2,048) and decodes, as in bench.py.
     ck = gpu.DeviceBuffer(nn * chunk * row * 2)
     cv = gpu.DeviceBuffer(nn * chunk * row * 2)
     gpu.fill_normal_bf16(ck, nn * chunk * row, 77)
@@ -121,7 +132,7 @@ def test_full_size_churn_config5(gpu):
     zero = gpu.DeviceBuffer.from_numpy(np.zeros(nn, np.int32))
     gpu.kv_append(ck, cv, gpu.DTYPE_BF16, d["k"], d["v"], total, d["t"].ptr + nl * mb * 4, mb, zero,
                   nn, chunk, Hkv, hd, bs)
-    out = decode()
+    out = decode(fused=True)
     assert np.isfinite(out).all()
     q = d["q"].download(np.uint16, (B, Hq, hd))
     kc = ck.download(np.uint16, (nn, chunk // bs, bs, Hkv, hd))
