@@ -17,7 +17,8 @@ Default workload: config 4 of BASELINE.json (Llama-3-8B geometry: 32 Q heads,
 8192 and sigma 0.6 clipped to [2048, 32768], 16-token blocks allocated
 round-robin across sequences), the configuration the >= 70 % of HBM peak
 target is quoted on.  --config 2 / 3 / 5 select the other single-GPU
-attention configs.
+attention configs; --config 1 times the same call per layer and position of
+a 22-layer TinyLlama-shaped generation (16 prompt + 128 new tokens).
 
 Output: one JSON line on stdout.  value = algorithmic bytes of a whole step
 / device time per step, in GB/s.  roofline = the decode call (fused append +
@@ -104,7 +105,7 @@ def workload(cfg: int):
     elif cfg == 5:
         return churn_workload()
     else:
-        raise SystemExit(f"bench.py: unknown --config {cfg} (single-GPU attention configs: 2, 3, 4, 5)")
+        raise SystemExit(f"bench.py: unknown --config {cfg} (configs: 1, 2, 3, 4, 5)")
     return dict(cfg=cfg, Hq=Hq, Hkv=Hkv, hd=hd, B=B, bs=bs, lens=lens, tables=tables,
                 total=int(total), desc=desc, seed=0x5EED0000 + cfg)
 
@@ -355,6 +356,123 @@ def cpu_baseline(w, budget_s: float = 12.0):
     return out[1], out[threads_all]
 
 
+# ---------------------------------------------------------------------------
+# cfg1: the hot path of a TinyLlama-shaped generation, per layer per position
+# ---------------------------------------------------------------------------
+CFG1_LAYERS, CFG1_PROMPT, CFG1_NEW, CFG1_POOL_BLOCKS = 22, 16, 128, 1024
+
+
+def cfg1_bytes(Hq, Hkv, hd, bs, positions, layers):
+    """Algorithmic bytes of one generation: per layer and position p (context
+    p + 1) the K/V read once, the table, the fp32 query and output, and the
+    fp32 new rows read + bf16 rows written."""
+    total = 0
+    for p in range(positions):
+        L = p + 1
+        total += 2 * L * Hkv * hd * 2 + 4 * (-(-L // bs)) + 4 + Hq * hd * 4 * 2 + 2 * Hkv * hd * (4 + 2)
+    return total * layers
+
+
+def run_cfg1(steps: int, warmup: int, with_cpu: bool):
+    """cfg1 of BASELINE.json on the GPU side: a TinyLlama-shaped model (32 Q / 4
+    KV heads, head_dim 64, 22 layers, a 1,024-block pool per layer as the
+    reference CLI sizes it) generating 16 prompt + 128 new tokens one position
+    at a time, as forward_into runs them.  One step = one generation: for every
+    position p and layer, one skv_paged_attention_decode_append call (the
+    append of the token's fp32 K/V rows at p, then attention over p + 1 tokens,
+    with the fp32 query) on that layer's pool -- the call forward_into makes.
+    The GEMVs, norms and RoPE around it are not part of the measured path."""
+    import stratakv_amd as skv
+
+    skv.require_gpu()
+    Hq, Hkv, hd, bs, layers = 32, 4, 64, 16, CFG1_LAYERS
+    P = CFG1_PROMPT + CFG1_NEW
+    rng = np.random.default_rng(0x5EED0001)
+    q = skv.DeviceBuffer.from_numpy(rng.standard_normal((layers, P, Hq, hd), dtype=np.float32))
+    kr = skv.DeviceBuffer.from_numpy(rng.standard_normal((layers, P, Hkv, hd), dtype=np.float32))
+    vr = skv.DeviceBuffer.from_numpy(rng.standard_normal((layers, P, Hkv, hd), dtype=np.float32))
+    pool_elems = CFG1_POOL_BLOCKS * bs * Hkv * hd
+    kp = [skv.DeviceBuffer(pool_elems * 2) for _ in range(layers)]
+    vp = [skv.DeviceBuffer(pool_elems * 2) for _ in range(layers)]
+    for i in range(layers):
+        skv.fill_normal_bf16(kp[i], pool_elems, 0x5EED0100 + 2 * i)
+        skv.fill_normal_bf16(vp[i], pool_elems, 0x5EED0101 + 2 * i)
+    # A fresh LIFO pool hands the one sequence blocks 0, 1, 2, ... in every layer.
+    table = skv.DeviceBuffer.from_numpy(np.arange(-(-P // bs), dtype=np.int32))
+    out = skv.DeviceBuffer(Hq * hd * 4)
+    wsb = int(skv.lib().skv_paged_attention_decode_workspace_bytes(Hq, Hkv, hd))
+    ws = skv.DeviceBuffer(wsb)
+    stream = skv.Stream()
+    scale = 1.0 / math.sqrt(hd)
+    qrow, kvrow = Hq * hd * 4, Hkv * hd * 4
+
+    def generation():
+        for p in range(P):
+            for i in range(layers):
+                off = i * P + p
+                skv.paged_attention_decode_append(
+                    q.ptr + off * qrow, kr.ptr + off * kvrow, vr.ptr + off * kvrow, skv.DTYPE_FP32,
+                    kp[i], vp[i], CFG1_POOL_BLOCKS, table, out, p + 1, bs, Hq, Hkv, hd, scale, ws,
+                    wsb, stream=stream.handle)
+
+    skv.synchronize()
+    for _ in range(warmup):
+        generation()
+    skv.synchronize()
+    log(f"cfg1 warmup done ({warmup} generations); timing {steps}")
+    e0, e1 = skv.Event(), skv.Event()
+    t0 = time.perf_counter()
+    e0.record(stream.handle)
+    for _ in range(steps):
+        generation()
+    e1.record(stream.handle)
+    skv.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1) / steps
+    nbytes = cfg1_bytes(Hq, Hkv, hd, bs, P, layers)
+    calls = P * layers
+    gbs = nbytes / (ms / 1e3) / 1e9
+    line = {
+        "metric": METRIC, "value": round(gbs, 3), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) fp32 queries and K/V rows, bf16 pools)",
+        "config": {"workload": ("cfg1: TinyLlama-shaped generation, 22 layers x (16 prompt + 128 new) "
+                                "positions, one skv_paged_attention_decode_append per layer and "
+                                "position (32 Q / 4 KV heads, head_dim 64, 1,024-block pool per "
+                                "layer); a step is one whole generation"),
+                   "layers": layers, "positions": P, "num_q_heads": Hq, "num_kv_heads": Hkv,
+                   "head_dim": hd, "block_size": bs, "parallelism": "none (1 GPU)"},
+        "tokens_per_s": round(P / (ms / 1e3), 1),
+        "us_per_layer_position": round(ms * 1e3 / calls, 3),
+        "host_wall_ms_per_step": round(wall * 1e3 / steps, 3),
+        "roofline": {"bound": "hbm", "note": "launch-bound: each call moves 20-90 KB",
+                     "kernel": "skv_paged_attention_decode_append (fused append + attention, merge)",
+                     "achieved": round(gbs, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 6), "traffic": None,
+                     "algorithmic_bytes": nbytes},
+    }
+    if with_cpu:
+        import oracle
+        # One layer's 144 single-sequence decodes with the oracle, scaled to 22 layers.
+        kpool = oracle.f32_to_bf16(rng.standard_normal((-(-P // bs), bs, Hkv, hd), dtype=np.float32))
+        vpool = oracle.f32_to_bf16(rng.standard_normal((-(-P // bs), bs, Hkv, hd), dtype=np.float32))
+        qh = rng.standard_normal((1, Hq, hd), dtype=np.float32)
+        tab = np.arange(-(-P // bs), dtype=np.int32)[None, :]
+        t0 = time.perf_counter()
+        for p in range(P):
+            oracle.paged_decode(qh, kpool, vpool, tab, np.array([p + 1], np.int32), Hkv, bs, scale)
+        dt = (time.perf_counter() - t0) * layers
+        line["cpu_baseline"] = {
+            "value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "tokens_per_s": round(P / dt, 2),
+            "sample": ("oracle two-pass fp32 attention (restatement of src/layers/attention.cpp:"
+                       "263-337) over one layer's 144 positions, scaled by 22 layers; the "
+                       "append is not timed on the CPU")}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def profile_traffic(workload_key: str):
     """HBM bytes per launch of the decode kernel from the committed rocprof
     counter summary, if one exists for this workload."""
@@ -390,7 +508,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=4, help="BASELINE.json config (2, 3, 4 or 5)")
+    ap.add_argument("--config", type=int, default=4, help="BASELINE.json config (1, 2, 3, 4 or 5)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--separate", action="store_true",
                     help="time the decode-token append and the decode as two calls "
@@ -405,6 +523,8 @@ def main() -> int:
               f"decode path shards by sequence or KV head with no exchange; the multi-GPU design is "
               f"described in DESIGN.md but not built or measured.", file=sys.stderr)
         return 2
+    if args.config == 1:
+        return run_cfg1(args.steps, args.warmup, not args.no_cpu_baseline)
     w = churn_workload(args.warmup + args.steps) if args.config == 5 else workload(args.config)
     dec_bytes, tok_bytes, churn_bytes, flops = algorithmic_bytes(w)
     log(w["desc"])

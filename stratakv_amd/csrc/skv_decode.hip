@@ -75,6 +75,7 @@ struct DecodeParams {
     int kv_new_fp32;       // 1: fp32 rows, rounded to nearest-even; 0: bf16 bits
     uint16_t* k_pool_w;    // the pools again, writable (the new rows are stored)
     uint16_t* v_pool_w;
+    int merge_cw;          // output columns per merge workgroup (a multiple of 64)
 };
 
 constexpr int kMaxHeadDim = 512;
@@ -608,135 +609,170 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Merge: one 256-thread workgroup per segment (sequence, head group).
-// Segments held by a single range were finalised by the attention kernel;
-// sequences without context get zeros.  For each of the NH heads:
-//   out = sum_r acc_r 2^(m_r - M) / sum_r l_r 2^(m_r - M)
-// over the ranges r that touch the segment.  NH divides 256, so thread t only
-// ever sees head t % NH in the (partial, head) loops; the per-thread results
-// are reduced through LDS.  The P.V rows of all partials are loaded
-// independently (no dependent chain), four at a time.
+// Merge of the segments cut by range boundaries:
+//   out = sum_r acc_r 2^(m_r - M) / sum_r l_r 2^(m_r - M),  M = max_r m_r,
+// over the n ranges r that touch the segment, per query head.  One 256-thread
+// workgroup per (segment, 64 output columns).  With at most 8 partials (long
+// batches) the segment's first workgroup merges all its columns in one round
+// of loads and the others exit.  With more (short batches, one long
+// sequence), thread (c, pg) = (t % 64, t / 64) of every workgroup takes
+// partials pg, pg + 4, ... of column c, 8 at a time with all their loads in
+// flight, and keeps its own (max, sum, acc) triple, rescaled per batch; the 4
+// partial groups are combined the same way through LDS.  Segments held by one
+// range were finalised by the attention kernel; sequences without context get
+// zeros.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
-    constexpr int kMaxN = 8;   // partials per segment kept in registers (fast path)
-    constexpr int kMaxE = 8;   // output elements per thread (NH * HD <= 2048)
-    __shared__ float red[256], w_s[256];
-    __shared__ float M_s[16], inv_s[16];
+constexpr int kMergeFew = 8;   // partials merged by one workgroup per segment
+
+// NP partials (exactly), NC columns per thread: every load is unconditional,
+// so all 3 * NP * NC of them are in flight together (a conditional load makes
+// the compiler wait for it before issuing the next one).
+template <int NC, int NP>
+__device__ __forceinline__ void merge_few(const DecodeParams& p, int grp, int r0, bool first_tail,
+                                          float* out0, int c0, int c1) {
     const int t = threadIdx.x;
-    const int s = blockIdx.x;
+    const int HD = p.HD, NH = p.NH;
+    float a[NC][NP], m[NC][NP], l[NC][NP];
+#pragma unroll
+    for (int e = 0; e < NC; ++e) {
+        const int col = min(c0 + t + 256 * e, c1 - 1);
+        const int g = col / HD;
+        const int d = col - g * HD;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int64_t row = partial_row(r0 + i, i == 0 && first_tail, p.Hseg, grp) * NH + g;
+            a[e][i] = p.ws_acc[row * HD + d];
+            m[e][i] = p.ws_ml[row * 2];
+            l[e][i] = p.ws_ml[row * 2 + 1];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < NC; ++e) {
+        const int col = c0 + t + 256 * e;
+        if (col >= c1) continue;
+        float M = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) M = fmaxf(M, m[e][i]);
+        float L = 0.0f, A = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const float w = fast_exp2(m[e][i] - M);
+                L = fmaf(w, l[e][i], L);
+                A = fmaf(w, a[e][i], A);
+            }
+        }
+        out0[col] = L > 0.0f ? A / L : 0.0f;
+    }
+}
+
+template <int NC>
+__device__ __forceinline__ void merge_few_n(const DecodeParams& p, int grp, int r0, int n,
+                                            bool first_tail, float* out0, int c0, int c1) {
+    switch (n) {
+        case 2: merge_few<NC, 2>(p, grp, r0, first_tail, out0, c0, c1); break;
+        case 3: merge_few<NC, 3>(p, grp, r0, first_tail, out0, c0, c1); break;
+        case 4: merge_few<NC, 4>(p, grp, r0, first_tail, out0, c0, c1); break;
+        case 5: merge_few<NC, 5>(p, grp, r0, first_tail, out0, c0, c1); break;
+        case 6: merge_few<NC, 6>(p, grp, r0, first_tail, out0, c0, c1); break;
+        case 7: merge_few<NC, 7>(p, grp, r0, first_tail, out0, c0, c1); break;
+        default: merge_few<NC, 8>(p, grp, r0, first_tail, out0, c0, c1); break;
+    }
+}
+
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
+    __shared__ float gm[4], gl[4];
+    __shared__ float ga[4][64];
+    const int t = threadIdx.x;
+    const int HD = p.HD, NH = p.NH;
+    const int cols = NH * HD;
+    const int cw = p.merge_cw;
+    const int nchunk = cdiv(cols, cw);
+    const int s = blockIdx.x / nchunk;
+    const int chunk = blockIdx.x - s * nchunk;
+    const int c0 = chunk * cw, c1 = min(cols, c0 + cw);
     const int b = s / p.Hseg;
     const int grp = s - b * p.Hseg;
     const int per = p.plan[1];
     const int32_t* P = p.plan + 3;
     const int lo = P[b], hi = P[b + 1];
-    const int HD = p.HD, NH = p.NH;
     float* out0 = p.out + (static_cast<int64_t>(b) * p.Hq + grp * NH) * HD;
     if (lo == hi) {
-        for (int e = t; e < NH * HD; e += 256) out0[e] = 0.0f;
+        for (int col = c0 + t; col < c1; col += 256) out0[col] = 0.0f;
         return;
     }
     const int r0 = lo / per, r1 = (hi - 1) / per;
     if (r0 == r1) return;
     const int n = r1 - r0 + 1;
     const bool first_tail = lo > r0 * per;
-    auto row_of = [&](int i, int g) -> int64_t {
-        return partial_row(r0 + i, i == 0 && first_tail, p.Hseg, grp) * NH + g;
-    };
-    const int g_t = t % NH;
-    const int elems = NH * HD;
-
-    if (n <= kMaxN && n * NH <= 256 && elems <= 256 * kMaxE) {
-        // Fast path: every load is issued before any reduction.
-        float m_t = -INFINITY, l_t = 0.0f;
-        if (t < n * NH) {
-            const int64_t row = row_of(t / NH, g_t);
-            m_t = p.ws_ml[row * 2];
-            l_t = p.ws_ml[row * 2 + 1];
-        }
-        float a[kMaxE][kMaxN];
-#pragma unroll
-        for (int k = 0; k < kMaxE; ++k) {
-            const int e = t + 256 * k;
-            const int g = e / HD, d = e - (e / HD) * HD;
-#pragma unroll
-            for (int i = 0; i < kMaxN; ++i)
-                a[k][i] = (e < elems && i < n) ? p.ws_acc[row_of(i, g) * HD + d] : 0.0f;
-        }
-        red[t] = m_t;
-        __syncthreads();
-        if (t < NH) {
-            float m = -INFINITY;
-            for (int i = 0; i < n; ++i) m = fmaxf(m, red[i * NH + t]);
-            M_s[t] = m == -INFINITY ? 0.0f : m;
-        }
-        __syncthreads();
-        const float w = t < n * NH ? fast_exp2(m_t - M_s[g_t]) : 0.0f;
-        w_s[t] = w;
-        red[t] = l_t * w;
-        __syncthreads();
-        if (t < NH) {
-            float l = 0.0f;
-            for (int i = 0; i < n; ++i) l += red[i * NH + t];
-            inv_s[t] = l > 0.0f ? 1.0f / l : 0.0f;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < kMaxE; ++k) {
-            const int e = t + 256 * k;
-            if (e < elems) {
-                const int g = e / HD;
-                float acc = 0.0f;
-#pragma unroll
-                for (int i = 0; i < kMaxN; ++i)
-                    if (i < n) acc = fmaf(w_s[i * NH + g], a[k][i], acc);
-                out0[e] = acc * inv_s[g];
-            }
-        }
+    if (n <= kMergeFew && cw <= 1024) {
+        // Few partials (long batches): thread t takes columns c0 + t,
+        // c0 + t + 256, ... with all n partials of each loaded at once.
+        if (cw <= 256) merge_few_n<1>(p, grp, r0, n, first_tail, out0, c0, c1);
+        else if (cw <= 512) merge_few_n<2>(p, grp, r0, n, first_tail, out0, c0, c1);
+        else merge_few_n<4>(p, grp, r0, n, first_tail, out0, c0, c1);
         return;
     }
-
-    // General path: any number of partials.
-    float mx = -INFINITY;
-    for (int idx = t; idx < n * NH; idx += 256) mx = fmaxf(mx, p.ws_ml[row_of(idx / NH, g_t) * 2]);
-    red[t] = mx;
-    __syncthreads();
-    if (t < NH) {
-        float m = -INFINITY;
-        for (int k = t; k < 256; k += NH) m = fmaxf(m, red[k]);
-        M_s[t] = m == -INFINITY ? 0.0f : m;
-    }
-    __syncthreads();
-    float lsum = 0.0f;
-    for (int idx = t; idx < n * NH; idx += 256) {
-        const int64_t row = row_of(idx / NH, g_t);
-        lsum += p.ws_ml[row * 2 + 1] * fast_exp2(p.ws_ml[row * 2] - M_s[g_t]);
-    }
-    red[t] = lsum;
-    __syncthreads();
-    if (t < NH) {
-        float l = 0.0f;
-        for (int k = t; k < 256; k += NH) l += red[k];
-        inv_s[t] = l > 0.0f ? 1.0f / l : 0.0f;
-    }
-    __syncthreads();
-
-    for (int e = t; e < elems; e += 256) {
-        const int g = e / HD, d = e - g * HD;
-        const float Mg = M_s[g];
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        int i = 0;
-        for (; i + 4 <= n; i += 4) {
+    // Many partials (short batches, one long sequence): 64 columns at a time,
+    // thread (c, pg) = (t % 64, t / 64) taking partials pg, pg + 4, ...
+    const int cl = t & 63, pg = t >> 6;
+    for (int sub = c0; sub < c1; sub += 64) {
+        const int col = sub + cl;
+        // 64 divides HD on the MFMA path; the generic path has one head per segment.
+        const int g = sub / HD;
+        const int d = min(col, c1 - 1) - g * HD;
+        auto row_of = [&](int i) -> int64_t {
+            return partial_row(r0 + i, i == 0 && first_tail, p.Hseg, grp) * NH + g;
+        };
+        float Mt = -INFINITY, Lt = 0.0f, At = 0.0f;  // this thread's partials
+        for (int base = pg; base < n; base += 32) {
+            float a[8], m[8], l[8];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int64_t row = row_of(i + u, g);
-                acc[u] = fmaf(fast_exp2(p.ws_ml[row * 2] - Mg), p.ws_acc[row * HD + d], acc[u]);
+            for (int k = 0; k < 8; ++k) {  // unconditional loads (clamped), masked below
+                const int64_t row = row_of(min(base + 4 * k, n - 1));
+                a[k] = p.ws_acc[row * HD + d];
+                m[k] = p.ws_ml[row * 2];
+                l[k] = p.ws_ml[row * 2 + 1];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (base + 4 * k >= n) m[k] = -INFINITY;
+            float mb = Mt;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) mb = fmaxf(mb, m[k]);
+            if (mb != -INFINITY) {
+                const float sc = fast_exp2(Mt - mb);  // 0 while Mt = -inf
+                Lt *= sc;
+                At *= sc;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float w = fast_exp2(m[k] - mb);
+                    Lt = fmaf(w, l[k], Lt);
+                    At = fmaf(w, a[k], At);
+                }
+                Mt = mb;
             }
         }
-        for (; i < n; ++i) {
-            const int64_t row = row_of(i, g);
-            acc[0] = fmaf(fast_exp2(p.ws_ml[row * 2] - Mg), p.ws_acc[row * HD + d], acc[0]);
+        __syncthreads();  // the previous sub-pass has read gm, gl, ga
+        if (cl == 0) {
+            gm[pg] = Mt;
+            gl[pg] = Lt;
         }
-        out0[e] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) * inv_s[g];
+        ga[pg][cl] = At;
+        __syncthreads();
+        if (pg == 0 && col < c1) {
+            const float M = fmaxf(fmaxf(gm[0], gm[1]), fmaxf(gm[2], gm[3]));
+            float L = 0.0f, A = 0.0f;
+            if (M != -INFINITY) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float w = fast_exp2(gm[q] - M);
+                    L = fmaf(w, gl[q], L);
+                    A = fmaf(w, ga[q][cl], A);
+                }
+            }
+            out0[col] = L > 0.0f ? A / L : 0.0f;
+        }
     }
 }
 
@@ -795,11 +831,22 @@ template <typename K>
 int launch_pair(K kern, int wpw, int max_per_simd, DecodeParams p, hipStream_t s, const char* name) {
     const size_t lds = sizeof(int) * (static_cast<size_t>(p.B) + 1);
     const int waves = resident_waves(kern, wpw, lds, max_per_simd);
-    p.ranges = std::max(1, waves / p.Hseg);
+    // No more ranges than the largest possible work needs (small batches and
+    // short contexts launch a small grid).
+    const int64_t max_work = static_cast<int64_t>(p.B) * p.max_blocks;
+    p.ranges = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(waves / p.Hseg, cdiv<int64_t>(max_work, p.min_per))));
     const unsigned groups = static_cast<unsigned>(p.ranges) * (p.Hseg / wpw);
     kern<<<groups, 64 * wpw, lds, s>>>(p);
     if (int rc = check_launch(name)) return rc;
-    decode_merge_kernel<<<static_cast<unsigned>(p.B) * p.Hseg, 256, 0, s>>>(p);
+    // Merge grid: about 1,024 workgroups.  Many segments -> one workgroup per
+    // segment; few (one long sequence) -> each segment split into 64-column
+    // slices merged side by side.
+    const int segs = p.B * p.Hseg;
+    const int c64 = cdiv(p.NH * p.HD, 64);
+    const int split = std::max(1, std::min(c64, 1024 / std::max(segs, 1)));
+    p.merge_cw = 64 * cdiv(c64, split);
+    const unsigned merge_groups = static_cast<unsigned>(segs) * cdiv(p.NH * p.HD, p.merge_cw);
+    decode_merge_kernel<<<merge_groups, 256, 0, s>>>(p);
     return check_launch("decode_merge_kernel");
 }
 
