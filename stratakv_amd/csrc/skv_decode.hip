@@ -116,6 +116,17 @@ __device__ WorkSplit build_split(const DecodeParams& p, int* P_s) {
         for (int b0 = 0; b0 < p.B; b0 += 64) {
             const int b = b0 + lane;
             int v = b < p.B ? seq_blocks(p, b) : 0;
+            if (blockIdx.x == 0) {
+                // Sequences without context produce zeros (workgroup 0 writes them).
+                uint64_t empty = __ballot(b < p.B && v == 0);
+                const int64_t row = static_cast<int64_t>(p.Hq) * p.HD;
+                while (empty != 0) {
+                    const int e = __builtin_ctzll(empty);
+                    empty &= empty - 1;
+                    float* o = p.out + static_cast<int64_t>(b0 + e) * row;
+                    for (int64_t i = lane; i < row; i += 64) o[i] = 0.0f;
+                }
+            }
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const int u = __shfl_up(v, o, 64);
@@ -619,8 +630,8 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
 // partials pg, pg + 4, ... of column c, 8 at a time with all their loads in
 // flight, and keeps its own (max, sum, acc) triple, rescaled per batch; the 4
 // partial groups are combined the same way through LDS.  Segments held by one
-// range were finalised by the attention kernel; sequences without context get
-// zeros.
+// range, and sequences without context, were written by the attention kernel;
+// with a single range the merge is not launched at all.
 // ---------------------------------------------------------------------------
 constexpr int kMergeFew = 8;   // partials merged by one workgroup per segment
 
@@ -697,10 +708,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
     const int32_t* P = p.plan + 3;
     const int lo = P[b], hi = P[b + 1];
     float* out0 = p.out + (static_cast<int64_t>(b) * p.Hq + grp * NH) * HD;
-    if (lo == hi) {
-        for (int col = c0 + t; col < c1; col += 256) out0[col] = 0.0f;
-        return;
-    }
+    if (lo == hi) return;  // no context: zeroed by the attention kernel
     const int r0 = lo / per, r1 = (hi - 1) / per;
     if (r0 == r1) return;
     const int n = r1 - r0 + 1;
@@ -838,6 +846,7 @@ int launch_pair(K kern, int wpw, int max_per_simd, DecodeParams p, hipStream_t s
     const unsigned groups = static_cast<unsigned>(p.ranges) * (p.Hseg / wpw);
     kern<<<groups, 64 * wpw, lds, s>>>(p);
     if (int rc = check_launch(name)) return rc;
+    if (p.ranges == 1) return SKV_OK;  // one range: no segment is cut, nothing to merge
     // Merge grid: about 1,024 workgroups.  Many segments -> one workgroup per
     // segment; few (one long sequence) -> each segment split into 64-column
     // slices merged side by side.
