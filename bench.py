@@ -452,6 +452,21 @@ def run_cfg1(steps: int, warmup: int, with_cpu: bool):
                      "frac": round(gbs / HBM_PEAK_GBS, 6), "traffic": None,
                      "algorithmic_bytes": nbytes},
     }
+    # The whole layer stack through the C++ API (TransformerBlock::forward_into
+    # of every layer per token), when the driver is built.
+    driver = os.path.join(ROOT, "build", "bin", "bench_layer_stack")
+    if os.path.exists(driver):
+        import subprocess
+        proc = subprocess.run([driver, str(layers), str(P), "1"], stdout=subprocess.PIPE,
+                              stderr=subprocess.PIPE, text=True, timeout=600)
+        if proc.returncode == 0:
+            stack = json.loads(proc.stdout.strip().splitlines()[-1])
+            line["layer_stack"] = dict(stack, note=(
+                "end-to-end forward_into of 22 TinyLlama-shaped layers per token (bf16 N(0,0.02) "
+                "weights, GEMVs, norms, RoPE, fused append + decode, SwiGLU, residuals); "
+                "embedding, lm_head and sampling are not part of this build"))
+        else:
+            log(f"layer stack driver failed ({proc.returncode}): {proc.stderr.strip()[-300:]}")
     if with_cpu:
         import oracle
         # One layer's 144 single-sequence decodes with the oracle, scaled to 22 layers.

@@ -92,6 +92,10 @@ int skv_scatter_i32(int32_t* dst, const int32_t* pairs, int n, void* stream);
  * counter hash (no library RNG), so any sub-range can be regenerated alone. */
 int skv_fill_normal_bf16(uint16_t* dst, size_t count, uint64_t seed,
                          uint64_t first_index, void* stream);
+/* The same with each sample scaled by stddev before rounding (random-init
+ * weights, e.g. N(0, 0.02)). */
+int skv_fill_normal_scaled_bf16(uint16_t* dst, size_t count, uint64_t seed,
+                                uint64_t first_index, float stddev, void* stream);
 /* Fill count elements of a bf16 buffer with one 16-bit pattern. */
 int skv_fill_u16(uint16_t* dst, size_t count, uint16_t value, void* stream);
 

@@ -68,6 +68,7 @@ _PROTOS = {
     "skv_memcpy_h2d_async": (_i32, [_vp, _vp, _sz, _vp]),
     "skv_scatter_i32": (_i32, [_vp, _vp, _i32, _vp]),
     "skv_fill_normal_bf16": (_i32, [_vp, _sz, _u64, _u64, _vp]),
+    "skv_fill_normal_scaled_bf16": (_i32, [_vp, _sz, _u64, _u64, _f32, _vp]),
     "skv_fill_u16": (_i32, [_vp, _sz, _c.c_uint16, _vp]),
     "skv_kv_append": (_i32, [_vp, _vp, _i32, _vp, _vp, _i64, _vp, _i32, _vp, _vp,
                              _i32, _i32, _i32, _i32, _i32, _vp]),

@@ -5,7 +5,8 @@ Everything is compiled in-tree so the built files travel with the source tree:
 * ``stratakv_amd/libstratakv_amd.so`` -- the gfx950 HIP kernels, the C ABI
   (``include/stratakv_amd.h``) and the C++17 host layer (``include/stratakv/``),
   built with ``hipcc --offload-arch=gfx950``.
-* ``build/bin/*`` -- the C++ test programs under ``tests/cpp``.
+* ``build/bin/test_*`` -- the C++ test programs under ``tests/cpp``;
+  ``build/bin/bench_*`` -- the C++ benchmark drivers under ``stratakv_amd/csrc/bench``.
 * ``oracle/liboracle.so`` and, when the StrataKV sources are present,
   ``oracle/_ref/libstratakv_ref.so`` -- test infrastructure (``oracle/Makefile``).
 """
@@ -81,6 +82,19 @@ def build_cpp_tests() -> list[str]:
     return outs
 
 
+def build_bench() -> list[str]:
+    """Compile the C++ benchmark drivers (stratakv_amd/csrc/bench/*.cpp) into
+    build/bin/bench_<name>; they use only the library's public headers."""
+    os.makedirs(BIN, exist_ok=True)
+    outs = []
+    for src in sorted(glob.glob(os.path.join(CSRC, "bench", "*.cpp"))):
+        exe = os.path.join(BIN, "bench_" + os.path.splitext(os.path.basename(src))[0])
+        _run([CXX, "-O2", "-std=c++17", "-Wall", f"-I{INCLUDE}", src, f"-L{PKG}", "-lstratakv_amd",
+              f"-Wl,-rpath,{PKG}", "-o", exe])
+        outs.append(exe)
+    return outs
+
+
 def build_oracle() -> None:
     """Test infrastructure: the C oracle, plus the reference checker when present."""
     _run(["make", "-B", "-C", ORACLE, "all"])
@@ -90,6 +104,7 @@ def build_oracle() -> None:
 
 def build_all() -> None:
     build_library()
+    build_bench()
     build_oracle()
     build_cpp_tests()
 

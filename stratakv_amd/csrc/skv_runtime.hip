@@ -58,7 +58,7 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
 }
 
 __global__ void fill_normal_bf16_kernel(uint16_t* __restrict__ dst, size_t count,
-                                        uint64_t seed, uint64_t first) {
+                                        uint64_t seed, uint64_t first, float stddev) {
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
     for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
          i < count; i += stride) {
@@ -69,7 +69,7 @@ __global__ void fill_normal_bf16_kernel(uint16_t* __restrict__ dst, size_t count
                          (1.0f / 16777216.0f);                      // [0, 1)
         const float r = sqrtf(-2.0f * logf(u1));
         const float z = r * cospif(2.0f * u2);
-        dst[i] = static_cast<uint16_t>(f32_to_bf16_bits(z));
+        dst[i] = static_cast<uint16_t>(f32_to_bf16_bits(z * stddev));
     }
 }
 
@@ -260,7 +260,18 @@ int skv_fill_normal_bf16(uint16_t* dst, size_t count, uint64_t seed, uint64_t fi
     SKV_REQUIRE(dst != nullptr, "skv_fill_normal_bf16: NULL destination");
     const unsigned grid = static_cast<unsigned>(std::min<size_t>(cdiv<size_t>(count, 256), 16384));
     fill_normal_bf16_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
-        dst, count, seed, first_index);
+        dst, count, seed, first_index, 1.0f);
+    return check_launch("fill_normal_bf16_kernel");
+}
+
+int skv_fill_normal_scaled_bf16(uint16_t* dst, size_t count, uint64_t seed, uint64_t first_index,
+                                float stddev, void* stream) {
+    if (count == 0) return SKV_OK;
+    SKV_REQUIRE(dst != nullptr, "skv_fill_normal_scaled_bf16: NULL destination");
+    SKV_REQUIRE(std::isfinite(stddev), "skv_fill_normal_scaled_bf16: stddev must be finite");
+    const unsigned grid = static_cast<unsigned>(std::min<size_t>(cdiv<size_t>(count, 256), 16384));
+    fill_normal_bf16_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+        dst, count, seed, first_index, stddev);
     return check_launch("fill_normal_bf16_kernel");
 }
 
