@@ -241,6 +241,41 @@ int skv_swiglu_f32(float* gate, const float* up, int n, void* stream);
 /* target[i] += source[i]. */
 int skv_add_f32(float* target, const float* source, int n, void* stream);
 
+/* Fused projections of one decode step (a single token), each one launch and
+ * bit-identical to the separate kernels above on the same inputs.  Weights
+ * must be output-major rows (stride_k == 1: the transpose view of a checkpoint
+ * [out][in] matrix), 16-byte aligned, with in_dim <= 8192; otherwise the call
+ * returns SKV_ERR_UNSUPPORTED and changes nothing (use the separate kernels).
+ * The outputs must not alias the input x / hidden.
+ *
+ * q, k, v = (rmsnorm(hidden; gamma) W_q, W_k, W_v) + bias; with position >= 0
+ * q and k are then rotated like skv_rope_f32 at that position (gamma NULL: no
+ * normalisation).  stride_n[3]: row strides of W_q, W_k, W_v.
+ * Replaces: rmsnorm_cuda + 3 x Linear::forward_into + generate_rope_frequencies
+ * + 2 x rope_split_half_cuda (src/models/transformer_block.cpp:432-474). */
+int skv_fused_qkv_f32(const float* hidden, const float* gamma, float epsilon,
+                      const void* wq, const void* wk, const void* wv, int weight_dtype,
+                      int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
+                      const float* bias_k, const float* bias_v, int hidden_dim,
+                      int num_heads, int num_kv_heads, int head_dim, int position,
+                      float* q, float* k, float* v, void* stream);
+/* act[n] = swiglu(gate_n, up_n), gate/up = rmsnorm(x; gamma) W + bias.
+ * Replaces: rmsnorm_cuda + gate/up Linear::forward_into + swiglu_inplace_cuda
+ * (src/models/transformer_block.cpp:542-575). */
+int skv_fused_gate_up_swiglu_f32(const float* x, const float* gamma, float epsilon,
+                                 const void* w_gate, const void* w_up, int weight_dtype,
+                                 int64_t stride_k, int64_t stride_n_gate,
+                                 int64_t stride_n_up, const float* bias_gate,
+                                 const float* bias_up, int in_dim, int out_dim,
+                                 float* act, void* stream);
+/* y = x W + bias + residual (y may alias residual).
+ * Replaces: Linear::forward_into + add_inplace_cuda of o_proj and of
+ * down_proj (src/models/transformer_block.cpp:528-541, 582-594). */
+int skv_linear_residual_f32(const float* x, const void* weight, int weight_dtype,
+                            int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
+                            const float* bias, const float* residual, float* y,
+                            void* stream);
+
 /* ---- test support --------------------------------------------------------
  * Copy the blocks listed in table[0..num_blocks) of a pool into a contiguous
  * device buffer dst[num_blocks][block_elems] (so one sequence can be read back

@@ -91,6 +91,11 @@ _PROTOS = {
     "skv_rope_f32": (_i32, [_vp, _i32, _i32, _i32, _vp]),
     "skv_swiglu_f32": (_i32, [_vp, _vp, _i32, _vp]),
     "skv_add_f32": (_i32, [_vp, _vp, _i32, _vp]),
+    "skv_fused_qkv_f32": (_i32, [_vp, _vp, _f32, _vp, _vp, _vp, _i32, _i64, _c.POINTER(_c.c_int64),
+                                 _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "skv_fused_gate_up_swiglu_f32": (_i32, [_vp, _vp, _f32, _vp, _vp, _i32, _i64, _i64, _i64, _vp,
+                                            _vp, _i32, _i32, _vp, _vp]),
+    "skv_linear_residual_f32": (_i32, [_vp, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
 }
 
 _lib = None

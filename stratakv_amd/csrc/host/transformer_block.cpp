@@ -2,7 +2,9 @@
 // The GPU decode step follows src/models/transformer_block.cpp:334-613 of the
 // reference sub-step for sub-step; the KV append and the paged decode are the
 // hot path (skv_paged_attention_decode_append: append + decode in one launch); the other
-// sub-steps use the simple kernels of skv_layer_ops.hip.
+// sub-steps run as fused projections (norm + q/k/v + RoPE, o_proj + residual,
+// norm + gate/up + SwiGLU, down_proj + residual) when the weights are aligned
+// output-major rows, else as the separate kernels of skv_layer_ops.hip.
 #include "stratakv/models/transformer_block.h"
 
 #include <cmath>
@@ -166,14 +168,44 @@ void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output,
     Tensor& up = *up_workspace_;
     Tensor& down = *down_workspace_;
 
-    detail::check(skv_rmsnorm_f32(cfp(hidden_states), fp(normalized_input), cfp(norm1_.gamma()), 1, hidden,
-                                  norm1_.epsilon(), s),
-                  "forward_into: input rmsnorm");
-    linear(attention_.query_projection(), normalized_input, queries, "forward_into: q_proj");
-    linear(attention_.key_projection(), normalized_input, keys, "forward_into: k_proj");
-    linear(attention_.value_projection(), normalized_input, values, "forward_into: v_proj");
-    detail::check(skv_rope_f32(fp(queries), num_heads, head_dim, position, s), "forward_into: rope q");
-    detail::check(skv_rope_f32(fp(keys), num_kv_heads, head_dim, position, s), "forward_into: rope k");
+    auto wdtype = [](const layers::Linear& l) {
+        return l.weight().dtype() == DataType::BF16 ? SKV_DTYPE_BF16 : SKV_DTYPE_FP32;
+    };
+    auto stride_k = [](const layers::Linear& l) { return static_cast<int64_t>(l.weight().strides()[0]); };
+    auto stride_n = [](const layers::Linear& l) { return static_cast<int64_t>(l.weight().strides()[1]); };
+    auto bias_of = [&](const layers::Linear& l) { return l.bias() ? cfp(*l.bias()) : nullptr; };
+    // A fused call returns SKV_ERR_UNSUPPORTED (doing nothing) for weights that
+    // are not aligned output-major rows; the separate kernels then run.
+    auto fused = [](int rc, const char* what) {
+        if (rc == SKV_ERR_UNSUPPORTED) return false;
+        detail::check(rc, what);
+        return true;
+    };
+    const layers::Linear& wq = attention_.query_projection();
+    const layers::Linear& wk = attention_.key_projection();
+    const layers::Linear& wv = attention_.value_projection();
+    const layers::Linear& wo = attention_.output_projection();
+    const bool same_dtype = wdtype(wq) == wdtype(wk) && wdtype(wq) == wdtype(wv) &&
+                            stride_k(wq) == stride_k(wk) && stride_k(wq) == stride_k(wv);
+
+    // Input RMSNorm, q/k/v projections and RoPE at `position`.
+    const int64_t qkv_strides[3] = {stride_n(wq), stride_n(wk), stride_n(wv)};
+    if (!(same_dtype &&
+          fused(skv_fused_qkv_f32(cfp(hidden_states), cfp(norm1_.gamma()), norm1_.epsilon(),
+                                  wq.weight().raw_data(), wk.weight().raw_data(), wv.weight().raw_data(),
+                                  wdtype(wq), stride_k(wq), qkv_strides, bias_of(wq), bias_of(wk),
+                                  bias_of(wv), hidden, num_heads, num_kv_heads, head_dim, position,
+                                  fp(queries), fp(keys), fp(values), s),
+                "forward_into: fused rmsnorm + q/k/v + rope"))) {
+        detail::check(skv_rmsnorm_f32(cfp(hidden_states), fp(normalized_input), cfp(norm1_.gamma()), 1,
+                                      hidden, norm1_.epsilon(), s),
+                      "forward_into: input rmsnorm");
+        linear(wq, normalized_input, queries, "forward_into: q_proj");
+        linear(wk, normalized_input, keys, "forward_into: k_proj");
+        linear(wv, normalized_input, values, "forward_into: v_proj");
+        detail::check(skv_rope_f32(fp(queries), num_heads, head_dim, position, s), "forward_into: rope q");
+        detail::check(skv_rope_f32(fp(keys), num_kv_heads, head_dim, position, s), "forward_into: rope k");
+    }
 
     // The paged-KV hot path: device block table (only new block ids are
     // uploaded), then one launch that appends this token's K/V rows at
@@ -188,19 +220,42 @@ void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output,
                       ws.num_elements() * ws.element_size(), s),
                   "forward_into: KV append + paged attention");
 
-    linear(attention_.output_projection(), context, down, "forward_into: o_proj");
-    // Residual: reads hidden_states before output is written (aliasing-safe).
-    detail::check(skv_add_f32(fp(down), cfp(hidden_states), hidden, s), "forward_into: residual");
-    detail::check(skv_rmsnorm_f32(cfp(down), fp(normalized_residual), cfp(norm2_.gamma()), 1, hidden,
-                                  norm2_.epsilon(), s),
-                  "forward_into: post-attention rmsnorm");
-    linear(gate_proj_, normalized_residual, gate, "forward_into: gate_proj");
-    linear(up_proj_, normalized_residual, up, "forward_into: up_proj");
-    detail::check(skv_swiglu_f32(fp(gate), cfp(up), inter, s), "forward_into: swiglu");
-    linear(down_proj_, gate, context, "forward_into: down_proj");
-    detail::check(skv_add_f32(fp(down), cfp(context), hidden, s), "forward_into: residual");
-    detail::check(skv_memcpy_d2d(output.raw_data(), down.raw_data(), hidden_dim_ * sizeof(float), s),
-                  "forward_into: output copy");
+    // o_proj + residual: reads hidden_states before output is written
+    // (aliasing-safe).  down holds h = hidden + attention output.
+    if (!fused(skv_linear_residual_f32(cfp(context), wo.weight().raw_data(), wdtype(wo), stride_k(wo),
+                                       stride_n(wo), static_cast<int>(wo.input_dim()),
+                                       static_cast<int>(wo.output_dim()), bias_of(wo),
+                                       cfp(hidden_states), fp(down), s),
+               "forward_into: fused o_proj + residual")) {
+        linear(wo, context, down, "forward_into: o_proj");
+        detail::check(skv_add_f32(fp(down), cfp(hidden_states), hidden, s), "forward_into: residual");
+    }
+    // Post-attention RMSNorm, gate/up projections and SwiGLU.
+    const bool ffn_same = wdtype(gate_proj_) == wdtype(up_proj_) && stride_k(gate_proj_) == stride_k(up_proj_);
+    if (!(ffn_same &&
+          fused(skv_fused_gate_up_swiglu_f32(cfp(down), cfp(norm2_.gamma()), norm2_.epsilon(),
+                                             gate_proj_.weight().raw_data(), up_proj_.weight().raw_data(),
+                                             wdtype(gate_proj_), stride_k(gate_proj_), stride_n(gate_proj_),
+                                             stride_n(up_proj_), bias_of(gate_proj_), bias_of(up_proj_),
+                                             hidden, inter, fp(gate), s),
+                "forward_into: fused rmsnorm + gate/up + swiglu"))) {
+        detail::check(skv_rmsnorm_f32(cfp(down), fp(normalized_residual), cfp(norm2_.gamma()), 1, hidden,
+                                      norm2_.epsilon(), s),
+                      "forward_into: post-attention rmsnorm");
+        linear(gate_proj_, normalized_residual, gate, "forward_into: gate_proj");
+        linear(up_proj_, normalized_residual, up, "forward_into: up_proj");
+        detail::check(skv_swiglu_f32(fp(gate), cfp(up), inter, s), "forward_into: swiglu");
+    }
+    // down_proj + residual straight into output (hidden_states is not read any more).
+    if (!fused(skv_linear_residual_f32(cfp(gate), down_proj_.weight().raw_data(), wdtype(down_proj_),
+                                       stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
+                                       bias_of(down_proj_), cfp(down), fp(output), s),
+               "forward_into: fused down_proj + residual")) {
+        linear(down_proj_, gate, context, "forward_into: down_proj");
+        detail::check(skv_add_f32(fp(down), cfp(context), hidden, s), "forward_into: residual");
+        detail::check(skv_memcpy_d2d(output.raw_data(), down.raw_data(), hidden_dim_ * sizeof(float), s),
+                      "forward_into: output copy");
+    }
 }
 
 }  // namespace models

@@ -19,22 +19,59 @@
 
 namespace skv {
 
+// Loads of 256-thread loops over n elements, 8 per thread in flight: element
+// i0 + 256 u of chunk i0 (clamped into range, so every load is issued
+// unconditionally; callers ignore the clamped lanes).
+constexpr int kChunk = 8;
+
+__device__ __forceinline__ void load_chunk(const float* src, int i0, int n, float (&v)[kChunk]) {
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) v[u] = src[min(i0 + 256 * u, n - 1)];
+}
+
+// Copies n floats into LDS (256 threads).
+__device__ __forceinline__ void stage_to_lds(const float* src, float* dst, int n) {
+    for (int i0 = threadIdx.x; i0 < n; i0 += 256 * kChunk) {
+        float v[kChunk];
+        load_chunk(src, i0, n, v);
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u)
+            if (i0 + 256 * u < n) dst[i0 + 256 * u] = v[u];
+    }
+}
+
+// 1 / sqrt(mean(x^2) + eps) of n values (256 threads, `red` = 4 floats of
+// LDS): thread t sums x[t], x[t + 256], ... in that order with fma, then the
+// wavefront and the 4 wavefronts are reduced.  rmsnorm_kernel and the fused
+// projections use this same order, so they normalise to the same bits.
+template <typename Get>
+__device__ __forceinline__ float rms_inverse(Get get, int n, float eps, float* red) {
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = get(i);
+        ss = fmaf(v, v, ss);
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = (red[0] + red[1]) + (red[2] + red[3]);
+    return 1.0f / sqrtf(total / static_cast<float>(n) + eps);
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ in,
                                                       float* __restrict__ out,
                                                       const float* __restrict__ gamma, int n,
                                                       float eps) {
+    extern __shared__ float xg_s[];  // [2][n]: the row and gamma
     __shared__ float red[4];
     const int row = blockIdx.x;
     const float* x = in + static_cast<int64_t>(row) * n;
     float* y = out + static_cast<int64_t>(row) * n;
-    float s = 0.0f;
-    for (int i = threadIdx.x; i < n; i += 256) s = fmaf(x[i], x[i], s);
-    s = wave_sum(s);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    stage_to_lds(x, xg_s, n);
+    stage_to_lds(gamma, xg_s + n, n);
     __syncthreads();
-    const float total = (red[0] + red[1]) + (red[2] + red[3]);
-    const float inv = 1.0f / sqrtf(total / static_cast<float>(n) + eps);
-    for (int i = threadIdx.x; i < n; i += 256) y[i] = x[i] * inv * gamma[i];
+    const float inv = rms_inverse([&](int i) { return xg_s[i]; }, n, eps, red);
+    for (int i = threadIdx.x; i < n; i += 256) y[i] = xg_s[i] * inv * xg_s[n + i];
 }
 
 template <bool BF16W>
@@ -59,82 +96,130 @@ constexpr int kGemvRowsPerWave = 2;    // output rows per wavefront
 constexpr int kGemvUnroll = 4;         // 16-byte loads per row in flight
 constexpr int kGemvMaxLdsK = 8192;     // x staged in LDS up to this many inputs
 
+// Dot products of x (K floats, LDS or global) with two output-major weight
+// rows (byte pointers, 16-byte aligned, K elements each; r1 may repeat r0), by
+// one wavefront: 16 bytes per lane per load, kGemvUnroll loads per row issued
+// together, fp32 accumulation, then a wave reduction.  Every caller computes a
+// row with exactly this arithmetic, so fused and separate projections give
+// the same bits.  The loads of the first kGemvUnroll steps are issued by
+// PairPrefetch before x is needed (callers stage x meanwhile).
+template <bool BF16W>
+struct PairPrefetch {
+    static constexpr int EPL = BF16W ? 8 : 4;    // elements per 16-byte load
+    static constexpr int STEP = 64 * EPL;        // elements per wave-wide load
+    static constexpr int64_t ESZ = BF16W ? 2 : 4;
+    const char* rows[2];
+    uint4 q[2][kGemvUnroll];
+    bool full;                                   // K holds the first kGemvUnroll steps
+
+    __device__ __forceinline__ PairPrefetch(const char* r0, const char* r1, int K, int lane) {
+        rows[0] = r0;
+        rows[1] = r1;
+        full = kGemvUnroll * STEP <= K;
+        if (full) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int u = 0; u < kGemvUnroll; ++u)
+                    q[j][u] = *reinterpret_cast<const uint4*>(rows[j] + (u * STEP + lane * EPL) * ESZ);
+        }
+    }
+
+    __device__ __forceinline__ void accumulate(const float* xr, int k0, int lane, float (&acc)[2]) const {
+#pragma unroll
+        for (int u = 0; u < kGemvUnroll; ++u) {
+            float xv[EPL];
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) xv[e] = xr[k0 + u * STEP + lane * EPL + e];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float f[EPL];
+                widen16<BF16W>(q[j][u], f);
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[j] = fmaf(xv[e], f[e], acc[j]);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void finish(const float* xr, int K, int lane, float& out0, float& out1) {
+        float acc[2] = {0.0f, 0.0f};
+        int k0 = 0;
+        if (full) {
+            accumulate(xr, 0, lane, acc);
+            k0 = kGemvUnroll * STEP;
+        }
+        for (; k0 + kGemvUnroll * STEP <= K; k0 += kGemvUnroll * STEP) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int u = 0; u < kGemvUnroll; ++u)
+                    q[j][u] = *reinterpret_cast<const uint4*>(rows[j] + (k0 + u * STEP + lane * EPL) * ESZ);
+            accumulate(xr, k0, lane, acc);
+        }
+        for (int k = k0 + lane * EPL; k + EPL <= K; k += STEP) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float f[EPL];
+                widen16<BF16W>(*reinterpret_cast<const uint4*>(rows[j] + k * ESZ), f);
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[j] = fmaf(xr[k + e], f[e], acc[j]);
+            }
+        }
+        for (int k = K - K % EPL + lane; k < K; k += 64)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[j] = fmaf(xr[k], weight_at<BF16W>(rows[j], k), acc[j]);
+        out0 = wave_sum(acc[0]);
+        out1 = wave_sum(acc[1]);
+    }
+};
+
+template <bool BF16W>
+__device__ __forceinline__ void gemv_pair(const float* xr, const char* r0, const char* r1, int K,
+                                          int lane, float& out0, float& out1) {
+    PairPrefetch<BF16W> pf(r0, r1, K, lane);
+    pf.finish(xr, K, lane, out0, out1);
+}
+
 // Output-major weights (stride_k == 1, 16-byte aligned rows): output n is the
-// dot product of x with the contiguous row n.  One wavefront per 2 rows, 16
-// bytes per lane per load with 4 loads per row issued together (8 KiB in
-// flight per wavefront); x is staged once per workgroup in LDS.  Further rows
-// of x (tokens) read the weights again, from L2.
+// dot product of x with the contiguous row n.  One wavefront per 2 rows
+// (gemv_pair: 8 KiB in flight per wavefront); x is staged once per workgroup
+// in LDS.  Further rows of x (tokens) read the weights again, from L2.
 template <bool BF16W>
 __global__ __launch_bounds__(256) void gemv_rows_vec_kernel(const float* __restrict__ x, int rows,
                                                             const void* __restrict__ w,
                                                             int64_t stride_n, int K, int N,
                                                             const float* __restrict__ bias,
                                                             float* __restrict__ y) {
-    constexpr int EPL = BF16W ? 8 : 4;           // elements per 16-byte load
-    constexpr int STEP = 64 * EPL;               // elements per wave-wide load
     extern __shared__ float x_s[];               // [rows][K] when it fits
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int n0 = wave * kGemvRowsPerWave;
+    const int n0 = min(wave * kGemvRowsPerWave, N - 1);  // waves past N redo row N-1, store nothing
+    const int n1 = min(n0 + 1, N - 1);
+    const char* wb = static_cast<const char*>(w);
+    const int64_t rb = stride_n * (BF16W ? 2 : 4);
     const bool lds_x = static_cast<int64_t>(rows) * K <= kGemvMaxLdsK;
+    const int nx = rows * K;
+    // Issue order: the first chunk of x, then the weights (see fused_gemv_kernel).
+    float xv[kChunk];
+    if (lds_x) load_chunk(x, threadIdx.x, nx, xv);
+    PairPrefetch<BF16W> pf(wb + n0 * rb, wb + n1 * rb, K, lane);
     if (lds_x) {
-        for (int i = threadIdx.x; i < rows * K; i += 256) x_s[i] = x[i];
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u)
+            if (threadIdx.x + 256 * u < nx) x_s[threadIdx.x + 256 * u] = xv[u];
+        if (nx > 256 * kChunk) stage_to_lds(x + 256 * kChunk, x_s + 256 * kChunk, nx - 256 * kChunk);
         __syncthreads();
     }
-    if (n0 >= N) return;
-    const int nrows = min(kGemvRowsPerWave, N - n0);
-    const char* wb = static_cast<const char*>(w);
-    const int64_t esz = BF16W ? 2 : 4;
+    if (wave * kGemvRowsPerWave >= N) return;
     for (int r = 0; r < rows; ++r) {
         const float* xr = lds_x ? x_s + static_cast<int64_t>(r) * K : x + static_cast<int64_t>(r) * K;
-        float acc[kGemvRowsPerWave] = {};
-        int k0 = 0;
-        // Main part: kGemvUnroll full wave-wide steps, every load unconditional.
-        for (; k0 + kGemvUnroll * STEP <= K; k0 += kGemvUnroll * STEP) {
-            uint4 q[kGemvRowsPerWave][kGemvUnroll];
-#pragma unroll
-            for (int j = 0; j < kGemvRowsPerWave; ++j) {
-                const int n = n0 + min(j, nrows - 1);
-#pragma unroll
-                for (int u = 0; u < kGemvUnroll; ++u)
-                    q[j][u] = *reinterpret_cast<const uint4*>(
-                        wb + (static_cast<int64_t>(n) * stride_n + k0 + u * STEP + lane * EPL) * esz);
-            }
-#pragma unroll
-            for (int u = 0; u < kGemvUnroll; ++u) {
-                float xv[EPL];
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) xv[e] = xr[k0 + u * STEP + lane * EPL + e];
-#pragma unroll
-                for (int j = 0; j < kGemvRowsPerWave; ++j) {
-                    float f[EPL];
-                    widen16<BF16W>(q[j][u], f);
-#pragma unroll
-                    for (int e = 0; e < EPL; ++e) acc[j] = fmaf(xv[e], f[e], acc[j]);
-                }
-            }
-        }
-        // Tail: whole 16-byte chunks, then single elements.
-        for (int k = k0 + lane * EPL; k + EPL <= K; k += STEP) {
-#pragma unroll
-            for (int j = 0; j < kGemvRowsPerWave; ++j) {
-                if (j >= nrows) break;
-                float f[EPL];
-                widen16<BF16W>(*reinterpret_cast<const uint4*>(
-                                   wb + (static_cast<int64_t>(n0 + j) * stride_n + k) * esz), f);
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) acc[j] = fmaf(xr[k + e], f[e], acc[j]);
-            }
-        }
-        const int kt = K - K % EPL;
-        for (int k = kt + lane; k < K; k += 64)
-            for (int j = 0; j < nrows; ++j)
-                acc[j] = fmaf(xr[k], weight_at<BF16W>(w, static_cast<int64_t>(n0 + j) * stride_n + k), acc[j]);
-#pragma unroll
-        for (int j = 0; j < kGemvRowsPerWave; ++j) {
-            const float v = wave_sum(acc[j]);
-            if (lane == 0 && j < nrows)
-                y[static_cast<int64_t>(r) * N + n0 + j] = v + (bias ? bias[n0 + j] : 0.0f);
+        float a0, a1;
+        if (r == 0) pf.finish(xr, K, lane, a0, a1);
+        else gemv_pair<BF16W>(xr, wb + n0 * rb, wb + n1 * rb, K, lane, a0, a1);
+        if (lane == 0) {
+            y[static_cast<int64_t>(r) * N + n0] = a0 + (bias ? bias[n0] : 0.0f);
+            if (n1 != n0) y[static_cast<int64_t>(r) * N + n1] = a1 + (bias ? bias[n1] : 0.0f);
         }
     }
 }
@@ -196,16 +281,28 @@ __global__ __launch_bounds__(256) void gemv_cols_kernel(const float* __restrict_
             ((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane])) + (bias ? bias[n] : 0.0f);
 }
 
+// cos and sin of pair `pair` of a head_dim-hd head at `position`: inverse
+// frequency 10000^(-2 pair / hd) rounded to float, angle in double.
+__device__ __forceinline__ void rope_cos_sin(int pair, int hd, int position, float& c, float& s) {
+    const float inv = static_cast<float>(pow(10000.0, -2.0 * pair / static_cast<double>(hd)));
+    const double angle = static_cast<double>(position) * static_cast<double>(inv);
+    c = static_cast<float>(cos(angle));
+    s = static_cast<float>(sin(angle));
+}
+
+__device__ __forceinline__ float swiglu_of(float g, float u) {
+    const float sig = g >= 0.0f ? 1.0f / (1.0f + expf(-g)) : expf(g) / (1.0f + expf(g));
+    return g * sig * u;
+}
+
 __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ x, int heads, int hd,
                                                    int position) {
     const int half = hd / 2;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= heads * half) return;
     const int h = i / half, pair = i - h * half;
-    const float inv = static_cast<float>(pow(10000.0, -2.0 * pair / static_cast<double>(hd)));
-    const double angle = static_cast<double>(position) * static_cast<double>(inv);
-    const float c = static_cast<float>(cos(angle));
-    const float s = static_cast<float>(sin(angle));
+    float c, s;
+    rope_cos_sin(pair, hd, position, c, s);
     float* p = x + static_cast<int64_t>(h) * hd;
     const float a = p[pair], b = p[pair + half];
     p[pair] = a * c - b * s;
@@ -216,15 +313,148 @@ __global__ __launch_bounds__(256) void swiglu_kernel(float* __restrict__ gate,
                                                      const float* __restrict__ up, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const float g = gate[i];
-    const float sig = g >= 0.0f ? 1.0f / (1.0f + expf(-g)) : expf(g) / (1.0f + expf(g));
-    gate[i] = g * sig * up[i];
+    gate[i] = swiglu_of(gate[i], up[i]);
 }
 
 __global__ __launch_bounds__(256) void add_kernel(float* __restrict__ t, const float* __restrict__ s,
                                                   int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) t[i] += s[i];
+}
+
+// ---------------------------------------------------------------------------
+// Fused projections of the decode step (single token).  Each workgroup stages
+// the input in LDS, RMS-normalised on the way when gamma is given (the same
+// reduction and rounding as rmsnorm_kernel), and every wavefront computes two
+// output rows with gemv_pair; the epilogue then applies what the separate
+// kernels would, to the same values:
+//   QKV       q, k, v projections of the normalised input; with position >= 0
+//             a wavefront of q or k takes rows (i, i + hd/2) of one head and
+//             rotates them (rope_kernel's arithmetic) before storing;
+//   GATE_UP   gate row n and up row n of the normalised input -> swiglu;
+//   RESIDUAL  y = W x + residual (o_proj and down_proj with their residual add).
+// Bias, when present, is added before the rotation, as Linear::forward_into
+// does before the RoPE step.
+// ---------------------------------------------------------------------------
+enum FusedMode : int { FUSED_QKV = 0, FUSED_GATE_UP = 1, FUSED_RESIDUAL = 2 };
+
+struct FusedGemv {
+    const float* x;
+    const float* gamma;       // nullptr: no normalisation
+    float eps;
+    int K;
+    const void* w[3];
+    int64_t row_bytes[3];     // byte stride between output rows
+    const float* bias[3];
+    int n[3];                 // output rows per matrix
+    float* y[3];
+    int head_dim;             // QKV
+    int position;             // QKV: RoPE position, < 0 = none
+    const float* residual;    // RESIDUAL
+};
+
+template <bool BF16W, int MODE>
+__global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
+    extern __shared__ float x_s[];  // [K] input (+ [K] gamma while normalising)
+    __shared__ float red[4];
+    const int t = threadIdx.x, lane = t & 63;
+    const int K = f.K;
+    const int item = blockIdx.x * 4 + (t >> 6);
+    auto row_ptr = [&](int m, int r) {
+        return static_cast<const char*>(f.w[m]) + static_cast<int64_t>(r) * f.row_bytes[m];
+    };
+    auto bias_of = [&](int m, int r) { return f.bias[m] != nullptr ? f.bias[m][r] : 0.0f; };
+    // This wavefront's two rows (matrix ma row ra, matrix mb row rb); a wave
+    // past the end computes a valid row and stores nothing.
+    int ma = 0, mb = 0, ra = 0, rb = 0, seg = 0, p = item;
+    bool live = true, rope = false;
+    if constexpr (MODE == FUSED_QKV) {
+        while (seg < 3 && p >= f.n[seg] / 2) p -= f.n[seg] / 2, ++seg;
+        live = seg < 3;
+        if (!live) seg = 2, p = f.n[2] / 2 - 1;
+        const int hd = f.head_dim, half = hd / 2;
+        rope = seg < 2 && f.position >= 0;
+        ma = mb = seg;
+        ra = rope ? (p / half) * hd + p % half : 2 * p;
+        rb = rope ? ra + half : 2 * p + 1;
+    } else if constexpr (MODE == FUSED_GATE_UP) {
+        live = item < f.n[0];
+        ra = rb = min(item, f.n[0] - 1);
+        mb = 1;
+    } else {
+        live = 2 * item < f.n[0];
+        ra = min(2 * item, f.n[0] - 1);
+        rb = min(ra + 1, f.n[0] - 1);
+    }
+    // Loads in issue order: the first chunk of x (and gamma), then this
+    // wavefront's weights, so storing x to LDS waits only for x (wait counts
+    // are in issue order) while the weights stay in flight.
+    float xv[kChunk], gv[kChunk];
+    const bool norm = f.gamma != nullptr;
+    load_chunk(f.x, t, K, xv);
+    if (norm) load_chunk(f.gamma, t, K, gv);
+    PairPrefetch<BF16W> pf(row_ptr(ma, ra), row_ptr(mb, rb), K, lane);
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+        const int i = t + 256 * u;
+        if (i < K) {
+            x_s[i] = xv[u];
+            if (norm) x_s[K + i] = gv[u];
+        }
+    }
+    if (K > 256 * kChunk) {  // the rest of x (and gamma)
+        stage_to_lds(f.x + 256 * kChunk, x_s + 256 * kChunk, K - 256 * kChunk);
+        if (norm) stage_to_lds(f.gamma + 256 * kChunk, x_s + K + 256 * kChunk, K - 256 * kChunk);
+    }
+    if (norm) {
+        __syncthreads();
+        const float inv = rms_inverse([&](int i) { return x_s[i]; }, K, f.eps, red);
+        for (int i = t; i < K; i += 256) x_s[i] = x_s[i] * inv * x_s[K + i];
+    }
+    __syncthreads();
+    if (!live) return;
+    float a, b;
+    pf.finish(x_s, K, lane, a, b);
+
+    if constexpr (MODE == FUSED_QKV) {
+        const int hd = f.head_dim, half = hd / 2;
+        if (lane == 0) {
+            a += bias_of(seg, ra);
+            b += bias_of(seg, rb);
+            if (rope) {
+                float c, s;
+                rope_cos_sin(p % half, hd, f.position, c, s);
+                const float a0 = a, b0 = b;
+                a = a0 * c - b0 * s;
+                b = a0 * s + b0 * c;
+            }
+            f.y[seg][ra] = a;
+            f.y[seg][rb] = b;
+        }
+    } else if constexpr (MODE == FUSED_GATE_UP) {
+        if (lane == 0) f.y[0][ra] = swiglu_of(a + bias_of(0, ra), b + bias_of(1, ra));
+    } else {
+        if (lane == 0) {
+            f.y[0][ra] = (a + bias_of(0, ra)) + f.residual[ra];
+            if (rb != ra) f.y[0][rb] = (b + bias_of(0, rb)) + f.residual[rb];
+        }
+    }
+}
+
+// Common checks of the fused entry points: output-major rows, 16-byte aligned,
+// input staged in LDS.
+bool fused_rows_ok(const void* w, int64_t stride_k, int64_t stride_n, int K, int esz) {
+    return w != nullptr && stride_k == 1 && stride_n >= K && aligned16(w) &&
+           (stride_n * esz) % 16 == 0 && K <= kGemvMaxLdsK;
+}
+
+template <int MODE>
+int launch_fused(const FusedGemv& f, bool bf16, int items, hipStream_t s) {
+    const unsigned grid = static_cast<unsigned>(cdiv(items, 4));
+    const size_t lds = sizeof(float) * static_cast<size_t>(f.K) * (f.gamma != nullptr ? 2 : 1);
+    if (bf16) fused_gemv_kernel<true, MODE><<<grid, 256, lds, s>>>(f);
+    else fused_gemv_kernel<false, MODE><<<grid, 256, lds, s>>>(f);
+    return check_launch("fused_gemv_kernel");
 }
 
 }  // namespace skv
@@ -235,8 +465,9 @@ extern "C" int skv_rmsnorm_f32(const float* input, float* output, const float* g
                                int hidden, float epsilon, void* stream) {
     SKV_REQUIRE(input && output && gamma && rows > 0 && hidden > 0,
                 "skv_rmsnorm_f32: invalid pointers or sizes");
-    rmsnorm_kernel<<<rows, 256, 0, static_cast<hipStream_t>(stream)>>>(input, output, gamma, hidden,
-                                                                        epsilon);
+    SKV_REQUIRE(hidden <= 8192, "skv_rmsnorm_f32: hidden size %d exceeds 8192", hidden);
+    rmsnorm_kernel<<<rows, 256, 2 * sizeof(float) * hidden, static_cast<hipStream_t>(stream)>>>(
+        input, output, gamma, hidden, epsilon);
     return check_launch("rmsnorm_kernel");
 }
 
@@ -291,4 +522,105 @@ extern "C" int skv_add_f32(float* target, const float* source, int n, void* stre
     SKV_REQUIRE(target && source && n > 0, "skv_add_f32: invalid pointers or sizes");
     add_kernel<<<cdiv(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(target, source, n);
     return check_launch("add_kernel");
+}
+
+extern "C" int skv_fused_qkv_f32(const float* hidden, const float* gamma, float epsilon,
+                                 const void* wq, const void* wk, const void* wv, int weight_dtype,
+                                 int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
+                                 const float* bias_k, const float* bias_v, int hidden_dim,
+                                 int num_heads, int num_kv_heads, int head_dim, int position,
+                                 float* q, float* k, float* v, void* stream) {
+    SKV_REQUIRE(hidden && stride_n && q && k && v && hidden_dim > 0 && num_heads > 0 &&
+                    num_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
+                "skv_fused_qkv_f32: invalid pointers or sizes");
+    SKV_REQUIRE(weight_dtype == SKV_DTYPE_BF16 || weight_dtype == SKV_DTYPE_FP32,
+                "skv_fused_qkv_f32: unknown weight dtype %d", weight_dtype);
+    const int esz = weight_dtype == SKV_DTYPE_BF16 ? 2 : 4;
+    const void* ws[3] = {wq, wk, wv};
+    for (int m = 0; m < 3; ++m)
+        if (!fused_rows_ok(ws[m], stride_k, stride_n[m], hidden_dim, esz))
+            return set_error(SKV_ERR_UNSUPPORTED,
+                             "skv_fused_qkv_f32: weights must be 16-byte aligned output-major rows "
+                             "and hidden_dim <= %d",
+                             kGemvMaxLdsK);
+    FusedGemv f{};
+    f.x = hidden;
+    f.gamma = gamma;
+    f.eps = epsilon;
+    f.K = hidden_dim;
+    const int ns[3] = {num_heads * head_dim, num_kv_heads * head_dim, num_kv_heads * head_dim};
+    const float* bs[3] = {bias_q, bias_k, bias_v};
+    float* ys[3] = {q, k, v};
+    for (int m = 0; m < 3; ++m) {
+        f.w[m] = ws[m];
+        f.row_bytes[m] = stride_n[m] * esz;
+        f.bias[m] = bs[m];
+        f.n[m] = ns[m];
+        f.y[m] = ys[m];
+    }
+    f.head_dim = head_dim;
+    f.position = position;
+    return launch_fused<FUSED_QKV>(f, esz == 2, (ns[0] + ns[1] + ns[2]) / 2,
+                                   static_cast<hipStream_t>(stream));
+}
+
+extern "C" int skv_fused_gate_up_swiglu_f32(const float* x, const float* gamma, float epsilon,
+                                            const void* w_gate, const void* w_up, int weight_dtype,
+                                            int64_t stride_k, int64_t stride_n_gate,
+                                            int64_t stride_n_up, const float* bias_gate,
+                                            const float* bias_up, int in_dim, int out_dim,
+                                            float* act, void* stream) {
+    SKV_REQUIRE(x && act && in_dim > 0 && out_dim > 0,
+                "skv_fused_gate_up_swiglu_f32: invalid pointers or sizes");
+    SKV_REQUIRE(weight_dtype == SKV_DTYPE_BF16 || weight_dtype == SKV_DTYPE_FP32,
+                "skv_fused_gate_up_swiglu_f32: unknown weight dtype %d", weight_dtype);
+    const int esz = weight_dtype == SKV_DTYPE_BF16 ? 2 : 4;
+    if (!fused_rows_ok(w_gate, stride_k, stride_n_gate, in_dim, esz) ||
+        !fused_rows_ok(w_up, stride_k, stride_n_up, in_dim, esz))
+        return set_error(SKV_ERR_UNSUPPORTED,
+                         "skv_fused_gate_up_swiglu_f32: weights must be 16-byte aligned "
+                         "output-major rows and in_dim <= %d",
+                         kGemvMaxLdsK);
+    FusedGemv f{};
+    f.x = x;
+    f.gamma = gamma;
+    f.eps = epsilon;
+    f.K = in_dim;
+    f.w[0] = w_gate;
+    f.w[1] = w_up;
+    f.row_bytes[0] = stride_n_gate * esz;
+    f.row_bytes[1] = stride_n_up * esz;
+    f.bias[0] = bias_gate;
+    f.bias[1] = bias_up;
+    f.n[0] = f.n[1] = out_dim;
+    f.y[0] = act;
+    return launch_fused<FUSED_GATE_UP>(f, esz == 2, out_dim, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int skv_linear_residual_f32(const float* x, const void* weight, int weight_dtype,
+                                       int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
+                                       const float* bias, const float* residual, float* y,
+                                       void* stream) {
+    SKV_REQUIRE(x && residual && y && in_dim > 0 && out_dim > 0,
+                "skv_linear_residual_f32: invalid pointers or sizes");
+    SKV_REQUIRE(weight_dtype == SKV_DTYPE_BF16 || weight_dtype == SKV_DTYPE_FP32,
+                "skv_linear_residual_f32: unknown weight dtype %d", weight_dtype);
+    const int esz = weight_dtype == SKV_DTYPE_BF16 ? 2 : 4;
+    if (!fused_rows_ok(weight, stride_k, stride_n, in_dim, esz))
+        return set_error(SKV_ERR_UNSUPPORTED,
+                         "skv_linear_residual_f32: weights must be 16-byte aligned output-major "
+                         "rows and in_dim <= %d",
+                         kGemvMaxLdsK);
+    FusedGemv f{};
+    f.x = x;
+    f.gamma = nullptr;
+    f.K = in_dim;
+    f.w[0] = weight;
+    f.row_bytes[0] = stride_n * esz;
+    f.bias[0] = bias;
+    f.n[0] = out_dim;
+    f.y[0] = y;
+    f.residual = residual;
+    return launch_fused<FUSED_RESIDUAL>(f, esz == 2, cdiv(out_dim, 2),
+                                        static_cast<hipStream_t>(stream));
 }

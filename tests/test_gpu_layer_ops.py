@@ -8,6 +8,8 @@ transformer_block.cpp:315-323 (SwiGLU), the residual add.
 Tolerance for the fp32-accumulated dot products: |gpu - ref| <= 1e-5 * sum|x w|
 + 1e-6 (the accumulation order differs from the reference loop, the rounding
 bound scales with the sum of absolute products)."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -99,3 +101,96 @@ def test_rmsnorm_rope_swiglu_add(gpu):
     dt, ds = gpu.DeviceBuffer.from_numpy(t), gpu.DeviceBuffer.from_numpy(x[0])
     gpu._check(gpu.lib().skv_add_f32(dt.ptr, ds.ptr, H, None))
     assert np.array_equal(dt.download(np.float32, t.shape), t + x[0])
+
+
+def _bf16_rows(rng, n, k, scale=0.05):
+    return oracle.f32_to_bf16((scale * rng.standard_normal((n, k))).astype(np.float32))
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+@pytest.mark.parametrize("position", [-1, 0, 777])
+def test_fused_projections_match_separate_kernels(gpu, with_bias, position):
+    """skv_fused_qkv_f32, skv_fused_gate_up_swiglu_f32 and skv_linear_residual_f32
+    give the same bits as rmsnorm + linear + rope / swiglu / add run separately."""
+    rng = np.random.default_rng(11 + position)
+    H, Hq, Hkv, hd, inter = 1024, 16, 4, 64, 2816
+    lib, D = gpu.lib(), gpu.DeviceBuffer
+    h = rng.standard_normal(H).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    W = {n: _bf16_rows(rng, o, i) for n, o, i in
+         (("q", Hq * hd, H), ("k", Hkv * hd, H), ("v", Hkv * hd, H), ("o", H, Hq * hd),
+          ("g", inter, H), ("u", inter, H), ("d", H, inter))}
+    B = {n: (rng.standard_normal(w.shape[0]).astype(np.float32) if with_bias else None)
+         for n, w in W.items()}
+    dW = {n: D.from_numpy(w) for n, w in W.items()}
+    dB = {n: (D.from_numpy(b) if b is not None else None) for n, b in B.items()}
+    bp = lambda n: dB[n].ptr if dB[n] is not None else None
+    dh, dg = D.from_numpy(h), D.from_numpy(gamma)
+
+    def out(n):
+        return D(4 * n)
+
+    def lin(x, name, y):
+        w = W[name]
+        gpu._check(lib.skv_linear_f32(x.ptr, 1, dW[name].ptr, gpu.DTYPE_BF16, 1, w.shape[1], w.shape[1],
+                                      w.shape[0], bp(name), y.ptr, None))
+
+    # separate
+    xn = out(H)
+    gpu._check(lib.skv_rmsnorm_f32(dh.ptr, xn.ptr, dg.ptr, 1, H, 1e-5, None))
+    qs, ks, vs = out(Hq * hd), out(Hkv * hd), out(Hkv * hd)
+    lin(xn, "q", qs), lin(xn, "k", ks), lin(xn, "v", vs)
+    if position >= 0:
+        gpu._check(lib.skv_rope_f32(qs.ptr, Hq, hd, position, None))
+        gpu._check(lib.skv_rope_f32(ks.ptr, Hkv, hd, position, None))
+    # fused
+    qf, kf, vf = out(Hq * hd), out(Hkv * hd), out(Hkv * hd)
+    strides = (ctypes.c_int64 * 3)(H, H, H)
+    gpu._check(lib.skv_fused_qkv_f32(dh.ptr, dg.ptr, ctypes.c_float(1e-5), dW["q"].ptr, dW["k"].ptr,
+                                     dW["v"].ptr, gpu.DTYPE_BF16, 1, strides, bp("q"), bp("k"), bp("v"),
+                                     H, Hq, Hkv, hd, position, qf.ptr, kf.ptr, vf.ptr, None))
+    gpu.synchronize()
+    for a, b, n in ((qs, qf, Hq * hd), (ks, kf, Hkv * hd), (vs, vf, Hkv * hd)):
+        assert np.array_equal(a.download(np.uint32, (n,)), b.download(np.uint32, (n,)))
+
+    # o_proj + residual
+    ctx = D.from_numpy(rng.standard_normal(Hq * hd).astype(np.float32))
+    hs = out(H)
+    lin(ctx, "o", hs)
+    gpu._check(lib.skv_add_f32(hs.ptr, dh.ptr, H, None))
+    hf = out(H)
+    gpu._check(lib.skv_linear_residual_f32(ctx.ptr, dW["o"].ptr, gpu.DTYPE_BF16, 1, Hq * hd, Hq * hd, H,
+                                           bp("o"), dh.ptr, hf.ptr, None))
+    # rmsnorm + gate/up + swiglu
+    xn2, gs, us = out(H), out(inter), out(inter)
+    gpu._check(lib.skv_rmsnorm_f32(hs.ptr, xn2.ptr, dg.ptr, 1, H, 1e-5, None))
+    lin(xn2, "g", gs), lin(xn2, "u", us)
+    gpu._check(lib.skv_swiglu_f32(gs.ptr, us.ptr, inter, None))
+    af = out(inter)
+    gpu._check(lib.skv_fused_gate_up_swiglu_f32(hs.ptr, dg.ptr, ctypes.c_float(1e-5), dW["g"].ptr,
+                                                dW["u"].ptr, gpu.DTYPE_BF16, 1, H, H, bp("g"), bp("u"),
+                                                H, inter, af.ptr, None))
+    # down + residual
+    ds_, yf = out(H), out(H)
+    lin(gs, "d", ds_)
+    gpu._check(lib.skv_add_f32(ds_.ptr, hs.ptr, H, None))
+    gpu._check(lib.skv_linear_residual_f32(gs.ptr, dW["d"].ptr, gpu.DTYPE_BF16, 1, inter, inter, H,
+                                           bp("d"), hs.ptr, yf.ptr, None))
+    gpu.synchronize()
+    for a, b, n in ((hs, hf, H), (gs, af, inter), (ds_, yf, H)):
+        assert np.array_equal(a.download(np.uint32, (n,)), b.download(np.uint32, (n,)))
+
+
+def test_fused_projections_refuse_unsupported_layouts(gpu):
+    """GEMM-ready (input-major) or misaligned weights: SKV_ERR_UNSUPPORTED, nothing written."""
+    lib = gpu.lib()
+    H = 256
+    w = gpu.DeviceBuffer(H * H * 2 + 16)
+    x = gpu.DeviceBuffer.from_numpy(np.ones(H, np.float32))
+    y = gpu.DeviceBuffer.from_numpy(np.full(H, 7.0, np.float32))
+    rc = lib.skv_linear_residual_f32(x.ptr, w.ptr, gpu.DTYPE_BF16, H, 1, H, H, None, x.ptr, y.ptr, None)
+    assert rc == gpu.SKV_ERR_UNSUPPORTED
+    rc = lib.skv_linear_residual_f32(x.ptr, w.ptr + 2, gpu.DTYPE_BF16, 1, H, H, H, None, x.ptr, y.ptr, None)
+    assert rc == gpu.SKV_ERR_UNSUPPORTED
+    gpu.synchronize()
+    assert np.array_equal(y.download(np.float32, (H,)), np.full(H, 7.0, np.float32))
