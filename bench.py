@@ -488,6 +488,78 @@ def run_cfg1(steps: int, warmup: int, with_cpu: bool):
     return 0
 
 
+def run_prefill(steps: int, warmup: int):
+    """cfg5's prefill compute: the 4 new sequences of a churn step, each with a
+    2,048-token chunk at positions 0..2,047 (their whole context, in LIFO-reused
+    blocks), causal prefill attention over the paged cache (skv_paged_prefill)
+    at Llama-2-70B-style geometry.  The chunks are appended once before timing;
+    a step is one skv_paged_prefill call over the 4 chunks.  Compute-bound:
+    flops = 4 * sum over rows of (visible keys) * head_dim per query head
+    (q.k and P.V, 2 flops per multiply-add), against MI355X's dense bf16 peak."""
+    import stratakv_amd as skv
+
+    skv.require_gpu()
+    w = churn_workload(1)
+    Hq, Hkv, hd, bs, total = w["Hq"], w["Hkv"], w["hd"], w["bs"], w["total"]
+    nl, nn, chunk = CHURN_LONG, CHURN_NEW, CHURN_CHUNK
+    tables = np.ascontiguousarray(w["tables"][nl:])
+    mb = tables.shape[1]
+    pool_elems = total * bs * Hkv * hd
+    stream = skv.Stream()
+    k_pool, v_pool = skv.DeviceBuffer(pool_elems * 2), skv.DeviceBuffer(pool_elems * 2)
+    skv.fill_normal_bf16(k_pool, pool_elems, 0x5EED0505, 0, stream.handle)
+    skv.fill_normal_bf16(v_pool, pool_elems, 0x5EED0506, 0, stream.handle)
+    n_rows = nn * chunk
+    ck, cv = skv.DeviceBuffer(n_rows * Hkv * hd * 2), skv.DeviceBuffer(n_rows * Hkv * hd * 2)
+    skv.fill_normal_bf16(ck, n_rows * Hkv * hd, 0x5EED0507, 0, stream.handle)
+    skv.fill_normal_bf16(cv, n_rows * Hkv * hd, 0x5EED0508, 0, stream.handle)
+    q = skv.DeviceBuffer(n_rows * Hq * hd * 2)
+    skv.fill_normal_bf16(q, n_rows * Hq * hd, 0x5EED0509, 0, stream.handle)
+    dt = skv.DeviceBuffer.from_numpy(tables)
+    zero = skv.DeviceBuffer.from_numpy(np.zeros(nn, np.int32))
+    skv.kv_append(ck, cv, skv.DTYPE_BF16, k_pool, v_pool, total, dt, mb, zero, nn, chunk, Hkv, hd, bs,
+                  stream=stream.handle)
+    offsets = skv.DeviceBuffer.from_numpy((np.arange(nn + 1) * chunk).astype(np.int32))
+    lens = skv.DeviceBuffer.from_numpy(np.full(nn, chunk, np.int32))
+    out = skv.DeviceBuffer(n_rows * Hq * hd * 4)
+    scale = 1.0 / math.sqrt(hd)
+
+    def call():
+        skv.paged_prefill(q, skv.DTYPE_BF16, k_pool, v_pool, total, dt, mb, offsets, lens, nn, n_rows,
+                          Hq, Hkv, hd, bs, scale, out, stream=stream.handle)
+
+    for _ in range(warmup):
+        call()
+    skv.synchronize()
+    e0, e1 = skv.Event(), skv.Event()
+    e0.record(stream.handle)
+    for _ in range(steps):
+        call()
+    e1.record(stream.handle)
+    skv.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    visible = nn * chunk * (chunk + 1) // 2            # keys seen by the rows, summed
+    flops = 4 * visible * Hq * hd
+    tflops = flops / (ms / 1e3) / 1e12
+    kv_bytes = nn * chunk * 2 * Hkv * hd * 2
+    print(json.dumps({
+        "metric": "paged prefill attention TFLOP/s (cfg5 prefill chunks)", "value": round(tflops, 2),
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (device counter-hash N(0,1) bf16 Q/K/V, seeded)",
+        "config": {"workload": ("cfg5 prefill: 4 sequences x 2,048-token chunks at positions "
+                                "0..2,047 (LIFO-reused blocks), 64 Q / 8 KV heads, head_dim 128, "
+                                "causal"), "chunk_tokens": chunk, "sequences": nn},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+                     "algorithmic_flops": flops,
+                     "note": ("P.V runs as two bf16 MFMAs (P split into hi + lo parts), so the "
+                              "matrix cores execute 1.5x the algorithmic flops")},
+        "kv_gbs": round(kv_bytes / (ms / 1e3) / 1e9, 2),
+    }), flush=True)
+    return 0
+
+
 def profile_traffic(workload_key: str):
     """HBM bytes per launch of the decode kernel from the committed rocprof
     counter summary, if one exists for this workload."""
@@ -525,6 +597,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=4, help="BASELINE.json config (1, 2, 3, 4 or 5)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prefill", action="store_true",
+                    help="with --config 5: time the chunked prefill attention of its 4 new "
+                         "sequences (skv_paged_prefill) instead of the decode step")
     ap.add_argument("--separate", action="store_true",
                     help="time the decode-token append and the decode as two calls "
                          "(skv_kv_append + skv_paged_decode) instead of the fused call")
@@ -538,6 +613,10 @@ def main() -> int:
               f"decode path shards by sequence or KV head with no exchange; the multi-GPU design is "
               f"described in DESIGN.md but not built or measured.", file=sys.stderr)
         return 2
+    if args.prefill:
+        if args.config != 5:
+            raise SystemExit("bench.py: --prefill measures config 5's prefill chunks (--config 5)")
+        return run_prefill(args.steps, args.warmup)
     if args.config == 1:
         return run_cfg1(args.steps, args.warmup, not args.no_cpu_baseline)
     w = churn_workload(args.warmup + args.steps) if args.config == 5 else workload(args.config)

@@ -180,6 +180,27 @@ int skv_paged_decode_append(const void* q, int q_dtype,
                             int block_size, float scale, float* out,
                             void* workspace, size_t workspace_bytes, void* stream);
 
+/* Chunked prefill attention over the paged cache.  The query rows
+ * seq_offsets[b] .. seq_offsets[b+1]-1 of q ([num_tokens][num_q_heads][head_dim],
+ * q_dtype) are sequence b's chunk: the last n_b positions of its
+ * context_lens[b]-token context, already appended to the pools
+ * (skv_kv_append).  Row i of the chunk attends causally to positions
+ * 0 .. context_lens[b] - n_b + i of its sequence.  out: [num_tokens][Hq][hd]
+ * fp32.  seq_offsets [num_seqs + 1] and context_lens [num_seqs] are device
+ * arrays; num_tokens (= seq_offsets[num_seqs]) sizes the grid on the host.
+ * num_seqs <= 4096.  Blocks outside the pool and positions past the table are
+ * skipped as in skv_paged_decode; a row with no visible key gives zeros.
+ * Replaces: the CPU-only multi-token path of PagedAttention::forward
+ * (src/layers/attention.cpp:197-337), which the reference has no GPU kernel
+ * for. */
+int skv_paged_prefill(const void* q, int q_dtype, const uint16_t* k_pool,
+                      const uint16_t* v_pool, int64_t total_blocks,
+                      const int32_t* block_tables, int max_blocks_per_seq,
+                      const int32_t* seq_offsets, const int32_t* context_lens,
+                      int num_seqs, int num_tokens, int num_q_heads,
+                      int num_kv_heads, int head_dim, int block_size, float scale,
+                      float* out, void* stream);
+
 /* Single-sequence decode with the reference's argument list (gemm_cuda.h:41-44)
  * on bf16 pools, plus the pool size, workspace and stream.  Equivalent to
  * skv_paged_decode with num_seqs = 1, an fp32 query, max_blocks_per_seq =

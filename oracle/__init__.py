@@ -43,6 +43,8 @@ _REF_PROTOS = {
     "ref_bf16_rne_n": (_i32, [_vp, _vp, _sz]),
     "ref_attention_trace": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
                                    _vp, _vp]),
+    "ref_prefill_trace": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                                 _vp, _vp]),
 }
 
 _lib = None
@@ -156,6 +158,63 @@ def paged_decode(q, k_pool, v_pool, tables, lens, num_kv_heads, block_size, scal
     if rc != 0:
         raise RuntimeError(f"oracle paged decode failed with status {rc}")
     return out
+
+
+def prefill_positions(seq_offsets, lens):
+    """Per query token of a prefill batch: (sequence, position).  Sequence b
+    owns tokens seq_offsets[b] .. seq_offsets[b+1]-1, the last n_b positions of
+    its lens[b]-token context."""
+    seq_offsets = np.asarray(seq_offsets, np.int64)
+    lens = np.asarray(lens, np.int64)
+    seqs, pos = [], []
+    for b in range(len(lens)):
+        n = int(seq_offsets[b + 1] - seq_offsets[b])
+        seqs += [b] * n
+        pos += list(range(int(lens[b]) - n, int(lens[b])))
+    return np.array(seqs, np.int64), np.array(pos, np.int64)
+
+
+def paged_prefill(q, k_pool, v_pool, tables, seq_offsets, lens, num_kv_heads, block_size, scale,
+                  precision: str = "f32", threads: int = 1):
+    """Causal chunked-prefill attention (src/layers/attention.cpp:263-337 per
+    token): query token i of sequence b sits at position p = lens[b] - n_b + i
+    and attends to positions 0..p of its sequence.  q [N, Hq, hd] float32 with
+    N = seq_offsets[-1]; returns [N, Hq, hd].  Each token is the reference's
+    decode loop at context p + 1, so this runs paged_decode with one row per
+    token (its sequence's table, length p + 1); tokens with p < 0 give zeros."""
+    seqs, pos = prefill_positions(seq_offsets, lens)
+    tables = np.ascontiguousarray(tables, np.int32)
+    tok_tables = np.ascontiguousarray(tables[seqs]) if len(seqs) else tables[:0]
+    tok_lens = np.maximum(pos + 1, 0).astype(np.int32)
+    q = np.ascontiguousarray(q, np.float32)
+    if len(seqs) == 0:
+        return np.zeros_like(q)
+    return paged_decode(q, k_pool, v_pool, tok_tables, tok_lens, num_kv_heads, block_size, scale,
+                        precision=precision, threads=threads)
+
+
+def ref_prefill_trace(hidden: int, heads: int, kv_heads: int, total_blocks: int, block_size: int,
+                      x: np.ndarray, chunk_lens):
+    """Run tokens x [T, hidden] through the reference's PagedAttention::forward
+    in chunks (sum(chunk_lens) == T)."""
+    x = np.ascontiguousarray(x, np.float32)
+    chunks = np.ascontiguousarray(chunk_lens, np.int32)
+    T = x.shape[0]
+    assert int(chunks.sum()) == T
+    hd = hidden // heads
+    kv_dim = kv_heads * hd
+    out = np.zeros((T, hidden), np.float32)
+    q = np.zeros((T, hidden), np.float32)
+    k = np.zeros((T, kv_dim), np.float32)
+    v = np.zeros((T, kv_dim), np.float32)
+    table = np.zeros(total_blocks, np.int32)
+    nb = ctypes.c_int(0)
+    rc = ref().ref_prefill_trace(hidden, heads, kv_heads, total_blocks, block_size, len(chunks),
+                                 _p(chunks), _p(x), _p(out), _p(q), _p(k), _p(v), _p(table),
+                                 ctypes.byref(nb))
+    if rc != 0:
+        raise RuntimeError("reference prefill trace failed")
+    return out, q, k, v, table[: nb.value].copy()
 
 
 def ref_attention_trace(hidden: int, heads: int, kv_heads: int, total_blocks: int, block_size: int,

@@ -176,4 +176,69 @@ int ref_attention_trace(int hidden, int heads, int kv_heads, int total_blocks, i
     }
 }
 
+// The same setup as ref_attention_trace, but the tokens go through
+// PagedAttention::forward in chunks of chunk_lens[c] tokens (a prefill chunk
+// per call: every token of a chunk attends causally to all earlier tokens,
+// those of the same chunk included).  The second sequence takes one token
+// after each chunk, so the first sequence's pages are non-contiguous.
+int ref_prefill_trace(int hidden, int heads, int kv_heads, int total_blocks, int block_size,
+                      int n_chunks, const int32_t* chunk_lens, const float* x, float* out,
+                      float* q_eff, float* k_eff, float* v_eff, int32_t* table, int* n_blocks) {
+    using stratakv::Tensor;
+    try {
+        stratakv::layers::PagedAttention attn(hidden, heads, kv_heads, total_blocks, block_size);
+        const int hd = hidden / heads;
+        const int kv_dim = kv_heads * hd;
+        const int voff = hidden - kv_dim;
+        auto& wq = attn.query_projection().weight();
+        auto& wk = attn.key_projection().weight();
+        auto& wv = attn.value_projection().weight();
+        auto& wo = attn.output_projection().weight();
+        for (int i = 0; i < hidden; ++i) {
+            for (int j = 0; j < hidden; ++j) {
+                wq[static_cast<std::size_t>(i) * hidden + j] = i == j ? 1.0f : 0.0f;
+                wo[static_cast<std::size_t>(i) * hidden + j] = i == j ? 1.0f : 0.0f;
+            }
+            for (int j = 0; j < kv_dim; ++j) {
+                wk[static_cast<std::size_t>(i) * kv_dim + j] = i == j ? 1.0f : 0.0f;
+                wv[static_cast<std::size_t>(i) * kv_dim + j] = i == j + voff ? 1.0f : 0.0f;
+            }
+        }
+        stratakv::memory::BlockPool pool(total_blocks, block_size);
+        stratakv::memory::PageTable pages;
+        pages.allocate_sequence(0, pool);
+        pages.allocate_sequence(1, pool);
+        int t0 = 0;
+        for (int c = 0; c < n_chunks; ++c) {
+            const int n = chunk_lens[c];
+            Tensor xt({static_cast<std::size_t>(n), static_cast<std::size_t>(hidden)});
+            for (int t = 0; t < n; ++t)
+                for (int i = 0; i < hidden; ++i)
+                    xt[static_cast<std::size_t>(t) * hidden + i] = x[static_cast<std::size_t>(t0 + t) * hidden + i];
+            Tensor o = attn.forward(xt, 0, pages, pool);
+            for (int t = 0; t < n; ++t)
+                for (int i = 0; i < hidden; ++i)
+                    out[static_cast<std::size_t>(t0 + t) * hidden + i] = o[static_cast<std::size_t>(t) * hidden + i];
+            pages.append_token(1, pool);
+            for (int t = t0; t < t0 + n; ++t) {
+                float* qr = q_eff + static_cast<std::size_t>(t) * hidden;
+                float* kr = k_eff + static_cast<std::size_t>(t) * kv_dim;
+                float* vr = v_eff + static_cast<std::size_t>(t) * kv_dim;
+                std::memcpy(qr, x + static_cast<std::size_t>(t) * hidden, sizeof(float) * hidden);
+                std::memcpy(kr, x + static_cast<std::size_t>(t) * hidden, sizeof(float) * kv_dim);
+                std::memcpy(vr, x + static_cast<std::size_t>(t) * hidden + voff, sizeof(float) * kv_dim);
+                rope_rows(qr, heads, hd, t);
+                rope_rows(kr, kv_heads, hd, t);
+            }
+            t0 += n;
+        }
+        const auto& pbs = pages.get_state(0).physical_blocks;
+        *n_blocks = static_cast<int>(pbs.size());
+        for (std::size_t k = 0; k < pbs.size(); ++k) table[k] = pbs[k];
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
 }  // extern "C"

@@ -82,6 +82,8 @@ _PROTOS = {
     "skv_paged_attention_decode_append": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _vp,
                                                  _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz,
                                                  _vp]),
+    "skv_paged_prefill": (_i32, [_vp, _i32, _vp, _vp, _i64, _vp, _i32, _vp, _vp, _i32, _i32, _i32,
+                                 _i32, _i32, _i32, _f32, _vp, _vp]),
     "skv_paged_attention_decode_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "skv_paged_attention_decode": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32,
                                           _i32, _f32, _vp, _sz, _vp]),
@@ -251,6 +253,17 @@ def paged_attention_decode_append(query, key_row, value_row, kv_dtype: int, key_
         _ptr(query), _ptr(key_row), _ptr(value_row), kv_dtype, _ptr(key_cache), _ptr(value_cache),
         total_blocks, _ptr(block_table), _ptr(output), context_len, block_size, num_q_heads,
         num_kv_heads, head_dim, scale, _ptr(workspace), workspace_bytes, stream))
+
+
+def paged_prefill(q, q_dtype: int, k_pool, v_pool, total_blocks: int, block_tables,
+                  max_blocks_per_seq: int, seq_offsets, context_lens, num_seqs: int,
+                  num_tokens: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                  block_size: int, scale: float, out, stream=None) -> None:
+    """Causal prefill attention of each sequence's chunk (rows seq_offsets[b]..)."""
+    _check(lib().skv_paged_prefill(_ptr(q), q_dtype, _ptr(k_pool), _ptr(v_pool), total_blocks,
+                                   _ptr(block_tables), max_blocks_per_seq, _ptr(seq_offsets),
+                                   _ptr(context_lens), num_seqs, num_tokens, num_q_heads,
+                                   num_kv_heads, head_dim, block_size, scale, _ptr(out), stream))
 
 
 def paged_attention_decode(query, key_cache, value_cache, total_blocks: int, block_table, output,
