@@ -1,0 +1,121 @@
+// generator.h -- token generation over the layer stack, on the device.
+//
+// Interface of the reference's stratakv::generation::Generator
+// (include/stratakv/generation/generator.h:9-124, src/generation/generator.cpp):
+// the configuration, the weight schema (Hugging Face Llama names, or the
+// one-layer "block.*" schema), the per-layer BlockPool / PageTable, and
+// generate(prompt, max_new_tokens) with its validation and EOS rule.
+//
+// What runs where: every token's embedding lookup, the layers'
+// TransformerBlock::forward_into, the final RMSNorm, the lm_head GEMV and the
+// token choice (skv_argmax_f32 / skv_sample_f32) are queued on one stream, and
+// the chosen id stays in device memory where the next step's embedding lookup
+// reads it.  The host queues steps ahead of the GPU and learns each token from
+// a small asynchronous copy, so it waits only to stop at EOS (at most
+// kLookahead steps are queued past the step it has checked).  The reference
+// instead copies the full logits to the host and samples there every token
+// (src/generation/generator.cpp:700-735).
+//
+// Weights may be the host FP32 tensors of io::load_safetensors (uploaded, and
+// linears truncated to BF16, as the reference's GPU path does) or the device
+// tensors of io::load_safetensors_device (used in place).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <vector>
+
+#include "stratakv/generation/sampler.h"
+#include "stratakv/io/safetensors.h"
+#include "stratakv/memory/block_pool.h"
+#include "stratakv/memory/page_table.h"
+#include "stratakv/models/transformer_block.h"
+
+namespace stratakv {
+namespace generation {
+
+struct GeneratorConfig {
+    Device device = Device::GPU;
+    std::size_t hidden_dim = 0;
+    std::size_t intermediate_dim = 0;
+    std::size_t num_heads = 0;
+    std::size_t num_kv_heads = 0;  // zero selects num_heads (MHA)
+    std::size_t num_layers = 0;
+    int total_blocks = 0;
+    int block_size = 0;
+    std::size_t vocab_size = 0;
+    int eos_token_id = -1;  // disabled when -1
+    SamplerConfig sampler{0.0f, 0, 1.0f};
+
+    GeneratorConfig() = default;
+    GeneratorConfig(std::size_t hidden, std::size_t intermediate, std::size_t heads, int total, int block,
+                    std::size_t vocab, int eos)
+        : hidden_dim(hidden), intermediate_dim(intermediate), num_heads(heads), num_kv_heads(0),
+          num_layers(1), total_blocks(total), block_size(block), vocab_size(vocab), eos_token_id(eos) {}
+    GeneratorConfig(std::size_t hidden, std::size_t intermediate, std::size_t heads, std::size_t layers,
+                    int total, int block, std::size_t vocab, int eos)
+        : hidden_dim(hidden), intermediate_dim(intermediate), num_heads(heads), num_kv_heads(0),
+          num_layers(layers), total_blocks(total), block_size(block), vocab_size(vocab), eos_token_id(eos) {}
+    GeneratorConfig(std::size_t hidden, std::size_t intermediate, std::size_t heads, std::size_t kv_heads,
+                    std::size_t layers, int total, int block, std::size_t vocab, int eos)
+        : hidden_dim(hidden), intermediate_dim(intermediate), num_heads(heads), num_kv_heads(kv_heads),
+          num_layers(layers), total_blocks(total), block_size(block), vocab_size(vocab), eos_token_id(eos) {}
+};
+
+class Generator {
+public:
+    // Steps queued beyond the last one whose token the host has seen.
+    static constexpr int kLookahead = 8;
+
+    Generator(GeneratorConfig config, io::WeightMap weights);
+    ~Generator();
+    Generator(const Generator&) = delete;
+    Generator& operator=(const Generator&) = delete;
+
+    std::vector<int> generate(const std::vector<int>& prompt, int max_new_tokens);
+    std::size_t free_block_count() const noexcept;
+    double last_generation_ms() const noexcept { return last_generation_ms_; }
+    double initialization_ms() const noexcept { return initialization_ms_; }
+
+    // Extensions (no counterpart in the reference).
+    // Stream for all device work (a hipStream_t; nullptr = default stream).
+    void set_stream(void* stream);
+    // Teacher forcing: tokens[0..n_prompt) are the prompt, then every later
+    // token is fed in turn.  Returns the logits after each of the positions
+    // n_prompt-1 .. tokens.size()-1, row-major [(tokens.size() - n_prompt + 1) x vocab].
+    std::vector<float> forced_logits(const std::vector<int>& tokens, std::size_t n_prompt);
+
+private:
+    void validate_prompt(const std::vector<int>& prompt, std::size_t extra) const;
+    void begin_sequence(std::size_t tokens);
+    void end_sequence() noexcept;
+    // One decode step: embedding of ids_[in_index], all layers, final norm,
+    // lm_head into `logits` (device [vocab]).
+    void step(int in_index, float* logits);
+    void raise_flags(std::int32_t flags) const;
+
+    GeneratorConfig config_;
+    void* stream_ = nullptr;
+    std::vector<models::TransformerBlock> blocks_;
+    std::vector<memory::BlockPool> pools_;
+    std::vector<memory::PageTable> pages_;
+    Sampler sampler_;
+    std::optional<Tensor> embeddings_;  // [vocab, hidden], BF16 or FP32, device
+    std::optional<layers::RMSNorm> final_norm_;
+    std::optional<layers::Linear> lm_head_;  // [hidden, vocab] view of BF16 [vocab, hidden] rows
+    std::optional<Tensor> hidden_;           // [1, hidden] FP32: embedding, then the layer stream
+    std::optional<Tensor> normed_;           // [1, hidden] FP32
+    std::optional<Tensor> logits_;           // [1, vocab] FP32
+    std::int32_t* ids_ = nullptr;            // device token ids, capacity ids_capacity_
+    std::size_t ids_capacity_ = 0;
+    std::int32_t* flags_ = nullptr;          // device SKV_FLAG_* bits
+    std::int32_t* host_ids_ = nullptr;       // page-locked copies of the chosen ids
+    std::vector<void*> step_events_;         // ring of kLookahead + 1 events
+    double last_generation_ms_ = 0.0;
+    double initialization_ms_ = 0.0;
+};
+
+}  // namespace generation
+}  // namespace stratakv

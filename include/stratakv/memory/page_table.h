@@ -8,7 +8,8 @@
 // blocks in table order.  get_device_block_table keeps a device copy of one
 // sequence's table; unlike the reference, which re-uploads the whole table
 // whenever it is dirty (every token), it uploads only the block ids appended
-// since the last call.
+// since the last call, as an asynchronous copy from a page-locked mirror
+// queued on the caller's stream (the host never waits for the GPU there).
 //
 // DeviceBatch is new API for the batched entry points (the reference decodes
 // one sequence per call): device arrays [max_seqs][max_blocks] block tables,
@@ -52,8 +53,11 @@ public:
     const SequenceState& get_state(int seq_id) const;
     bool has_sequence(int seq_id) const noexcept;
 
-    // Device copy of the sequence's block ids (valid until the next call).
-    const int* get_device_block_table(int seq_id);
+    // Device copy of the sequence's block ids (valid until the next call),
+    // brought up to date by work queued on `stream` (a hipStream_t; nullptr =
+    // the default stream): kernels that read it must run on that stream or
+    // after it.
+    const int* get_device_block_table(int seq_id, void* stream = nullptr);
     // Pre-size the device table so growth never allocates in the token loop.
     void reserve_device_block_table(std::size_t capacity);
 
@@ -62,6 +66,7 @@ private:
 
     std::unordered_map<int, SequenceState> table_;
     int* d_block_table_ = nullptr;
+    int* h_block_table_ = nullptr;  // page-locked mirror the uploads copy from
     std::size_t d_block_table_capacity_ = 0;
     int staged_seq_id_ = 0;
     std::size_t staged_block_count_ = 0;

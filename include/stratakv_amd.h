@@ -51,6 +51,14 @@ extern "C" {
 /* ---- element types ------------------------------------------------------- */
 #define SKV_DTYPE_BF16 0
 #define SKV_DTYPE_FP32 1
+#define SKV_DTYPE_F16  2  /* checkpoint tensors only (skv_convert_*, skv_embedding_f32) */
+
+/* ---- device status flags (bits of an int32 in device memory, set by the
+ *      token-choice and embedding kernels; never cleared by them) ---------- */
+#define SKV_FLAG_NONFINITE_LOGITS 1  /* a logit was NaN or infinite            */
+#define SKV_FLAG_BAD_TOKEN        2  /* an embedding id outside [0, vocab)      */
+#define SKV_FLAG_NONFINITE_SCALED 4  /* a logit / temperature was not finite   */
+#define SKV_FLAG_BAD_DISTRIBUTION 8  /* the filtered softmax total was not > 0  */
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* skv_last_error(void);
@@ -77,12 +85,16 @@ int skv_event_destroy(void* event);
 int skv_event_record(void* event, void* stream);
 int skv_event_synchronize(void* event);
 int skv_event_elapsed_ms(float* ms, void* start, void* stop);
+/* *done = 1 when the work before the event has completed, else 0 (no wait). */
+int skv_event_query(void* event, int* done);
 /* Page-locked host memory, so host-to-device copies can run asynchronously. */
 int skv_host_alloc(void** ptr, size_t bytes);
 int skv_host_free(void* ptr);
 /* Asynchronous copy on `stream` (src should be page-locked; the call returns
  * before the copy completes). */
 int skv_memcpy_h2d_async(void* dst, const void* src, size_t bytes, void* stream);
+/* The same device-to-host (dst should be page-locked). */
+int skv_memcpy_d2h_async(void* dst, const void* src, size_t bytes, void* stream);
 /* dst[pairs[2i]] = pairs[2i+1] for i < n: applies a batch of (index, value)
  * updates to a device int32 array (incremental block-table upload). */
 int skv_scatter_i32(int32_t* dst, const int32_t* pairs, int n, void* stream);
@@ -296,6 +308,57 @@ int skv_linear_residual_f32(const float* x, const void* weight, int weight_dtype
                             int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
                             const float* bias, const float* residual, float* y,
                             void* stream);
+
+/* ---- model boundary: checkpoint tensors, embedding, token choice --------
+ * Checkpoint decode on the device (the host only moves file bytes).  src holds
+ * `count` little-endian elements of src_dtype (SKV_DTYPE_BF16 / F16 / FP32).
+ * skv_convert_to_bf16: dst = the upper 16 bits of the exact fp32 value (BF16
+ *   copied, F16 widened exactly then truncated, FP32 truncated), the rule of
+ *   load_linear_bf16_transposed and convert_fp32_to_bf16_cuda
+ *   (src/io/safetensors.cpp:610-681, src/cuda/gemm_cuda.cu:74-83).
+ * skv_convert_to_f32: dst = the exact fp32 value (src/io/safetensors.cpp:98-104,
+ *   :219-250 for F16).
+ * skv_check_finite: no output.
+ * When nonfinite is not NULL, *nonfinite |= 1 if any element is NaN or
+ * infinite (the check behind the reference's "Non-finite weight" error,
+ * src/generation/generator.cpp:265-290). */
+int skv_convert_to_bf16(const void* src, int src_dtype, size_t count, uint16_t* dst,
+                        int32_t* nonfinite, void* stream);
+int skv_convert_to_f32(const void* src, int src_dtype, size_t count, float* dst,
+                       int32_t* nonfinite, void* stream);
+int skv_check_finite(const void* src, int src_dtype, size_t count, int32_t* nonfinite,
+                     void* stream);
+
+/* out[i] = table[token_ids[index] * hidden + i] as fp32 (exact widening of a
+ * BF16 / F16 table).  The id is read on the device; an id outside [0, vocab)
+ * writes zeros and sets SKV_FLAG_BAD_TOKEN in *flags (flags may be NULL).
+ * Replaces: embedding_lookup_cuda (src/cuda/gemm_cuda.cu:286-300,900-912). */
+int skv_embedding_f32(const void* table, int table_dtype, int vocab, int hidden,
+                      const int32_t* token_ids, int index, float* out, int32_t* flags,
+                      void* stream);
+
+/* token_ids[index] = the first index of the maximum of logits[0..n) (greedy,
+ * src/generation/sampler.cpp:57-62).  A non-finite logit sets
+ * SKV_FLAG_NONFINITE_LOGITS.  Replaces the logits download + host argmax of
+ * the reference's generate loop (src/generation/generator.cpp:700-735). */
+int skv_argmax_f32(const float* logits, int n, int32_t* token_ids, int index,
+                   int32_t* flags, void* stream);
+
+/* token_ids[index] = Sampler::sample(logits) (src/generation/sampler.cpp:43-147):
+ * temperature 0 -> greedy as skv_argmax_f32; otherwise logits / temperature,
+ * top-k (0 = off), top-p (1 = off), softmax of what is kept, and the
+ * categorical draw of std::discrete_distribution for the uniform `uniform`
+ * in [0, 1), which the caller draws as generate_canonical<double, 53> from the
+ * sampler's mt19937 (one draw per call with temperature > 0 and n >= 2).
+ * Configuration errors return SKV_ERR_INVALID_ARGUMENT with the reference's
+ * messages; data errors set SKV_FLAG_NONFINITE_LOGITS / _NONFINITE_SCALED /
+ * _BAD_DISTRIBUTION in *flags and write token 0.  Masses are summed in double
+ * in a different order than the reference's float loops, so the chosen token
+ * can differ only where `uniform` or top_p falls within rounding of a
+ * cumulative boundary. */
+int skv_sample_f32(const float* logits, int n, float temperature, int top_k, float top_p,
+                   double uniform, int32_t* token_ids, int index, int32_t* flags,
+                   void* stream);
 
 /* ---- test support --------------------------------------------------------
  * Copy the blocks listed in table[0..num_blocks) of a pool into a contiguous

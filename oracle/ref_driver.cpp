@@ -1,17 +1,27 @@
 // ref_driver.cpp -- C entry points over the reference's own CPU classes, used
-// to pin the oracle restatement.  Compiled together with the reference's
-// sources where they lie (oracle/Makefile, target `ref`) into
-// oracle/_ref/libstratakv_ref.so; only tests/ load it.  This file is test
-// infrastructure: it calls the reference's public API (BlockPool, PageTable,
-// Tensor, PagedAttention) and contains none of its code.
+// to pin the oracle restatement and to write golden vectors.  Compiled
+// together with the reference's sources where they lie (oracle/Makefile,
+// target `ref`) into oracle/_ref/libstratakv_ref.so; only tests/ load it.
+// This file is test infrastructure: it calls the reference's public API
+// (BlockPool, PageTable, Tensor, PagedAttention, TransformerBlock, RMSNorm,
+// Linear, load_safetensors, Sampler) and contains none of its code.
+#include "stratakv/generation/sampler.h"
+#include "stratakv/io/safetensors.h"
 #include "stratakv/layers/attention.h"
+#include "stratakv/layers/rmsnorm.h"
 #include "stratakv/memory/block_pool.h"
 #include "stratakv/memory/page_table.h"
+#include "stratakv/models/transformer_block.h"
 #include "stratakv/tensor.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
+#include <limits>
+#include <numeric>
+#include <random>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -238,6 +248,180 @@ int ref_prefill_trace(int hidden, int heads, int kv_heads, int total_blocks, int
         return 0;
     } catch (const std::exception&) {
         return -1;
+    }
+}
+
+// ---- checkpoint loader ----------------------------------------------------
+// Loads `path` with the reference's load_safetensors.  On success returns 0,
+// the number of tensors in *count, and, when `name` is given, copies that
+// tensor's FP32 values into out[0..cap) and its element count into *n.
+// On failure returns 1 and the exception text in err[0..err_cap).
+int ref_load_tensor(const char* path, int require_mapped_f32, const char* name, float* out,
+                    std::size_t cap, std::size_t* n, int* count, char* err, int err_cap) {
+    try {
+        auto weights = stratakv::io::load_safetensors(path, require_mapped_f32 != 0);
+        *count = static_cast<int>(weights.size());
+        if (name != nullptr) {
+            const auto it = weights.find(name);
+            if (it == weights.end()) {
+                std::snprintf(err, err_cap, "no tensor %s", name);
+                return 2;
+            }
+            const auto& t = it->second;
+            *n = t.num_elements();
+            for (std::size_t i = 0; i < t.num_elements() && i < cap; ++i) out[i] = t[i];
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        std::snprintf(err, err_cap, "%s", e.what());
+        return 1;
+    }
+}
+
+// load_linear_bf16_transposed of an [out_f, in_f] FP32 source; dst receives
+// the [in_f, out_f] bf16 bit patterns.
+int ref_linear_bf16_transposed(const float* src, std::size_t out_f, std::size_t in_f, uint16_t* dst) {
+    try {
+        stratakv::Tensor t({out_f, in_f});
+        std::memcpy(t.data(), src, sizeof(float) * out_f * in_f);
+        const auto r = stratakv::io::load_linear_bf16_transposed(t, out_f, in_f);
+        std::memcpy(dst, r.raw_data(), sizeof(uint16_t) * out_f * in_f);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// ---- sampler ----------------------------------------------------------------
+// tokens[r] = Sampler(config, seed).sample(logits row r) for rows in order,
+// one sampler (one mt19937 stream) across all rows.  Returns 0, or 1 with the
+// exception text (and the failing row in *failed_row).
+int ref_sample_rows(const float* logits, int rows, int vocab, float temperature, int top_k,
+                    float top_p, uint32_t seed, int32_t* tokens, int* failed_row, char* err,
+                    int err_cap) {
+    int r = 0;
+    try {
+        stratakv::generation::Sampler sampler({temperature, top_k, top_p}, seed);
+        stratakv::Tensor t({static_cast<std::size_t>(vocab)});
+        for (r = 0; r < rows; ++r) {
+            std::memcpy(t.data(), logits + static_cast<std::size_t>(r) * vocab, sizeof(float) * vocab);
+            tokens[r] = sampler.sample(t);
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        *failed_row = r;
+        std::snprintf(err, err_cap, "%s", e.what());
+        return 1;
+    }
+}
+
+// The uniform draws a std::discrete_distribution makes from std::mt19937(seed):
+// generate_canonical<double, 53>, one per draw.
+void ref_canonical_draws(uint32_t seed, int n, double* out) {
+    std::mt19937 g(seed);
+    for (int i = 0; i < n; ++i)
+        out[i] = std::generate_canonical<double, std::numeric_limits<double>::digits>(g);
+}
+
+// ---- greedy generation trace ---------------------------------------------
+// The reference's CPU generation path (Generator::generate with Device::CPU,
+// src/generation/generator.cpp:617-803) driven through the public classes so
+// the logits of every step can be recorded: the checkpoint is loaded with
+// load_safetensors, the Llama weights are placed as the Generator places them
+// (linears through load_linear_bf16_transposed), the prompt tokens[0..n_prompt)
+// run as one multi-token forward, then every later step feeds tokens[p]
+// (teacher forcing with the caller's stream) one token at a time.
+// Step s (0..n_tokens-n_prompt) records the greedy argmax and the top_k
+// logits (ids and values, descending, ties by index) of the logits that
+// predict position n_prompt + s.  A negative tokens[p] (p >= n_prompt) is
+// replaced by the argmax that predicts it (plain greedy generation).
+int ref_generate_trace(const char* path, int layers, int heads, int kv_heads, int32_t* tokens,
+                       int n_tokens, int n_prompt, int top_k, int32_t* argmax, int32_t* top_ids,
+                       float* top_vals, char* err, int err_cap) {
+    using stratakv::Tensor;
+    try {
+        auto w = stratakv::io::load_safetensors(path);
+        auto take = [&](const std::string& k) {
+            auto it = w.find(k);
+            if (it == w.end()) throw std::invalid_argument("missing " + k);
+            Tensor t = std::move(it->second);
+            w.erase(it);
+            return t;
+        };
+        Tensor emb = take("model.embed_tokens.weight");
+        const std::size_t vocab = emb.shape()[0], h = emb.shape()[1];
+        const std::size_t hd = h / heads;
+        const std::size_t kvd = hd * kv_heads;
+        auto set_linear = [&](stratakv::layers::Linear& lin, const std::string& k, std::size_t out_f,
+                              std::size_t in_f) {
+            Tensor src = take(k);
+            lin.set_weight(stratakv::io::load_linear_bf16_transposed(src, out_f, in_f));
+        };
+        std::vector<stratakv::models::TransformerBlock> blocks;
+        std::vector<stratakv::memory::BlockPool> pools;
+        std::vector<stratakv::memory::PageTable> pages(layers);
+        Tensor gate0 = std::move(w.at("model.layers.0.mlp.gate_proj.weight"));
+        const std::size_t inter = gate0.shape()[0];
+        w.at("model.layers.0.mlp.gate_proj.weight") = std::move(gate0);
+        blocks.reserve(layers);
+        for (int l = 0; l < layers; ++l) {
+            blocks.emplace_back(h, inter, heads, kv_heads, 1024, 16, stratakv::Device::CPU);
+            pools.emplace_back(1024, 16);
+            auto& b = blocks.back();
+            const std::string p = "model.layers." + std::to_string(l) + ".";
+            b.input_norm() = stratakv::layers::RMSNorm(take(p + "input_layernorm.weight"));
+            b.post_attention_norm() = stratakv::layers::RMSNorm(take(p + "post_attention_layernorm.weight"));
+            set_linear(b.attention().query_projection(), p + "self_attn.q_proj.weight", h, h);
+            set_linear(b.attention().key_projection(), p + "self_attn.k_proj.weight", kvd, h);
+            set_linear(b.attention().value_projection(), p + "self_attn.v_proj.weight", kvd, h);
+            set_linear(b.attention().output_projection(), p + "self_attn.o_proj.weight", h, h);
+            set_linear(b.gate_projection(), p + "mlp.gate_proj.weight", inter, h);
+            set_linear(b.up_projection(), p + "mlp.up_proj.weight", inter, h);
+            set_linear(b.down_projection(), p + "mlp.down_proj.weight", h, inter);
+            pages[l].allocate_sequence(0, pools[l]);
+        }
+        stratakv::layers::RMSNorm final_norm(take("model.norm.weight"));
+        stratakv::layers::Linear lm_head(h, vocab);
+        set_linear(lm_head, "lm_head.weight", vocab, h);
+
+        auto embed = [&](const int32_t* ids, std::size_t n) {
+            Tensor x({n, h});
+            for (std::size_t r = 0; r < n; ++r)
+                for (std::size_t c = 0; c < h; ++c) x[r * h + c] = emb[static_cast<std::size_t>(ids[r]) * h + c];
+            return x;
+        };
+        auto forward = [&](Tensor x) {
+            for (int l = 0; l < layers; ++l) x = blocks[l].forward(x, 0, pages[l], pools[l], true);
+            return x;
+        };
+        Tensor hidden = forward(embed(tokens, n_prompt));
+        Tensor last({1, h});
+        for (std::size_t c = 0; c < h; ++c) last[c] = hidden[(n_prompt - 1) * h + c];
+        std::vector<std::size_t> order(vocab);
+        for (int s = 0; n_prompt + s <= n_tokens; ++s) {
+            Tensor logits = lm_head.forward(final_norm.forward(last));
+            std::size_t best = 0;
+            for (std::size_t i = 1; i < vocab; ++i)
+                if (logits[i] > logits[best]) best = i;
+            argmax[s] = static_cast<int32_t>(best);
+            std::iota(order.begin(), order.end(), std::size_t{0});
+            std::partial_sort(order.begin(), order.begin() + top_k, order.end(),
+                              [&](std::size_t a, std::size_t b) {
+                                  if (logits[a] != logits[b]) return logits[a] > logits[b];
+                                  return a < b;
+                              });
+            for (int k = 0; k < top_k; ++k) {
+                top_ids[static_cast<std::size_t>(s) * top_k + k] = static_cast<int32_t>(order[k]);
+                top_vals[static_cast<std::size_t>(s) * top_k + k] = logits[order[k]];
+            }
+            if (n_prompt + s == n_tokens) break;
+            if (tokens[n_prompt + s] < 0) tokens[n_prompt + s] = static_cast<int32_t>(best);
+            last = forward(embed(tokens + n_prompt + s, 1));
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        std::snprintf(err, err_cap, "%s", e.what());
+        return 1;
     }
 }
 

@@ -1,0 +1,402 @@
+// generator.cpp -- Generator: weight placement, and a generation loop whose
+// every step (embedding, layers, final norm, lm_head, token choice) is queued
+// on the device with the token ids kept in device memory.
+//
+// Configuration, weight-schema and generate() rules with their messages
+// follow src/generation/generator.cpp:169-200 (validate_config), :265-345
+// (take / load_linear / take_embedding / take_final_norm), :374-518 (the
+// constructor) and :617-803 (generate).
+#include "stratakv/generation/generator.h"
+
+#include <algorithm>
+#include <chrono>
+#include <climits>
+#include <cmath>
+#include <initializer_list>
+#include <limits>
+#include <stdexcept>
+#include <string>
+#include <utility>
+
+#include "abi_check.h"
+
+namespace stratakv {
+namespace generation {
+namespace {
+
+using Clock = std::chrono::steady_clock;
+
+std::size_t checked_elements(std::initializer_list<std::size_t> dims) {
+    const auto byte_limit = std::min<std::size_t>(std::numeric_limits<std::size_t>::max() - 63u,
+                                                  static_cast<std::size_t>(std::numeric_limits<std::ptrdiff_t>::max()));
+    const std::size_t limit = byte_limit / sizeof(float);
+    std::size_t n = 1;
+    for (std::size_t d : dims) {
+        if (d == 0 || n > limit / d) throw std::overflow_error("Generator: invalid/overflowing tensor size");
+        n *= d;
+    }
+    return n;
+}
+
+GeneratorConfig validate_config(GeneratorConfig c) {
+    if (c.device != Device::GPU) throw std::invalid_argument("Generator: GPU builds require Device::GPU");
+    const std::size_t kv = c.num_kv_heads == 0 ? c.num_heads : c.num_kv_heads;
+    if (c.hidden_dim == 0 || c.intermediate_dim == 0 || c.num_heads == 0 || c.num_layers == 0 || kv == 0 ||
+        c.num_heads % kv != 0 || c.vocab_size == 0 || c.vocab_size > static_cast<std::size_t>(INT_MAX) ||
+        c.total_blocks <= 0 || c.block_size <= 0 || c.hidden_dim % c.num_heads != 0 || c.eos_token_id < -1 ||
+        (c.eos_token_id >= 0 && static_cast<std::size_t>(c.eos_token_id) >= c.vocab_size))
+        throw std::invalid_argument("Generator: invalid configuration");
+    checked_elements({c.hidden_dim, c.hidden_dim});
+    checked_elements({c.hidden_dim, c.intermediate_dim});
+    checked_elements({c.vocab_size, c.hidden_dim});
+    checked_elements({c.num_layers, c.hidden_dim, c.hidden_dim});
+    checked_elements({c.num_layers, c.hidden_dim, c.intermediate_dim});
+    const std::size_t kv_dim = kv * (c.hidden_dim / c.num_heads);
+    checked_elements({c.num_layers, c.hidden_dim, kv_dim});
+    checked_elements({c.num_layers, static_cast<std::size_t>(c.total_blocks), static_cast<std::size_t>(c.block_size),
+                      kv_dim});
+    return c;
+}
+
+// Takes weights out of the map, checks shape and finiteness (on the device)
+// and converts them to the role's device form.
+class WeightTaker {
+public:
+    WeightTaker(io::WeightMap& weights, void* stream) : weights_(weights), stream_(stream) {
+        void* p = nullptr;
+        detail::check(skv_malloc(&p, sizeof(std::int32_t)), "Generator: weight check");
+        flag_ = static_cast<std::int32_t*>(p);
+    }
+    ~WeightTaker() { (void)skv_free(flag_); }
+    WeightTaker(const WeightTaker&) = delete;
+    WeightTaker& operator=(const WeightTaker&) = delete;
+
+    bool has(const std::string& key) const { return weights_.find(key) != weights_.end(); }
+
+    // Device tensor with the expected shape and only finite values, in its
+    // stored dtype (BF16 or FP32).
+    Tensor take(const std::string& key, std::initializer_list<std::size_t> expected) {
+        auto it = weights_.find(key);
+        if (it == weights_.end()) throw std::invalid_argument("Missing weight: " + key);
+        const Tensor& src = it->second;
+        if (src.shape() != std::vector<std::size_t>(expected) || src.num_elements() != checked_elements(expected) ||
+            !src.raw_data() || !src.is_contiguous())
+            throw std::invalid_argument("Wrong shape/storage: " + key);
+        Tensor t = src.device() == Device::GPU ? std::move(it->second) : src.to(Device::GPU);
+        weights_.erase(it);
+        const int dt = t.dtype() == DataType::BF16 ? SKV_DTYPE_BF16 : SKV_DTYPE_FP32;
+        detail::check(skv_memset_d8(flag_, 0, sizeof(std::int32_t), stream_), "Generator: weight check");
+        detail::check(skv_check_finite(t.raw_data(), dt, t.num_elements(), flag_, stream_), "Generator: weight check");
+        std::int32_t bad = 0;
+        detail::check(skv_memcpy_d2h(&bad, flag_, sizeof(bad), stream_), "Generator: weight check");
+        if (bad != 0) throw std::invalid_argument("Non-finite weight: " + key);
+        return t;
+    }
+
+    // FP32 norm gamma [n].
+    Tensor take_f32(const std::string& key, std::size_t n) {
+        Tensor t = take(key, {n});
+        if (t.dtype() == DataType::FP32) return t;
+        Tensor f({n}, DataType::FP32, Device::GPU);
+        detail::check(skv_convert_to_f32(t.raw_data(), SKV_DTYPE_BF16, n, static_cast<float*>(f.raw_data()), nullptr,
+                                         stream_),
+                      "Generator: norm weight");
+        detail::check(skv_stream_synchronize(stream_), "Generator: norm weight");
+        return f;
+    }
+
+    // A checkpoint [out, in] linear as BF16 rows behind a [in, out] view;
+    // FP32 values keep their upper 16 bits (src/generation/generator.cpp:292-328).
+    void take_linear(const std::string& key, layers::Linear& layer) {
+        const std::size_t in = layer.input_dim(), out = layer.output_dim();
+        Tensor t = take(key, {out, in});
+        if (t.dtype() != DataType::BF16) {
+            Tensor b({out, in}, DataType::BF16, Device::GPU);
+            detail::check(skv_convert_to_bf16(t.raw_data(), SKV_DTYPE_FP32, out * in,
+                                              static_cast<std::uint16_t*>(b.raw_data()), nullptr, stream_),
+                          "Generator: linear weight");
+            detail::check(skv_stream_synchronize(stream_), "Generator: linear weight");
+            t = std::move(b);
+        }
+        layer.set_weight(t.transpose_2d());
+    }
+
+private:
+    io::WeightMap& weights_;
+    void* stream_;
+    std::int32_t* flag_ = nullptr;
+};
+
+}  // namespace
+
+Generator::Generator(GeneratorConfig config, io::WeightMap weights)
+    : config_(validate_config(config)), sampler_(config_.sampler) {
+    const auto t0 = Clock::now();
+    const std::size_t h = config_.hidden_dim, inter = config_.intermediate_dim;
+    const std::size_t kv_heads = config_.num_kv_heads == 0 ? config_.num_heads : config_.num_kv_heads;
+    const std::size_t kv_dim = kv_heads * (h / config_.num_heads);
+    blocks_.reserve(config_.num_layers);
+    pools_.reserve(config_.num_layers);
+    for (std::size_t l = 0; l < config_.num_layers; ++l) {
+        blocks_.emplace_back(h, inter, config_.num_heads, kv_heads, config_.total_blocks, config_.block_size,
+                             Device::CPU);
+        pools_.emplace_back(config_.total_blocks, config_.block_size, static_cast<int>(kv_heads),
+                            static_cast<int>(h / config_.num_heads), Device::GPU);
+    }
+    pages_.resize(config_.num_layers);
+
+    WeightTaker w(weights, stream_);
+    const char* emb_key = w.has("model.embed_tokens.weight") ? "model.embed_tokens.weight" : "tok_embeddings.weight";
+    embeddings_.emplace(w.take(emb_key, {config_.vocab_size, h}));
+    const char* norm_key = w.has("model.norm.weight") ? "model.norm.weight" : "norm.weight";
+    final_norm_.emplace(w.take_f32(norm_key, h));
+    if (w.has("model.layers.0.input_layernorm.weight")) {
+        for (std::size_t l = 0; l < config_.num_layers; ++l) {
+            const std::string p = "model.layers." + std::to_string(l) + ".";
+            auto& b = blocks_[l];
+            b.input_norm() = layers::RMSNorm(w.take_f32(p + "input_layernorm.weight", h));
+            b.post_attention_norm() = layers::RMSNorm(w.take_f32(p + "post_attention_layernorm.weight", h));
+            w.take_linear(p + "self_attn.q_proj.weight", b.attention().query_projection());
+            w.take_linear(p + "self_attn.k_proj.weight", b.attention().key_projection());
+            w.take_linear(p + "self_attn.v_proj.weight", b.attention().value_projection());
+            w.take_linear(p + "self_attn.o_proj.weight", b.attention().output_projection());
+            w.take_linear(p + "mlp.gate_proj.weight", b.gate_projection());
+            w.take_linear(p + "mlp.up_proj.weight", b.up_projection());
+            w.take_linear(p + "mlp.down_proj.weight", b.down_projection());
+        }
+    } else {
+        // The one-layer "block.*" schema (src/generation/generator.cpp:430-461):
+        // its single FFN input matrix serves as both gate and up projection.
+        if (config_.num_layers != 1) throw std::invalid_argument("Generator: Llama layer weights are missing");
+        auto& b = blocks_.front();
+        b.input_norm() = layers::RMSNorm(w.take_f32("block.input_norm.weight", h));
+        b.post_attention_norm() = layers::RMSNorm(w.take_f32("block.post_attention_norm.weight", h));
+        w.take_linear("block.attn.q_proj.weight", b.attention().query_projection());
+        w.take_linear("block.attn.k_proj.weight", b.attention().key_projection());
+        w.take_linear("block.attn.v_proj.weight", b.attention().value_projection());
+        w.take_linear("block.attn.o_proj.weight", b.attention().output_projection());
+        w.take_linear("block.ffn.up_proj.weight", b.gate_projection());
+        b.up_projection().set_weight(b.gate_projection().weight().to(Device::GPU));
+        w.take_linear("block.ffn.down_proj.weight", b.down_projection());
+    }
+    lm_head_.emplace(h, config_.vocab_size);
+    w.take_linear("lm_head.weight", *lm_head_);
+    (void)kv_dim;
+
+    for (auto& b : blocks_) b.to(Device::GPU);
+    hidden_.emplace(std::vector<std::size_t>{1, h}, DataType::FP32, Device::GPU);
+    normed_.emplace(std::vector<std::size_t>{1, h}, DataType::FP32, Device::GPU);
+    logits_.emplace(std::vector<std::size_t>{1, config_.vocab_size}, DataType::FP32, Device::GPU);
+    void* p = nullptr;
+    detail::check(skv_malloc(&p, sizeof(std::int32_t)), "Generator: workspace");
+    flags_ = static_cast<std::int32_t*>(p);
+    step_events_.assign(kLookahead + 2, nullptr);
+    for (auto& e : step_events_) detail::check(skv_event_create(&e), "Generator: workspace");
+    if (!weights.empty()) throw std::invalid_argument("Unexpected weight: " + weights.begin()->first);
+    initialization_ms_ = std::chrono::duration<double, std::milli>(Clock::now() - t0).count();
+}
+
+Generator::~Generator() {
+    (void)skv_device_synchronize();
+    for (void* e : step_events_)
+        if (e) (void)skv_event_destroy(e);
+    if (ids_) (void)skv_free(ids_);
+    if (flags_) (void)skv_free(flags_);
+    if (host_ids_) (void)skv_host_free(host_ids_);
+}
+
+void Generator::set_stream(void* stream) {
+    stream_ = stream;
+    for (auto& b : blocks_) b.set_stream(stream);
+}
+
+std::size_t Generator::free_block_count() const noexcept {
+    std::size_t total = 0;
+    for (const auto& pool : pools_) total += pool.free_count();
+    return total;
+}
+
+void Generator::validate_prompt(const std::vector<int>& prompt, std::size_t extra) const {
+    for (int id : prompt)
+        if (id < 0 || static_cast<std::size_t>(id) >= config_.vocab_size)
+            throw std::invalid_argument("Generator: prompt token outside vocabulary");
+    if (prompt.size() > static_cast<std::size_t>(INT_MAX) - extra)
+        throw std::overflow_error("Generator: prompt plus max exceeds INT_MAX");
+}
+
+void Generator::begin_sequence(std::size_t tokens) {
+    const auto bs = static_cast<std::size_t>(config_.block_size);
+    const std::size_t blocks = tokens / bs + (tokens % bs != 0);
+    if (blocks > static_cast<std::size_t>(config_.total_blocks))
+        throw std::length_error("Generator: prompt plus max exceeds KV capacity");
+    if (tokens > ids_capacity_) {
+        (void)skv_device_synchronize();
+        if (ids_) (void)skv_free(ids_);
+        if (host_ids_) (void)skv_host_free(host_ids_);
+        ids_ = nullptr;
+        host_ids_ = nullptr;
+        ids_capacity_ = 0;
+        void* d = nullptr;
+        void* hp = nullptr;
+        detail::check(skv_malloc(&d, tokens * sizeof(std::int32_t)), "Generator: token buffer");
+        ids_ = static_cast<std::int32_t*>(d);
+        detail::check(skv_host_alloc(&hp, tokens * sizeof(std::int32_t)), "Generator: token buffer");
+        host_ids_ = static_cast<std::int32_t*>(hp);
+        ids_capacity_ = tokens;
+    }
+    std::size_t done = 0;
+    try {
+        for (; done < pages_.size(); ++done) {
+            pages_[done].allocate_sequence(0, pools_[done]);
+            pages_[done].reserve_device_block_table(blocks);
+        }
+    } catch (...) {
+        for (std::size_t l = 0; l < done; ++l)
+            if (pages_[l].has_sequence(0)) pages_[l].free_sequence(0, pools_[l]);
+        throw;
+    }
+}
+
+void Generator::end_sequence() noexcept {
+    (void)skv_stream_synchronize(stream_);
+    for (std::size_t l = 0; l < pages_.size(); ++l) {
+        try {
+            if (pages_[l].has_sequence(0)) pages_[l].free_sequence(0, pools_[l]);
+        } catch (...) {
+        }
+    }
+}
+
+void Generator::step(int in_index, float* logits) {
+    const int dtype = embeddings_->dtype() == DataType::BF16 ? SKV_DTYPE_BF16 : SKV_DTYPE_FP32;
+    const int h = static_cast<int>(config_.hidden_dim);
+    const int vocab = static_cast<int>(config_.vocab_size);
+    auto* x = static_cast<float*>(hidden_->raw_data());
+    detail::check(skv_embedding_f32(embeddings_->raw_data(), dtype, vocab, h, ids_, in_index, x, flags_, stream_),
+                  "Generator: embedding");
+    for (std::size_t l = 0; l < blocks_.size(); ++l)
+        blocks_[l].forward_into(*hidden_, *hidden_, 0, pages_[l], pools_[l], true);
+    if (logits == nullptr) return;
+    detail::check(skv_rmsnorm_f32(x, static_cast<float*>(normed_->raw_data()),
+                                  static_cast<const float*>(final_norm_->gamma().raw_data()), 1, h,
+                                  final_norm_->epsilon(), stream_),
+                  "Generator: final rmsnorm");
+    const Tensor& wt = lm_head_->weight();
+    detail::check(skv_linear_f32(static_cast<const float*>(normed_->raw_data()), 1, wt.raw_data(), SKV_DTYPE_BF16,
+                                 static_cast<int64_t>(wt.strides()[0]), static_cast<int64_t>(wt.strides()[1]), h,
+                                 vocab, nullptr, logits, stream_),
+                  "Generator: lm_head");
+}
+
+void Generator::raise_flags(std::int32_t flags) const {
+    if (flags & SKV_FLAG_NONFINITE_LOGITS)
+        throw std::runtime_error(
+            "CRITICAL NUMERICAL COLLAPSE: NaN/Inf detected in logits! Safetensors dtype mismatch (FP16 weights "
+            "fed to BF16 kernel).");
+    if (flags & SKV_FLAG_NONFINITE_SCALED) throw std::invalid_argument("Sampler: scaled logits are not finite");
+    if (flags & SKV_FLAG_BAD_DISTRIBUTION) throw std::runtime_error("Sampler: invalid softmax distribution");
+    if (flags & SKV_FLAG_BAD_TOKEN) throw std::runtime_error("Generator: token id outside vocabulary");
+}
+
+std::vector<int> Generator::generate(const std::vector<int>& prompt, int max_new_tokens) {
+    if (prompt.empty() || max_new_tokens < 0)
+        throw std::invalid_argument("Generator: nonempty prompt and nonnegative max required");
+    validate_prompt(prompt, static_cast<std::size_t>(max_new_tokens));
+    if (max_new_tokens == 0 || prompt.back() == config_.eos_token_id) return prompt;
+    const std::size_t P = prompt.size();
+    const std::size_t required = P + static_cast<std::size_t>(max_new_tokens);
+    const auto bs = static_cast<std::size_t>(config_.block_size);
+    if (required / bs + (required % bs != 0) > static_cast<std::size_t>(config_.total_blocks))
+        throw std::length_error("Generator: prompt plus max exceeds KV capacity");
+    checked_elements({P, config_.hidden_dim});
+    checked_elements({P, config_.intermediate_dim});
+    const auto t0 = Clock::now();
+    begin_sequence(required);
+    std::vector<int> result(prompt);
+    try {
+        for (std::size_t i = 0; i < P; ++i) host_ids_[i] = prompt[i];
+        detail::check(skv_memcpy_h2d_async(ids_, host_ids_, P * sizeof(std::int32_t), stream_), "Generator: prompt");
+        detail::check(skv_memset_d8(flags_, 0, sizeof(std::int32_t), stream_), "Generator: flags");
+        auto* logits = static_cast<float*>(logits_->raw_data());
+        const int vocab = static_cast<int>(config_.vocab_size);
+        for (std::size_t i = 0; i + 1 < P; ++i) step(static_cast<int>(i), nullptr);
+        step(static_cast<int>(P - 1), logits);
+
+        const int R = static_cast<int>(step_events_.size());
+        int checked = 0;      // generated tokens the host has read
+        bool stop = false;    // EOS seen at generated index `checked - 1`
+        int queued = 0;       // generated tokens queued
+        auto read_one = [&](bool wait) {
+            void* ev = step_events_[checked % R];
+            if (wait) {
+                detail::check(skv_event_synchronize(ev), "Generator: token copy");
+            } else {
+                int done = 0;
+                detail::check(skv_event_query(ev, &done), "Generator: token copy");
+                if (!done) return false;
+            }
+            const int tok = host_ids_[P + checked];
+            ++checked;
+            if (tok == config_.eos_token_id) stop = true;
+            return true;
+        };
+        for (int s = 0; s < max_new_tokens && !stop; ++s) {
+            const int pos = static_cast<int>(P) + s;
+            sampler_.sample_into(logits, vocab, ids_, pos, flags_, stream_);
+            detail::check(skv_memcpy_d2h_async(host_ids_ + pos, ids_ + pos, sizeof(std::int32_t), stream_),
+                          "Generator: token copy");
+            detail::check(skv_event_record(step_events_[s % R], stream_), "Generator: token copy");
+            queued = s + 1;
+            while (!stop && checked < queued && read_one(queued - checked > kLookahead)) {
+            }
+            if (stop || s + 1 == max_new_tokens) break;
+            step(pos, logits);  // embeds the token just chosen
+        }
+        while (!stop && checked < queued) read_one(true);
+        detail::check(skv_stream_synchronize(stream_), "Generator: generate");
+        std::int32_t flags = 0;
+        detail::check(skv_memcpy_d2h(&flags, flags_, sizeof(flags), stream_), "Generator: flags");
+        raise_flags(flags);
+        for (int s = 0; s < checked; ++s) result.push_back(host_ids_[P + s]);
+    } catch (...) {
+        end_sequence();
+        throw;
+    }
+    end_sequence();
+    last_generation_ms_ = std::chrono::duration<double, std::milli>(Clock::now() - t0).count();
+    return result;
+}
+
+std::vector<float> Generator::forced_logits(const std::vector<int>& tokens, std::size_t n_prompt) {
+    if (n_prompt == 0 || n_prompt > tokens.size())
+        throw std::invalid_argument("Generator: forced_logits needs 1 <= n_prompt <= tokens.size()");
+    validate_prompt(tokens, 0);
+    const std::size_t N = tokens.size();
+    const std::size_t rows = N - n_prompt + 1;
+    const std::size_t vocab = config_.vocab_size;
+    checked_elements({rows, vocab});
+    begin_sequence(N);
+    std::vector<float> out(rows * vocab);
+    try {
+        Tensor all({rows, vocab}, DataType::FP32, Device::GPU);
+        auto* base = static_cast<float*>(all.raw_data());
+        for (std::size_t i = 0; i < N; ++i) host_ids_[i] = tokens[i];
+        detail::check(skv_memcpy_h2d_async(ids_, host_ids_, N * sizeof(std::int32_t), stream_), "Generator: tokens");
+        detail::check(skv_memset_d8(flags_, 0, sizeof(std::int32_t), stream_), "Generator: flags");
+        for (std::size_t i = 0; i + 1 < n_prompt; ++i) step(static_cast<int>(i), nullptr);
+        for (std::size_t r = 0; r < rows; ++r) step(static_cast<int>(n_prompt - 1 + r), base + r * vocab);
+        detail::check(skv_stream_synchronize(stream_), "Generator: forced_logits");
+        detail::check(skv_memcpy_d2h(out.data(), base, out.size() * sizeof(float), stream_), "Generator: logits");
+        std::int32_t flags = 0;
+        detail::check(skv_memcpy_d2h(&flags, flags_, sizeof(flags), stream_), "Generator: flags");
+        raise_flags(flags & ~SKV_FLAG_NONFINITE_LOGITS);
+    } catch (...) {
+        end_sequence();
+        throw;
+    }
+    end_sequence();
+    return out;
+}
+
+}  // namespace generation
+}  // namespace stratakv

@@ -36,6 +36,7 @@ PageTable& PageTable::operator=(const PageTable& other) {
 PageTable::PageTable(PageTable&& other) noexcept
     : table_(std::move(other.table_)),
       d_block_table_(std::exchange(other.d_block_table_, nullptr)),
+      h_block_table_(std::exchange(other.h_block_table_, nullptr)),
       d_block_table_capacity_(std::exchange(other.d_block_table_capacity_, 0)),
       staged_seq_id_(other.staged_seq_id_),
       staged_block_count_(std::exchange(other.staged_block_count_, 0)),
@@ -46,6 +47,7 @@ PageTable& PageTable::operator=(PageTable&& other) noexcept {
         release_device_block_table();
         table_ = std::move(other.table_);
         d_block_table_ = std::exchange(other.d_block_table_, nullptr);
+        h_block_table_ = std::exchange(other.h_block_table_, nullptr);
         d_block_table_capacity_ = std::exchange(other.d_block_table_capacity_, 0);
         staged_seq_id_ = other.staged_seq_id_;
         staged_block_count_ = std::exchange(other.staged_block_count_, 0);
@@ -57,8 +59,12 @@ PageTable& PageTable::operator=(PageTable&& other) noexcept {
 PageTable::~PageTable() noexcept { release_device_block_table(); }
 
 void PageTable::release_device_block_table() noexcept {
+    // Queued kernels and copies may still use the table and its mirror.
+    if (d_block_table_ != nullptr || h_block_table_ != nullptr) (void)skv_device_synchronize();
     if (d_block_table_ != nullptr) (void)skv_free(d_block_table_);
+    if (h_block_table_ != nullptr) (void)skv_host_free(h_block_table_);
     d_block_table_ = nullptr;
+    h_block_table_ = nullptr;
     d_block_table_capacity_ = 0;
     staged_block_count_ = 0;
     device_table_dirty_ = true;
@@ -102,7 +108,7 @@ const SequenceState& PageTable::get_state(int seq_id) const {
 
 bool PageTable::has_sequence(int seq_id) const noexcept { return table_.count(seq_id) != 0; }
 
-const int* PageTable::get_device_block_table(int seq_id) {
+const int* PageTable::get_device_block_table(int seq_id, void* stream) {
     const SequenceState& state = get_state(seq_id);
     const std::size_t required = state.physical_blocks.size();
     if (required == 0) throw std::runtime_error("get_device_block_table: sequence has no physical blocks");
@@ -111,13 +117,19 @@ const int* PageTable::get_device_block_table(int seq_id) {
         reserve_device_block_table(std::max(required, 2 * d_block_table_capacity_));
     }
     // Blocks are only ever appended to a live sequence, so when the same
-    // sequence is staged and nothing else changed, only the tail is new.
+    // sequence is staged and nothing else changed, only the tail is new and
+    // the mirror entries it writes were never handed to a copy before.
     std::size_t first = 0;
     if (!device_table_dirty_ && staged_seq_id_ == seq_id && staged_block_count_ <= required)
         first = staged_block_count_;
+    else if (staged_block_count_ > 0)
+        // A full rewrite of the mirror: earlier copies out of it must be done.
+        detail::check(skv_device_synchronize(), "PageTable: block table upload");
     if (first < required) {
-        detail::check(skv_memcpy_h2d(d_block_table_ + first, state.physical_blocks.data() + first,
-                                     (required - first) * sizeof(int), nullptr),
+        std::copy(state.physical_blocks.begin() + static_cast<std::ptrdiff_t>(first),
+                  state.physical_blocks.end(), h_block_table_ + first);
+        detail::check(skv_memcpy_h2d_async(d_block_table_ + first, h_block_table_ + first,
+                                           (required - first) * sizeof(int), stream),
                       "PageTable: block table upload");
     }
     staged_seq_id_ = seq_id;
@@ -131,9 +143,16 @@ void PageTable::reserve_device_block_table(std::size_t capacity) {
     if (capacity > std::numeric_limits<std::size_t>::max() / sizeof(int))
         throw std::overflow_error("reserve_device_block_table: capacity is too large");
     void* replacement = nullptr;
+    void* mirror = nullptr;
     detail::check(skv_malloc(&replacement, capacity * sizeof(int)), "PageTable: block table allocation");
-    if (d_block_table_ != nullptr) (void)skv_free(d_block_table_);
+    const int rc = skv_host_alloc(&mirror, capacity * sizeof(int));
+    if (rc != SKV_OK) {
+        (void)skv_free(replacement);
+        detail::check(rc, "PageTable: block table allocation");
+    }
+    release_device_block_table();
     d_block_table_ = static_cast<int*>(replacement);
+    h_block_table_ = static_cast<int*>(mirror);
     d_block_table_capacity_ = capacity;
     device_table_dirty_ = true;
 }

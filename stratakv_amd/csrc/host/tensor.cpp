@@ -50,11 +50,12 @@ Tensor::Tensor(const std::vector<std::size_t>& shape, DataType dtype, Device dev
         detail::check(skv_stream_synchronize(nullptr), "Tensor: device zero fill");
         return;
     }
-    void* p = nullptr;
-    if (posix_memalign(&p, 64, bytes) != 0 || p == nullptr) throw std::bad_alloc();
-    owner_ = std::shared_ptr<void>(p, release_host);
-    data_ptr_ = p;
-    std::memset(p, 0, bytes);
+    // calloc hands large blocks out as fresh zero pages (nothing is touched
+    // until used); the data pointer is rounded up to 64 bytes.
+    void* raw = std::calloc(bytes + 64, 1);
+    if (raw == nullptr) throw std::bad_alloc();
+    owner_ = std::shared_ptr<void>(raw, release_host);
+    data_ptr_ = reinterpret_cast<void*>((reinterpret_cast<std::uintptr_t>(raw) + 63) & ~std::uintptr_t{63});
 }
 
 Tensor::Tensor(Tensor&& other) noexcept

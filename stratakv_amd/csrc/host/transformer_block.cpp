@@ -210,7 +210,7 @@ void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output,
     // The paged-KV hot path: device block table (only new block ids are
     // uploaded), then one launch that appends this token's K/V rows at
     // `position` (= context_len - 1) and decodes over the whole context.
-    const int* table = page_table.get_device_block_table(seq_id);
+    const int* table = page_table.get_device_block_table(seq_id, s);
     Tensor& ws = *decode_workspace_;
     detail::check(skv_paged_attention_decode_append(
                       cfp(queries), cfp(keys), cfp(values), SKV_DTYPE_FP32, block_pool.key_cache(),

@@ -218,6 +218,18 @@ int skv_event_synchronize(void* event) {
     return SKV_OK;
 }
 
+int skv_event_query(void* event, int* done) {
+    SKV_REQUIRE(event != nullptr && done != nullptr, "skv_event_query: NULL argument");
+    const hipError_t e = hipEventQuery(static_cast<hipEvent_t>(event));
+    if (e == hipErrorNotReady) {
+        *done = 0;
+        return SKV_OK;
+    }
+    SKV_HIP_TRY(e);
+    *done = 1;
+    return SKV_OK;
+}
+
 int skv_host_alloc(void** ptr, size_t bytes) {
     SKV_REQUIRE(ptr != nullptr, "skv_host_alloc: ptr is NULL");
     *ptr = nullptr;
@@ -235,6 +247,14 @@ int skv_memcpy_h2d_async(void* dst, const void* src, size_t bytes, void* stream)
     if (bytes == 0) return SKV_OK;
     SKV_REQUIRE(dst && src, "skv_memcpy_h2d_async: NULL pointer");
     SKV_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice,
+                               static_cast<hipStream_t>(stream)));
+    return SKV_OK;
+}
+
+int skv_memcpy_d2h_async(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return SKV_OK;
+    SKV_REQUIRE(dst && src, "skv_memcpy_d2h_async: NULL pointer");
+    SKV_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost,
                                static_cast<hipStream_t>(stream)));
     return SKV_OK;
 }
