@@ -27,6 +27,12 @@ SKV_ERR_UNSUPPORTED = 4
 
 DTYPE_BF16 = 0
 DTYPE_FP32 = 1
+DTYPE_F16 = 2
+
+FLAG_NONFINITE_LOGITS = 1
+FLAG_BAD_TOKEN = 2
+FLAG_NONFINITE_SCALED = 4
+FLAG_BAD_DISTRIBUTION = 8
 
 
 class SkvError(RuntimeError):
@@ -66,6 +72,8 @@ _PROTOS = {
     "skv_host_alloc": (_i32, [_c.POINTER(_vp), _sz]),
     "skv_host_free": (_i32, [_vp]),
     "skv_memcpy_h2d_async": (_i32, [_vp, _vp, _sz, _vp]),
+    "skv_memcpy_d2h_async": (_i32, [_vp, _vp, _sz, _vp]),
+    "skv_event_query": (_i32, [_vp, _c.POINTER(_i32)]),
     "skv_scatter_i32": (_i32, [_vp, _vp, _i32, _vp]),
     "skv_fill_normal_bf16": (_i32, [_vp, _sz, _u64, _u64, _vp]),
     "skv_fill_normal_scaled_bf16": (_i32, [_vp, _sz, _u64, _u64, _f32, _vp]),
@@ -98,6 +106,12 @@ _PROTOS = {
     "skv_fused_gate_up_swiglu_f32": (_i32, [_vp, _vp, _f32, _vp, _vp, _i32, _i64, _i64, _i64, _vp,
                                             _vp, _i32, _i32, _vp, _vp]),
     "skv_linear_residual_f32": (_i32, [_vp, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "skv_convert_to_bf16": (_i32, [_vp, _i32, _sz, _vp, _vp, _vp]),
+    "skv_convert_to_f32": (_i32, [_vp, _i32, _sz, _vp, _vp, _vp]),
+    "skv_check_finite": (_i32, [_vp, _i32, _sz, _vp, _vp]),
+    "skv_embedding_f32": (_i32, [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "skv_argmax_f32": (_i32, [_vp, _i32, _vp, _i32, _vp, _vp]),
+    "skv_sample_f32": (_i32, [_vp, _i32, _f32, _i32, _f32, _c.c_double, _vp, _i32, _vp, _vp]),
 }
 
 _lib = None
@@ -283,6 +297,35 @@ def gather_blocks(pool, total_blocks: int, table, num_blocks: int, block_elems: 
                                    _ptr(dst), stream))
 
 
+def convert_to_bf16(src, src_dtype: int, count: int, dst, nonfinite=None, stream=None) -> None:
+    _check(lib().skv_convert_to_bf16(_ptr(src), src_dtype, count, _ptr(dst), _ptr(nonfinite), stream))
+
+
+def convert_to_f32(src, src_dtype: int, count: int, dst, nonfinite=None, stream=None) -> None:
+    _check(lib().skv_convert_to_f32(_ptr(src), src_dtype, count, _ptr(dst), _ptr(nonfinite), stream))
+
+
+def check_finite(src, src_dtype: int, count: int, nonfinite, stream=None) -> None:
+    _check(lib().skv_check_finite(_ptr(src), src_dtype, count, _ptr(nonfinite), stream))
+
+
+def embedding(table, table_dtype: int, vocab: int, hidden: int, token_ids, index: int, out, flags=None,
+              stream=None) -> None:
+    _check(lib().skv_embedding_f32(_ptr(table), table_dtype, vocab, hidden, _ptr(token_ids), index, _ptr(out),
+                                   _ptr(flags), stream))
+
+
+def argmax(logits, n: int, token_ids, index: int, flags=None, stream=None) -> None:
+    _check(lib().skv_argmax_f32(_ptr(logits), n, _ptr(token_ids), index, _ptr(flags), stream))
+
+
+def sample(logits, n: int, temperature: float, top_k: int, top_p: float, uniform: float, token_ids,
+           index: int, flags=None, stream=None) -> None:
+    """token_ids[index] = the reference Sampler's choice for the draw `uniform`."""
+    _check(lib().skv_sample_f32(_ptr(logits), n, temperature, top_k, top_p, uniform, _ptr(token_ids), index,
+                                _ptr(flags), stream))
+
+
 class Event:
     def __init__(self):
         p = _c.c_void_p()
@@ -332,5 +375,6 @@ __all__ = [
     "LIB_PATH", "HEADER_PATH", "SkvError", "SkvInvalidArgument", "DTYPE_BF16", "DTYPE_FP32",
     "header_symbols", "lib", "device_count", "require_gpu", "synchronize", "DeviceBuffer",
     "fill_normal_bf16", "kv_append", "decode_workspace_bytes", "paged_decode",
-    "paged_attention_decode", "gather_blocks", "Event", "Stream",
+    "paged_attention_decode", "gather_blocks", "Event", "Stream", "convert_to_bf16", "convert_to_f32",
+    "check_finite", "embedding", "argmax", "sample",
 ]

@@ -10,12 +10,13 @@
 //   tool_model transpose IN OUT_F IN_F OUT
 //       io::load_linear_bf16_transposed of an FP32 [OUT_F, IN_F] file.
 //   tool_model generate <ckpt> MAX_NEW EOS [--host-loader] [--temp T]
-//       [--top-k K] [--top-p P] [--seed S] [--repeat N] -- PROMPT...
+//       [--top-k K] [--top-p P] [--repeat N] -- PROMPT...
 //       Generator::generate; prints tokens and timings.
 //   tool_model forced <ckpt> N_PROMPT OUT [--host-loader] -- TOKENS...
 //       Generator::forced_logits; writes [rows x vocab] FP32 logits.
 // Model dimensions are inferred from the checkpoint the way the reference's
 // CLI does (src/cli.cpp:80-140).
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <fstream>
@@ -158,7 +159,6 @@ struct GenArgs {
     std::string path;
     bool host_loader = false;
     generation::SamplerConfig sampler{0.0f, 0, 1.0f};
-    long seed = -1;
     int repeat = 1;
     std::vector<int> tokens;
 };
@@ -176,7 +176,6 @@ GenArgs parse_gen(int first, int argc, char** argv) {
         else if (s == "--temp") a.sampler.temperature = std::stof(argv[++i]);
         else if (s == "--top-k") a.sampler.top_k = std::stoi(argv[++i]);
         else if (s == "--top-p") a.sampler.top_p = std::stof(argv[++i]);
-        else if (s == "--seed") a.seed = std::stol(argv[++i]);
         else if (s == "--repeat") a.repeat = std::stoi(argv[++i]);
     }
     for (; i < argc; ++i) a.tokens.push_back(std::stoi(argv[i]));
@@ -210,10 +209,6 @@ int cmd_generate(int argc, char** argv) {
         auto cfg = config_for(l.dims, eos);
         cfg.sampler = a.sampler;
         generation::Generator gen(cfg, std::move(l.weights));
-        if (a.seed >= 0) {
-            // A seeded sampler (the reference's Sampler(config, seed)).
-            // Generator owns its sampler; rebuild it through the config path.
-        }
         std::vector<int> out;
         std::vector<double> gen_ms;
         for (int r = 0; r < a.repeat; ++r) {
