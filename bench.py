@@ -467,6 +467,24 @@ def run_cfg1(steps: int, warmup: int, with_cpu: bool):
                 "embedding, lm_head and sampling are not part of this build"))
         else:
             log(f"layer stack driver failed ({proc.returncode}): {proc.stderr.strip()[-300:]}")
+    # The whole generation through Generator::generate (embedding, 22 layers,
+    # final norm, lm_head, greedy choice on the device), the reference CLI's run.
+    gen_driver = os.path.join(ROOT, "build", "bin", "bench_generate")
+    if os.path.exists(gen_driver):
+        import subprocess
+        proc = subprocess.run([gen_driver, "--repeat", "5"], stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                              text=True, timeout=600)
+        if proc.returncode == 0:
+            g = json.loads(proc.stdout.strip().splitlines()[-1])
+            weight_bytes = 2 * (CFG1_LAYERS * (2 * 2048 * 2048 + 2 * 256 * 2048 + 3 * 5632 * 2048) + 32000 * 2048)
+            g["weight_gbs_per_decode_token"] = round(weight_bytes / (g["decode_ms_per_token"] / 1e3) / 1e9, 1)
+            line["generator"] = dict(g, note=(
+                "Generator::generate of a TinyLlama-shaped model, bf16 N(0,0.02) weights, 16 prompt + 128 greedy "
+                "tokens, everything on the device; tokens_per_s = 128 / gen time incl. the prompt (the "
+                "reference CLI's pure_decode_tps definition); decode_ms_per_token from generate(128) - "
+                "generate(1); weight_gbs = bf16 weight bytes read per decode token / decode time"))
+        else:
+            log(f"generate driver failed ({proc.returncode}): {proc.stderr.strip()[-300:]}")
     if with_cpu:
         import oracle
         # One layer's 144 single-sequence decodes with the oracle, scaled to 22 layers.
