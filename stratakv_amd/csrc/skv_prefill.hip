@@ -9,24 +9,29 @@
 // table).  The reference computes it on the CPU only.
 //
 // Kernel (block_size 16, head_dim 64/128, G = Hq/Hkv in {1, 2, 4, 8, 16}):
-// * A workgroup of 4 wavefronts owns 64 query rows = the G heads of one kv
-//   head for 64/G consecutive tokens of one sequence; wavefront w owns rows
-//   16w..16w+15 (row r = token * G + head).  Every K/V byte staged in LDS is
-//   used by all 64 rows.
-// * Keys are walked 32 at a time (two 16-token blocks) up to the tile's last
-//   position.  The workgroup stages K row-major (16-byte chunks XOR-swizzled
-//   by row) and V transposed (Vt[dim][key], padded rows) in LDS; the next
-//   step's K/V are loaded into registers while the current one is computed.
+// * A workgroup of 8 wavefronts owns 256 query rows = the G heads of one kv
+//   head for 256/G consecutive tokens of one sequence (row r = token * G +
+//   head); wavefront w owns rows 32w..32w+31 as two 16-row column groups.
+//   Every K/V byte staged in LDS serves all 256 rows.
+// * Keys are walked 64 at a time (four 16-token blocks) up to the tile's last
+//   position, through two LDS buffers: the next step's K/V are loaded into
+//   registers while the current step is computed, then stored into the other
+//   buffer; one barrier per step.  Rows are padded (K by 16 bytes, V by 32) so
+//   the operand reads below hit distinct banks.  The heaviest tiles (the
+//   latest tokens of each sequence) are scheduled first.
 // * S^T = K Q^T on the matrix cores (v_mfma_f32_16x16x32_bf16: keys as rows,
-//   query rows as columns), so each lane holds 8 scores of ONE query row
-//   (column lane % 16): the causal/validity mask, the row max (2 shuffles)
-//   and the rescale of that row's output are lane-local.
-// * O^T += Vt P^T, also on the matrix cores: P goes from the S^T output
-//   straight into the B operand (bf16, 8 keys per lane) with the key order
-//   {4j..4j+3, 16+4j..16+4j+3} of lane group j, and the A operand reads Vt in
-//   the same key order, so no shuffle or LDS round trip is needed for P.  P is
-//   split into hi + lo bf16 parts (two MFMAs) so the P.V products keep ~16
-//   mantissa bits, like the fp32 loops of the reference.
+//   query rows as columns), so each lane holds the scores of ONE query row:
+//   the causal/validity mask, the row max (2 shuffles) and the rescale of that
+//   row's output are lane-local.  Each K operand read serves both column
+//   groups.
+// * O^T += V^T P^T, also on the matrix cores: P goes from the S^T output
+//   registers straight into the B operand (keys {4j..4j+3, 16+4j..16+4j+3} of
+//   lane group j), and the V^T operand comes out of the row-major V tile with
+//   the LDS transpose read (ds_read_b64_tr_b16: in each 16-lane group, lane
+//   4a + c receives element c of the 8-byte rows addressed by lanes a, a+4,
+//   a+8, a+12), in the same key order.  P is split into hi + lo bf16 parts
+//   (two MFMAs) so the P.V products keep ~16 mantissa bits, like the fp32
+//   loops of the reference.
 // * Online softmax in the exp2 domain with lazy rescaling (threshold 2^8).
 // Other shapes run a simple kernel (one wavefront per token and query head).
 #include "skv_common.h"
@@ -63,14 +68,19 @@ __device__ __forceinline__ int chunk_tokens(const PrefillParams& p, int b) {
 }
 
 // Tiles of tile_tokens tokens per sequence, prefix-summed into T_s[0..B] by
-// wavefront 0 (the same scan for every workgroup); returns the total.
+// wavefront 0 (the same scan for every workgroup), T_s[B + 1] = the largest
+// per-sequence count; returns the total.
 __device__ int prefill_tile_scan(const PrefillParams& p, int* T_s) {
     const int lane = threadIdx.x;
     if (lane < 64) {
-        int carry = 0;
+        int carry = 0, most = 0;
         for (int b0 = 0; b0 < p.B; b0 += 64) {
             const int b = b0 + lane;
             int v = b < p.B ? cdiv(chunk_tokens(p, b), p.tile_tokens) : 0;
+            int mx = v;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o, 64));
+            most = max(most, mx);
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const int u = __shfl_up(v, o, 64);
@@ -79,7 +89,10 @@ __device__ int prefill_tile_scan(const PrefillParams& p, int* T_s) {
             if (b < p.B) T_s[b + 1] = carry + v;
             carry += __shfl(v, 63, 64);
         }
-        if (lane == 0) T_s[0] = 0;
+        if (lane == 0) {
+            T_s[0] = 0;
+            T_s[p.B + 1] = most;
+        }
     }
     __syncthreads();
     return T_s[p.B];
@@ -97,43 +110,72 @@ __device__ __forceinline__ int find_tile_seq(const int* T, int B, int tile) {
 // ---------------------------------------------------------------------------
 // MFMA kernel.  Lane layouts (16x16x32 MFMA): lane (t, j) = (lane % 16,
 // lane / 16).  A operand of S^T: key row t (+16 kt), head-dim chunk 4cc + j;
-// B operand: query row t, chunk 4cc + j; S^T output: keys 4j + i (+16 kt),
-// query row t.  P^T B operand: query row t, keys {4j..4j+3, 16+4j..16+4j+3};
-// Vt A operand: dim 16 dt + t, the same 8 keys; O^T output: dims 16 dt + 4j
-// + i, query row t.
+// B operand: query row t of column group c, chunk 4cc + j; S^T output: keys
+// 4j + i (+16 kt), query row t.  P^T B operand: query row t, keys {4j..4j+3,
+// 16+4j..16+4j+3} of a 32-key chunk; V^T A operand: dim 16 dt + t, the same 8
+// keys; O^T output: dims 16 dt + 4j + i, query row t.
 // ---------------------------------------------------------------------------
+constexpr int kPrefillWaves = 8;
+constexpr int kPrefillRows = kPrefillWaves * 32;   // query rows per workgroup
+constexpr int kPrefillKeys = 64;                   // keys per step
+
+template <int HD>
+struct PrefillLds {
+    static constexpr int KRS = HD * 2 + 16;        // K row stride (bytes)
+    static constexpr int VRS = HD * 2 + 32;        // V row stride (bytes)
+    static constexpr int KB = kPrefillKeys * KRS;
+    static constexpr int BUF = KB + kPrefillKeys * VRS;
+    static constexpr int TOTAL = 2 * BUF;          // two buffers; the tile scan follows
+};
+
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
+    const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 template <int HD, int G, bool QF32>
-__global__ __launch_bounds__(256) void prefill_mfma_kernel(PrefillParams p) {
-    constexpr int KS = 32;                  // keys per step (two blocks)
+__global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(PrefillParams p) {
+    using Lds = PrefillLds<HD>;
+    constexpr int KS = kPrefillKeys;
     constexpr int CH = HD / 8;              // 16-byte chunks per row
-    constexpr int NMF = HD / 32;            // MFMAs per 16 keys for S
+    constexpr int NKC = HD / 32;            // 32-dim steps of S
     constexpr int NDT = HD / 16;            // 16-dim tiles of O
     constexpr int QP = QF32 ? 2 : 1;
-    constexpr int QT = 64 / G;              // tokens per tile
-    constexpr int VS = KS + 4;              // Vt row stride (bf16): 72 bytes
-    constexpr int LOADS = KS * CH / 256;    // 16-byte chunks per thread per step (K, and V)
-    static_assert(LOADS >= 1 && KS * CH % 256 == 0, "load split");
+    constexpr int QT = kPrefillRows / G;    // tokens per tile
+    constexpr int NT = 64 * kPrefillWaves;
+    constexpr int LOADS = KS * CH / NT;     // 16-byte chunks per thread per step (K, and V)
+    static_assert(LOADS >= 1 && KS * CH % NT == 0, "load split");
 
-    extern __shared__ int T_s[];            // [B + 1] tile prefix
-    __shared__ u32x4_t k_s[KS * CH];        // K: row R, chunk c at R*CH + (c ^ swz(R))
-    __shared__ uint16_t vt_s[HD * VS];      // V transposed: [dim][key]
-    // Swizzle of K's 16-byte chunks by row so the 16 rows an MFMA operand read
-    // touches (one chunk column) fall in 16 different bank groups.
-    auto swz = [](int R) { return CH == 16 ? (R & 15) : ((R >> 1) & 7); };
+    extern __shared__ __align__(16) unsigned char lds[];
+    int* T_s = reinterpret_cast<int*>(lds + Lds::TOTAL);   // [B + 2]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t = lane & 15, j = lane >> 4;
     const int kvh = blockIdx.x % p.Hkv;
-    const int tile = blockIdx.x / p.Hkv;
+    const int slot = blockIdx.x / p.Hkv;
 
     const int ntiles = prefill_tile_scan(p, T_s);
-    if (tile >= ntiles) return;
-    const int b = find_tile_seq(T_s, p.B, tile);
+    if (slot >= ntiles) return;
+    // Heaviest first: with equal tile counts, the last tile of every sequence,
+    // then the one before, ...; otherwise the global order reversed.
+    const int most = T_s[p.B + 1];
+    int b, tile_in_seq;
+    if (most * p.B == ntiles) {
+        b = slot % p.B;
+        tile_in_seq = most - 1 - slot / p.B;
+    } else {
+        const int tile = ntiles - 1 - slot;
+        b = find_tile_seq(T_s, p.B, tile);
+        tile_in_seq = tile - T_s[b];
+    }
     const int n = chunk_tokens(p, b);
     const int L = p.lens[b];
-    const int tok0 = (tile - T_s[b]) * QT;             // first chunk token of the tile
+    const int tok0 = tile_in_seq * QT;
     const int ntok = min(QT, n - tok0);
     const int base_pos = L - n + tok0;                 // position of the tile's first token
     const int last_pos = base_pos + ntok - 1;
@@ -142,59 +184,68 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(PrefillParams p) {
     const int32_t* table = p.tables + static_cast<int64_t>(b) * p.max_blocks;
     const int64_t row_stride = static_cast<int64_t>(p.Hkv) * HD;
 
-    // This lane's query row (column t of the S^T tiles).
-    const int r = wv * 16 + t;
-    const int qtok = r / G, qhead = kvh * G + (r % G);
-    const bool row_live = qtok < ntok;
-    const int qpos = row_live ? base_pos + qtok : -1;  // -1: every key masked
-    const int64_t qrow = static_cast<int64_t>(p.offsets[b] + tok0 + qtok) * p.Hq + qhead;
-
-    bf16x8_t qop[QP][NMF];
+    // This lane's two query rows (column t of the two column groups).
+    int qpos[2];
+    int64_t qrow[2];
+    bool live[2];
 #pragma unroll
-    for (int cc = 0; cc < NMF; ++cc) {
-        u32x4_t hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
-        if (row_live) {
-            const int64_t off = qrow * HD + (4 * cc + j) * 8;
-            if constexpr (QF32) {
-                const float4* qp = reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + off);
-                const float4 a0 = qp[0], a1 = qp[1];
-                const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-                uint32_t hb[8], lb[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    hb[e] = f32_to_bf16_bits(x[e]);
-                    lb[e] = f32_to_bf16_bits(x[e] - __uint_as_float(hb[e] << 16));
-                }
-                hi = u32x4_t{hb[0] | hb[1] << 16, hb[2] | hb[3] << 16, hb[4] | hb[5] << 16, hb[6] | hb[7] << 16};
-                lo = u32x4_t{lb[0] | lb[1] << 16, lb[2] | lb[3] << 16, lb[4] | lb[5] << 16, lb[6] | lb[7] << 16};
-            } else {
-                hi = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.q) + off);
-            }
-        }
-        qop[0][cc] = __builtin_bit_cast(bf16x8_t, hi);
-        if constexpr (QF32) qop[QP - 1][cc] = __builtin_bit_cast(bf16x8_t, lo);
+    for (int c = 0; c < 2; ++c) {
+        const int r = wv * 32 + c * 16 + t;
+        const int qtok = r / G, qhead = kvh * G + r % G;
+        live[c] = qtok < ntok;
+        qpos[c] = live[c] ? base_pos + qtok : -1;      // -1: every key masked
+        qrow[c] = static_cast<int64_t>(p.offsets[b] + tok0 + qtok) * p.Hq + qhead;
     }
 
-    // Loader mapping: thread -> (key row lr, chunk lc) for each of LOADS passes;
-    // 16 consecutive threads read one 256-byte (HD 128) row slice.  `valid`
-    // (the same in every thread) has bit k set when key k0 + k exists: below
-    // keys_end and in a block whose table entry is inside the pool.
-    auto load_step = [&](int k0, u32x4_t (&kr)[LOADS], u32x4_t (&vr)[LOADS], uint32_t& valid) {
+    bf16x8_t qop[QP][2][NKC];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int cc = 0; cc < NKC; ++cc) {
+            u32x4_t hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
+            if (live[c]) {
+                const int64_t off = qrow[c] * HD + (4 * cc + j) * 8;
+                if constexpr (QF32) {
+                    const float4* qp = reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + off);
+                    const float4 a0 = qp[0], a1 = qp[1];
+                    const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                    uint32_t hb[4], lb[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        hb[e] = pack2_bf16(x[2 * e], x[2 * e + 1]);
+                        lb[e] = pack2_bf16(x[2 * e] - __uint_as_float(hb[e] << 16),
+                                           x[2 * e + 1] - __uint_as_float(hb[e] & 0xFFFF0000u));
+                    }
+                    hi = u32x4_t{hb[0], hb[1], hb[2], hb[3]};
+                    lo = u32x4_t{lb[0], lb[1], lb[2], lb[3]};
+                } else {
+                    hi = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.q) + off);
+                }
+            }
+            qop[0][c][cc] = __builtin_bit_cast(bf16x8_t, hi);
+            if constexpr (QF32) qop[QP - 1][c][cc] = __builtin_bit_cast(bf16x8_t, lo);
+        }
+
+    // Loader mapping: thread -> (key row lr, chunk lc) for each of LOADS
+    // passes; CH consecutive threads read one row slice.  `valid` (the same in
+    // every thread) has bit k set when key k0 + k exists: below keys_end and in
+    // a block whose table entry is inside the pool.
+    auto load_step = [&](int k0, u32x4_t (&kr)[LOADS], u32x4_t (&vr)[LOADS], uint64_t& valid) {
         valid = 0;
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
+        for (int hb = 0; hb < KS / 16; ++hb) {
             const int kb = k0 + 16 * hb;
             if (kb < keys_end) {
                 const int64_t pb = table[kb >> 4];
                 if (pb >= 0 && pb < p.total_blocks) {
                     const int cnt = min(16, keys_end - kb);
-                    valid |= (cnt == 16 ? 0xFFFFu : ((1u << cnt) - 1u)) << (16 * hb);
+                    valid |= static_cast<uint64_t>(cnt == 16 ? 0xFFFFu : ((1u << cnt) - 1u)) << (16 * hb);
                 }
             }
         }
 #pragma unroll
         for (int u = 0; u < LOADS; ++u) {
-            const int idx = tid + 256 * u;
+            const int idx = tid + NT * u;
             const int lr = idx / CH, lc = idx % CH;
             kr[u] = u32x4_t{0u, 0u, 0u, 0u};
             vr[u] = u32x4_t{0u, 0u, 0u, 0u};
@@ -202,125 +253,158 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(PrefillParams p) {
                 const int key = k0 + lr;
                 const int64_t pb = table[key >> 4];
                 const int64_t off = (pb * 16 + (key & 15)) * row_stride + static_cast<int64_t>(kvh) * HD + lc * 8;
-                kr[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p.k + off));
-                vr[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p.v + off));
+                kr[u] = *reinterpret_cast<const u32x4_t*>(p.k + off);
+                vr[u] = *reinterpret_cast<const u32x4_t*>(p.v + off);
             }
         }
     };
     // Rows of keys that do not exist are stored as zeros (V must not carry
     // NaN from unused slots into 0 * V).
-    auto store_step = [&](const u32x4_t (&kr)[LOADS], const u32x4_t (&vr)[LOADS]) {
+    auto store_step = [&](int buf, const u32x4_t (&kr)[LOADS], const u32x4_t (&vr)[LOADS]) {
+        unsigned char* kb = lds + buf * Lds::BUF;
+        unsigned char* vb = kb + Lds::KB;
 #pragma unroll
         for (int u = 0; u < LOADS; ++u) {
-            const int idx = tid + 256 * u;
+            const int idx = tid + NT * u;
             const int lr = idx / CH, lc = idx % CH;
-            k_s[lr * CH + (lc ^ swz(lr))] = kr[u];
-            const uint32_t w[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                vt_s[(lc * 8 + e) * VS + lr] = static_cast<uint16_t>((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu));
+            *reinterpret_cast<u32x4_t*>(kb + lr * Lds::KRS + lc * 16) = kr[u];
+            *reinterpret_cast<u32x4_t*>(vb + lr * Lds::VRS + lc * 16) = vr[u];
         }
     };
 
-    f32x4_t acc[NDT];
+    f32x4_t acc[NDT][2];
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    float m = -INFINITY;   // reference max of this lane's row (log2 units)
-    float lsum = 0.0f;     // this lane's share of the row's denominator
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[dt][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m[2] = {-INFINITY, -INFINITY};   // reference max of each row (log2 units)
+    float lsum[2] = {0.0f, 0.0f};          // this lane's share of each row's denominator
 
     const int nsteps = cdiv(keys_end, KS);
     u32x4_t kr[LOADS], vr[LOADS];
-    uint32_t valid = 0, valid_next = 0;
-    if (nsteps > 0) load_step(0, kr, vr, valid);
+    uint64_t valid_cur = 0, valid_next = 0;
+    if (nsteps > 0) {
+        load_step(0, kr, vr, valid_cur);
+        store_step(0, kr, vr);
+    }
+    __syncthreads();
     for (int st = 0; st < nsteps; ++st) {
-        __syncthreads();                 // every wavefront is done with the previous tiles
-        store_step(kr, vr);
-        __syncthreads();
-        const uint32_t kvalid = valid;
-        if (st + 1 < nsteps) {           // the next step's loads are in flight during compute
-            load_step((st + 1) * KS, kr, vr, valid_next);
-            valid = valid_next;
-        }
-
-        // ---- S^T tiles (keys 16 kt + 4j + i, query row t)
-        f32x4_t s[2];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            s[kt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-            const int R = kt * 16 + t;
-#pragma unroll
-            for (int cc = 0; cc < NMF; ++cc) {
-                const bf16x8_t a = __builtin_bit_cast(bf16x8_t, k_s[R * CH + ((4 * cc + j) ^ swz(R))]);
-#pragma unroll
-                for (int qp = 0; qp < QP; ++qp)
-                    s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qop[qp][cc], s[kt], 0, 0, 0);
-            }
-        }
-        float sc[8];
+        const int cur = st & 1;
+        if (st + 1 < nsteps) load_step((st + 1) * KS, kr, vr, valid_next);  // in flight during compute
+        const unsigned char* kb = lds + cur * Lds::BUF;
+        const unsigned char* vb = kb + Lds::KB;
         const int k0 = st * KS;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int kl = kt * 16 + 4 * j + i;
-                const bool keep = ((kvalid >> kl) & 1u) && (k0 + kl <= qpos);
-                sc[kt * 4 + i] = keep ? s[kt][i] * p.qscale : -INFINITY;
-            }
-        float mb = sc[0];
-#pragma unroll
-        for (int e = 1; e < 8; ++e) mb = fmaxf(mb, sc[e]);
-        mb = fmaxf(mb, shfl_xor_f(mb, 16));
-        mb = fmaxf(mb, shfl_xor_f(mb, 32));
-        if (mb > m + kPrefillLazy) {     // per-lane: the row's state is lane-local
-            const float alpha = m == -INFINITY ? 0.0f : fast_exp2(m - mb);
-            m = mb;
-            lsum *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha;
-        }
-        const float ms = m == -INFINITY ? 0.0f : m;
-        float pr[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            pr[e] = fast_exp2(sc[e] - ms);
-            lsum += pr[e];
-        }
-        // P^T operand, hi + lo bf16 parts.
-        uint32_t ph[8], pl[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            ph[e] = f32_to_bf16_bits(pr[e]);
-            pl[e] = f32_to_bf16_bits(pr[e] - __uint_as_float(ph[e] << 16));
-        }
-        const bf16x8_t phi = __builtin_bit_cast(
-            bf16x8_t, u32x4_t{ph[0] | ph[1] << 16, ph[2] | ph[3] << 16, ph[4] | ph[5] << 16, ph[6] | ph[7] << 16});
-        const bf16x8_t plo = __builtin_bit_cast(
-            bf16x8_t, u32x4_t{pl[0] | pl[1] << 16, pl[2] | pl[3] << 16, pl[4] | pl[5] << 16, pl[6] | pl[7] << 16});
 
-        // ---- O^T += Vt P^T
+        // ---- S^T tiles: s[c][kt] = scores of keys 16 kt + 4j + i, row t of group c
+        f32x4_t s[2][KS / 16];
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-            const uint16_t* vrow = vt_s + (dt * 16 + t) * VS;
-            const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 4 * j);
-            const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * j);
-            const bf16x8_t a = __builtin_bit_cast(bf16x8_t, u32x4_t{a0.x, a0.y, a1.x, a1.y});
-            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, phi, acc[dt], 0, 0, 0);
-            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, plo, acc[dt], 0, 0, 0);
+        for (int kt = 0; kt < KS / 16; ++kt) {
+            s[0][kt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            s[1][kt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int cc = 0; cc < NKC; ++cc) {
+                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(kb + (kt * 16 + t) * Lds::KRS + (4 * cc + j) * 16);
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int qp = 0; qp < QP; ++qp)
+                        s[c][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qop[qp][c][cc], s[c][kt], 0, 0, 0);
+            }
         }
+
+        // ---- online softmax per row, P^T operands (hi + lo bf16 parts)
+        bf16x8_t phi[2][KS / 32], plo[2][KS / 32];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            float sc[KS / 4];
+#pragma unroll
+            for (int kt = 0; kt < KS / 16; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int kl = kt * 16 + 4 * j + i;
+                    const bool keep = ((valid_cur >> kl) & 1u) && (k0 + kl <= qpos[c]);
+                    sc[kt * 4 + i] = keep ? s[c][kt][i] * p.qscale : -INFINITY;
+                }
+            float mb = sc[0];
+#pragma unroll
+            for (int e = 1; e < KS / 4; ++e) mb = fmaxf(mb, sc[e]);
+            mb = fmaxf(mb, shfl_xor_f(mb, 16));
+            mb = fmaxf(mb, shfl_xor_f(mb, 32));
+            if (mb > m[c] + kPrefillLazy) {   // lane-local: the row's state lives in this lane
+                const float alpha = m[c] == -INFINITY ? 0.0f : fast_exp2(m[c] - mb);
+                m[c] = mb;
+                lsum[c] *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[dt][c][i] *= alpha;
+            }
+            const float ms = m[c] == -INFINITY ? 0.0f : m[c];
+            float pr[KS / 4];
+#pragma unroll
+            for (int e = 0; e < KS / 4; ++e) {
+                pr[e] = fast_exp2(sc[e] - ms);
+                lsum[c] += pr[e];
+            }
+            // 32-key chunk h: keys {4j..4j+3} = kt 2h, {16+4j..} = kt 2h+1.
+#pragma unroll
+            for (int h = 0; h < KS / 32; ++h) {
+                uint32_t hw[4], lw[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float x0 = pr[8 * h + 2 * e], x1 = pr[8 * h + 2 * e + 1];
+                    hw[e] = pack2_bf16(x0, x1);
+                    lw[e] = pack2_bf16(x0 - __uint_as_float(hw[e] << 16), x1 - __uint_as_float(hw[e] & 0xFFFF0000u));
+                }
+                phi[c][h] = __builtin_bit_cast(bf16x8_t, u32x4_t{hw[0], hw[1], hw[2], hw[3]});
+                plo[c][h] = __builtin_bit_cast(bf16x8_t, u32x4_t{lw[0], lw[1], lw[2], lw[3]});
+            }
+        }
+
+        // ---- O^T += V^T P^T; V^T through the LDS transpose read.  Source
+        // lane 16g + a + 4e addresses key 32h + 16r + 4g + e, dims 16dt + 4a.
+        const int ga = lane & 3, ge = (lane >> 2) & 3, gg = lane >> 4;
+#pragma unroll
+        for (int h = 0; h < KS / 32; ++h) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                v4s_t part[2];
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const int key = 32 * h + 16 * r + 4 * gg + ge;
+                    const unsigned char* src = vb + key * Lds::VRS + (16 * dt + 4 * ga) * 2;
+                    part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4s_t*)(src));
+                }
+                const u32x4_t w = {__builtin_bit_cast(uint2, part[0]).x, __builtin_bit_cast(uint2, part[0]).y,
+                                   __builtin_bit_cast(uint2, part[1]).x, __builtin_bit_cast(uint2, part[1]).y};
+                const bf16x8_t a = __builtin_bit_cast(bf16x8_t, w);
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    acc[dt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, phi[c][h], acc[dt][c], 0, 0, 0);
+                    acc[dt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, plo[c][h], acc[dt][c], 0, 0, 0);
+                }
+            }
+        }
+
+        if (st + 1 < nsteps) store_step(cur ^ 1, kr, vr);
+        __syncthreads();
+        valid_cur = valid_next;
     }
 
-    // ---- output: O[row t][dims 16 dt + 4j + i] = acc / l
-    float ltot = lsum + shfl_xor_f(lsum, 16);
-    ltot += shfl_xor_f(ltot, 32);
-    if (row_live) {
-        const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
-        float* o = p.out + qrow * HD;
+    // ---- output: O[row][dims 16 dt + 4j + i] = acc / l
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-            *reinterpret_cast<float4*>(o + dt * 16 + 4 * j) =
-                make_float4(acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv, acc[dt][3] * inv);
+    for (int c = 0; c < 2; ++c) {
+        float ltot = lsum[c] + shfl_xor_f(lsum[c], 16);
+        ltot += shfl_xor_f(ltot, 32);
+        if (live[c]) {
+            const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+            float* o = p.out + qrow[c] * HD;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+                *reinterpret_cast<float4*>(o + dt * 16 + 4 * j) =
+                    make_float4(acc[dt][c][0] * inv, acc[dt][c][1] * inv, acc[dt][c][2] * inv, acc[dt][c][3] * inv);
+        }
     }
 }
 
@@ -410,18 +494,28 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillParams p, in
     }
 }
 
+template <int HD, int G, bool QF32>
+int launch_prefill_shape(const PrefillParams& p, unsigned grid, hipStream_t s) {
+    const size_t lds = PrefillLds<HD>::TOTAL + sizeof(int) * (static_cast<size_t>(p.B) + 2);
+    auto kern = prefill_mfma_kernel<HD, G, QF32>;
+    static size_t granted = 0;   // largest dynamic LDS size requested so far
+    if (lds > granted) {
+        SKV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        granted = lds;
+    }
+    kern<<<grid, 64 * kPrefillWaves, lds, s>>>(p);
+    return check_launch("prefill_mfma_kernel");
+}
+
 template <bool QF32>
 int launch_prefill_mfma(PrefillParams p, int num_tokens, hipStream_t s) {
     const int G = p.Hq / p.Hkv;
-    p.tile_tokens = 64 / G;
+    p.tile_tokens = kPrefillRows / G;
     const unsigned tiles = static_cast<unsigned>(cdiv(num_tokens, p.tile_tokens) + p.B);
     const unsigned grid = tiles * static_cast<unsigned>(p.Hkv);
-    const size_t lds = sizeof(int) * (static_cast<size_t>(p.B) + 1);
-#define SKV_PF(HD_, G_)                                                        \
-    if (p.HD == HD_ && G == G_) {                                              \
-        prefill_mfma_kernel<HD_, G_, QF32><<<grid, 256, lds, s>>>(p);          \
-        return check_launch("prefill_mfma_kernel");                            \
-    }
+#define SKV_PF(HD_, G_) \
+    if (p.HD == HD_ && G == G_) return launch_prefill_shape<HD_, G_, QF32>(p, grid, s);
     SKV_PF(64, 1) SKV_PF(64, 2) SKV_PF(64, 4) SKV_PF(64, 8) SKV_PF(64, 16)
     SKV_PF(128, 1) SKV_PF(128, 2) SKV_PF(128, 4) SKV_PF(128, 8) SKV_PF(128, 16)
 #undef SKV_PF
