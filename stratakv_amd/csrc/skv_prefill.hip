@@ -226,21 +226,34 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
             if constexpr (QF32) qop[QP - 1][c][cc] = __builtin_bit_cast(bf16x8_t, lo);
         }
 
+    // Block ids of a step's four 16-key blocks (-1: absent or outside the
+    // pool), read two steps ahead with uniform (scalar) loads so the K/V
+    // loads of a step never wait on a table read.
+    auto step_blocks = [&](int k0, int (&blk)[KS / 16]) {
+#pragma unroll
+        for (int hb = 0; hb < KS / 16; ++hb) {
+            const int kb = k0 + 16 * hb;
+            int pb = -1;
+            if (kb < keys_end) {
+                const int64_t e = table[kb >> 4];
+                if (e >= 0 && e < p.total_blocks) pb = static_cast<int>(e);
+            }
+            blk[hb] = pb;
+        }
+    };
     // Loader mapping: thread -> (key row lr, chunk lc) for each of LOADS
     // passes; CH consecutive threads read one row slice.  `valid` (the same in
     // every thread) has bit k set when key k0 + k exists: below keys_end and in
     // a block whose table entry is inside the pool.
-    auto load_step = [&](int k0, u32x4_t (&kr)[LOADS], u32x4_t (&vr)[LOADS], uint64_t& valid) {
+    auto load_step = [&](int k0, const int (&blk)[KS / 16], u32x4_t (&kr)[LOADS], u32x4_t (&vr)[LOADS],
+                         uint64_t& valid) {
         valid = 0;
 #pragma unroll
         for (int hb = 0; hb < KS / 16; ++hb) {
             const int kb = k0 + 16 * hb;
-            if (kb < keys_end) {
-                const int64_t pb = table[kb >> 4];
-                if (pb >= 0 && pb < p.total_blocks) {
-                    const int cnt = min(16, keys_end - kb);
-                    valid |= static_cast<uint64_t>(cnt == 16 ? 0xFFFFu : ((1u << cnt) - 1u)) << (16 * hb);
-                }
+            if (blk[hb] >= 0) {
+                const int cnt = min(16, keys_end - kb);
+                valid |= static_cast<uint64_t>(cnt == 16 ? 0xFFFFu : ((1u << cnt) - 1u)) << (16 * hb);
             }
         }
 #pragma unroll
@@ -250,9 +263,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
             kr[u] = u32x4_t{0u, 0u, 0u, 0u};
             vr[u] = u32x4_t{0u, 0u, 0u, 0u};
             if ((valid >> lr) & 1u) {
-                const int key = k0 + lr;
-                const int64_t pb = table[key >> 4];
-                const int64_t off = (pb * 16 + (key & 15)) * row_stride + static_cast<int64_t>(kvh) * HD + lc * 8;
+                int pb = blk[0];
+#pragma unroll
+                for (int hb = 1; hb < KS / 16; ++hb) pb = (lr >> 4) == hb ? blk[hb] : pb;
+                const int64_t off = (static_cast<int64_t>(pb) * 16 + (lr & 15)) * row_stride +
+                                    static_cast<int64_t>(kvh) * HD + lc * 8;
                 kr[u] = *reinterpret_cast<const u32x4_t*>(p.k + off);
                 vr[u] = *reinterpret_cast<const u32x4_t*>(p.v + off);
             }
@@ -283,14 +298,19 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
     const int nsteps = cdiv(keys_end, KS);
     u32x4_t kr[LOADS], vr[LOADS];
     uint64_t valid_cur = 0, valid_next = 0;
+    int blk1[KS / 16], blk2[KS / 16];   // block ids of steps st + 1 and st + 2
     if (nsteps > 0) {
-        load_step(0, kr, vr, valid_cur);
+        int blk0[KS / 16];
+        step_blocks(0, blk0);
+        step_blocks(KS, blk1);
+        load_step(0, blk0, kr, vr, valid_cur);
         store_step(0, kr, vr);
     }
     __syncthreads();
     for (int st = 0; st < nsteps; ++st) {
         const int cur = st & 1;
-        if (st + 1 < nsteps) load_step((st + 1) * KS, kr, vr, valid_next);  // in flight during compute
+        if (st + 1 < nsteps) load_step((st + 1) * KS, blk1, kr, vr, valid_next);  // in flight during compute
+        step_blocks((st + 2) * KS, blk2);
         const unsigned char* kb = lds + cur * Lds::BUF;
         const unsigned char* vb = kb + Lds::KB;
         const int k0 = st * KS;
@@ -390,6 +410,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
         if (st + 1 < nsteps) store_step(cur ^ 1, kr, vr);
         __syncthreads();
         valid_cur = valid_next;
+#pragma unroll
+        for (int hb = 0; hb < KS / 16; ++hb) blk1[hb] = blk2[hb];
     }
 
     // ---- output: O[row][dims 16 dt + 4j + i] = acc / l
