@@ -267,7 +267,9 @@ int skv_linear_f32(const float* x, int rows, const void* weight, int weight_dtyp
                    int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
                    const float* bias, float* y, void* stream);
 /* In-place split-half rotary embedding of `heads` contiguous head vectors at
- * `position` (src/layers/attention.cpp:96-135). */
+ * `position` (src/layers/attention.cpp:96-135).  The angles are computed on
+ * the host in double and rounded to float (cos, sin per pair), so head_dim is
+ * at most 512; larger head dimensions give SKV_ERR_INVALID_ARGUMENT. */
 int skv_rope_f32(float* x, int heads, int head_dim, int position, void* stream);
 /* gate[i] = gate[i] * sigmoid(gate[i]) * up[i]. */
 int skv_swiglu_f32(float* gate, const float* up, int n, void* stream);

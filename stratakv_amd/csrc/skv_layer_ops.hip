@@ -98,36 +98,41 @@ constexpr int kGemvMaxLdsK = 8192;     // x staged in LDS up to this many inputs
 
 // Dot products of x (K floats, LDS or global) with two output-major weight
 // rows (byte pointers, 16-byte aligned, K elements each; r1 may repeat r0), by
-// one wavefront: 16 bytes per lane per load, kGemvUnroll loads per row issued
-// together, fp32 accumulation, then a wave reduction.  Every caller computes a
-// row with exactly this arithmetic, so fused and separate projections give
-// the same bits.  The loads of the first kGemvUnroll steps are issued by
-// PairPrefetch before x is needed (callers stage x meanwhile).
-template <bool BF16W>
+// one wavefront: 16 bytes per lane per load, fp32 accumulation, then a wave
+// reduction.  The first min(NU, K / STEP) loads of each row are issued by the
+// constructor, before x is needed (callers stage x meanwhile); the rest follow
+// NU at a time.  Each lane accumulates its elements in increasing k whatever
+// NU is, so every caller computes a row with exactly the same arithmetic and
+// fused and separate projections give the same bits.
+template <bool BF16W, int NU = kGemvUnroll>
 struct PairPrefetch {
     static constexpr int EPL = BF16W ? 8 : 4;    // elements per 16-byte load
     static constexpr int STEP = 64 * EPL;        // elements per wave-wide load
     static constexpr int64_t ESZ = BF16W ? 2 : 4;
     const char* rows[2];
-    uint4 q[2][kGemvUnroll];
-    bool full;                                   // K holds the first kGemvUnroll steps
+    uint4 q[2][NU];
+    int npre;                                    // steps issued by the constructor
 
     __device__ __forceinline__ PairPrefetch(const char* r0, const char* r1, int K, int lane) {
         rows[0] = r0;
         rows[1] = r1;
-        full = kGemvUnroll * STEP <= K;
-        if (full) {
+        npre = min(NU, K / STEP);
+        // Every one of the NU loads is issued (steps past npre repeat step
+        // npre - 1, in bounds, and are never accumulated), so all of them are
+        // in flight together.
+        if (npre > 0) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int u = 0; u < NU; ++u)
 #pragma unroll
-                for (int u = 0; u < kGemvUnroll; ++u)
-                    q[j][u] = *reinterpret_cast<const uint4*>(rows[j] + (u * STEP + lane * EPL) * ESZ);
+                for (int j = 0; j < 2; ++j)
+                    q[j][u] = *reinterpret_cast<const uint4*>(rows[j] + (min(u, npre - 1) * STEP + lane * EPL) * ESZ);
         }
     }
 
-    __device__ __forceinline__ void accumulate(const float* xr, int k0, int lane, float (&acc)[2]) const {
+    __device__ __forceinline__ void accumulate(const float* xr, int k0, int lane, int n, float (&acc)[2]) const {
 #pragma unroll
-        for (int u = 0; u < kGemvUnroll; ++u) {
+        for (int u = 0; u < NU; ++u) {
+            if (u >= n) continue;
             float xv[EPL];
 #pragma unroll
             for (int e = 0; e < EPL; ++e) xv[e] = xr[k0 + u * STEP + lane * EPL + e];
@@ -143,18 +148,15 @@ struct PairPrefetch {
 
     __device__ __forceinline__ void finish(const float* xr, int K, int lane, float& out0, float& out1) {
         float acc[2] = {0.0f, 0.0f};
-        int k0 = 0;
-        if (full) {
-            accumulate(xr, 0, lane, acc);
-            k0 = kGemvUnroll * STEP;
-        }
-        for (; k0 + kGemvUnroll * STEP <= K; k0 += kGemvUnroll * STEP) {
+        accumulate(xr, 0, lane, npre, acc);
+        int k0 = npre * STEP;
+        for (; k0 + NU * STEP <= K; k0 += NU * STEP) {
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int u = 0; u < kGemvUnroll; ++u)
+                for (int u = 0; u < NU; ++u)
                     q[j][u] = *reinterpret_cast<const uint4*>(rows[j] + (k0 + u * STEP + lane * EPL) * ESZ);
-            accumulate(xr, k0, lane, acc);
+            accumulate(xr, k0, lane, NU, acc);
         }
         for (int k = k0 + lane * EPL; k + EPL <= K; k += STEP) {
 #pragma unroll
@@ -283,11 +285,31 @@ __global__ __launch_bounds__(256) void gemv_cols_kernel(const float* __restrict_
 
 // cos and sin of pair `pair` of a head_dim-hd head at `position`: inverse
 // frequency 10000^(-2 pair / hd) rounded to float, angle in double.
-__device__ __forceinline__ void rope_cos_sin(int pair, int hd, int position, float& c, float& s) {
-    const float inv = static_cast<float>(pow(10000.0, -2.0 * pair / static_cast<double>(hd)));
-    const double angle = static_cast<double>(position) * static_cast<double>(inv);
-    c = static_cast<float>(cos(angle));
-    s = static_cast<float>(sin(angle));
+// cos / sin of the rotation of pair `pair` at `position`: the inverse
+// frequency 10000^(-2 pair / hd) in double, rounded to float, the angle in
+// double (src/layers/attention.cpp:96-135).  Computed on the host, with the
+// same double routines as the reference's CPU path, once per (hd, position),
+// and handed to the kernels in their arguments (2 KiB at most): the kernels
+// never evaluate double transcendentals.
+constexpr int kMaxRopePairs = 256;   // head_dim <= 512
+struct RopeTable {
+    float cs[2 * kMaxRopePairs];     // [pair][cos, sin]
+};
+
+const RopeTable& rope_table(int hd, int position) {
+    thread_local RopeTable table;
+    thread_local int cached_hd = -1, cached_pos = -1;
+    if (hd != cached_hd || position != cached_pos) {
+        for (int i = 0; i < hd / 2; ++i) {
+            const float inv = static_cast<float>(std::pow(10000.0, -2.0 * i / static_cast<double>(hd)));
+            const double angle = static_cast<double>(position) * static_cast<double>(inv);
+            table.cs[2 * i] = static_cast<float>(std::cos(angle));
+            table.cs[2 * i + 1] = static_cast<float>(std::sin(angle));
+        }
+        cached_hd = hd;
+        cached_pos = position;
+    }
+    return table;
 }
 
 __device__ __forceinline__ float swiglu_of(float g, float u) {
@@ -295,18 +317,27 @@ __device__ __forceinline__ float swiglu_of(float g, float u) {
     return g * sig * u;
 }
 
+// One rotation, with the rounding spelled out (one product, one fused
+// multiply-add per output) so that every kernel that rotates gives the same
+// bits whatever the compiler would contract.
+__device__ __forceinline__ void rotate_pair(float& a, float& b, float c, float s) {
+    const float a0 = a, b0 = b;
+    a = fmaf(a0, c, -(b0 * s));
+    b = fmaf(a0, s, b0 * c);
+}
+
 __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ x, int heads, int hd,
-                                                   int position) {
+                                                   RopeTable rt) {
     const int half = hd / 2;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= heads * half) return;
     const int h = i / half, pair = i - h * half;
-    float c, s;
-    rope_cos_sin(pair, hd, position, c, s);
+    const float c = rt.cs[2 * pair], s = rt.cs[2 * pair + 1];
     float* p = x + static_cast<int64_t>(h) * hd;
-    const float a = p[pair], b = p[pair + half];
-    p[pair] = a * c - b * s;
-    p[pair + half] = a * s + b * c;
+    float a = p[pair], b = p[pair + half];
+    rotate_pair(a, b, c, s);
+    p[pair] = a;
+    p[pair + half] = b;
 }
 
 __global__ __launch_bounds__(256) void swiglu_kernel(float* __restrict__ gate,
@@ -351,9 +382,10 @@ struct FusedGemv {
     int head_dim;             // QKV
     int position;             // QKV: RoPE position, < 0 = none
     const float* residual;    // RESIDUAL
+    RopeTable rope;           // QKV with position >= 0
 };
 
-template <bool BF16W, int MODE>
+template <bool BF16W, int MODE, int NU, int XU>
 __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
     extern __shared__ float x_s[];  // [K] input (+ [K] gamma while normalising)
     __shared__ float red[4];
@@ -386,25 +418,24 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
         ra = min(2 * item, f.n[0] - 1);
         rb = min(ra + 1, f.n[0] - 1);
     }
-    // Loads in issue order: the first chunk of x (and gamma), then this
-    // wavefront's weights, so storing x to LDS waits only for x (wait counts
-    // are in issue order) while the weights stay in flight.
-    float xv[kChunk], gv[kChunk];
+    // Loads in issue order: all of x (and gamma), XU per thread (K <= 256 XU),
+    // then this wavefront's weights, so storing x to LDS waits only for x
+    // (wait counts are in issue order) while the weights stay in flight.
+    float xv[XU], gv[XU];
     const bool norm = f.gamma != nullptr;
-    load_chunk(f.x, t, K, xv);
-    if (norm) load_chunk(f.gamma, t, K, gv);
-    PairPrefetch<BF16W> pf(row_ptr(ma, ra), row_ptr(mb, rb), K, lane);
 #pragma unroll
-    for (int u = 0; u < kChunk; ++u) {
+    for (int u = 0; u < XU; ++u) xv[u] = f.x[min(t + 256 * u, K - 1)];
+    if (norm)
+#pragma unroll
+        for (int u = 0; u < XU; ++u) gv[u] = f.gamma[min(t + 256 * u, K - 1)];
+    PairPrefetch<BF16W, NU> pf(row_ptr(ma, ra), row_ptr(mb, rb), K, lane);
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
         const int i = t + 256 * u;
         if (i < K) {
             x_s[i] = xv[u];
             if (norm) x_s[K + i] = gv[u];
         }
-    }
-    if (K > 256 * kChunk) {  // the rest of x (and gamma)
-        stage_to_lds(f.x + 256 * kChunk, x_s + 256 * kChunk, K - 256 * kChunk);
-        if (norm) stage_to_lds(f.gamma + 256 * kChunk, x_s + K + 256 * kChunk, K - 256 * kChunk);
     }
     if (norm) {
         __syncthreads();
@@ -422,11 +453,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
             a += bias_of(seg, ra);
             b += bias_of(seg, rb);
             if (rope) {
-                float c, s;
-                rope_cos_sin(p % half, hd, f.position, c, s);
-                const float a0 = a, b0 = b;
-                a = a0 * c - b0 * s;
-                b = a0 * s + b0 * c;
+                rotate_pair(a, b, f.rope.cs[2 * (p % half)], f.rope.cs[2 * (p % half) + 1]);
             }
             f.y[seg][ra] = a;
             f.y[seg][rb] = b;
@@ -452,8 +479,19 @@ template <int MODE>
 int launch_fused(const FusedGemv& f, bool bf16, int items, hipStream_t s) {
     const unsigned grid = static_cast<unsigned>(cdiv(items, 4));
     const size_t lds = sizeof(float) * static_cast<size_t>(f.K) * (f.gamma != nullptr ? 2 : 1);
-    if (bf16) fused_gemv_kernel<true, MODE><<<grid, 256, lds, s>>>(f);
-    else fused_gemv_kernel<false, MODE><<<grid, 256, lds, s>>>(f);
+    // The whole input is preloaded (XU elements per thread) and up to 12
+    // wave-wide steps of each weight row are requested at once.
+    auto go = [&](auto kern) { kern<<<grid, 256, lds, s>>>(f); };
+#define SKV_FUSED(NU_B, NU_F, XU_)                                                  \
+    {                                                                               \
+        if (bf16) go(fused_gemv_kernel<true, MODE, NU_B, XU_>);                     \
+        else go(fused_gemv_kernel<false, MODE, NU_F, XU_>);                         \
+    }
+    if (f.K <= 2048) SKV_FUSED(4, 8, 8)
+    else if (f.K <= 4096) SKV_FUSED(8, 12, 16)
+    else if (f.K <= 6144) SKV_FUSED(12, 12, 24)
+    else SKV_FUSED(12, 12, 32)
+#undef SKV_FUSED
     return check_launch("fused_gemv_kernel");
 }
 
@@ -506,9 +544,11 @@ extern "C" int skv_linear_f32(const float* x, int rows, const void* weight, int 
 extern "C" int skv_rope_f32(float* x, int heads, int head_dim, int position, void* stream) {
     SKV_REQUIRE(x && heads > 0 && head_dim > 0 && head_dim % 2 == 0 && position >= 0,
                 "skv_rope_f32: invalid pointers or sizes");
+    SKV_REQUIRE(head_dim / 2 <= kMaxRopePairs, "skv_rope_f32: head_dim %d exceeds %d", head_dim,
+                2 * kMaxRopePairs);
     const int n = heads * (head_dim / 2);
     rope_kernel<<<cdiv(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(x, heads, head_dim,
-                                                                          position);
+                                                                          rope_table(head_dim, position));
     return check_launch("rope_kernel");
 }
 
@@ -560,6 +600,12 @@ extern "C" int skv_fused_qkv_f32(const float* hidden, const float* gamma, float 
     }
     f.head_dim = head_dim;
     f.position = position;
+    if (position >= 0) {
+        if (head_dim / 2 > kMaxRopePairs)
+            return set_error(SKV_ERR_UNSUPPORTED, "skv_fused_qkv_f32: head_dim %d exceeds %d", head_dim,
+                             2 * kMaxRopePairs);
+        f.rope = rope_table(head_dim, position);
+    }
     return launch_fused<FUSED_QKV>(f, esz == 2, (ns[0] + ns[1] + ns[2]) / 2,
                                    static_cast<hipStream_t>(stream));
 }

@@ -288,6 +288,7 @@ def test_generate_repeatable_and_errors(gpu, ckpt_dir):
     assert res["tokens"] == [3, gen[0]]
 
 
+@pytest.mark.timeout(400)  # writes a 2.2 GB checkpoint first (~30 s on 8 cores)
 def test_generate_tinyllama_matches_reference(gpu, ckpt_dir):
     golden = _golden("tinyllama")
     path = _checkpoint("tinyllama", ckpt_dir, golden)
