@@ -108,6 +108,48 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
+// Pairwise exchange-and-add between lane l and lane l ^ 32 (swap32_sum),
+// l ^ 16 (swap16_sum) or l ^ 8 (swap8_sum) of two values a, b: the lower lane
+// of each pair returns a(lower) + a(upper), the upper lane b(lower) + b(upper).
+// v_permlane32_swap exchanges the upper half of its first operand with the
+// lower half of its second, v_permlane16_swap the odd 16-lane rows of the
+// first with the even rows of the second; the 8-lane exchange is a row
+// rotation by 8 (DPP) written to one half of each row's banks at a time.
+__device__ __forceinline__ float swap32_sum(float a, float b) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float swap16_sum(float a, float b) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float swap8_sum(float a, float b) {
+    constexpr int kRowRor8 = 0x128;
+    const float lo = __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(b), __float_as_int(a), kRowRor8, 0xF, 0x3, false));
+    const float hi = __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(a), __float_as_int(b), kRowRor8, 0xF, 0xC, false));
+    return lo + hi;
+}
+
+// Reduce-scatter of N per-lane values over the lanes that share lane bits
+// 0 .. LO-1 (the groups l, l + 2^LO, ...; LO = 3 or 4): every exchange keeps
+// complementary halves, so afterwards lane l holds, in v[0 .. N/2^(6-LO)), the
+// group sums of values (l >> LO) * N/2^(6-LO) + i.  Each sum is the same
+// pairwise tree for every value: bit 5 pairs first, then bit 4, then bit 3.
+template <int N, int LO>
+__device__ __forceinline__ void reduce_scatter_high_bits(float (&v)[N]) {
+    static_assert((LO == 3 || LO == 4) && N % (1 << (6 - LO)) == 0, "reduce-scatter shape");
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) v[i] = swap32_sum(v[i], v[i + N / 2]);
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) v[i] = swap16_sum(v[i], v[i + N / 4]);
+    if constexpr (LO == 3) {
+#pragma unroll
+        for (int i = 0; i < N / 8; ++i) v[i] = swap8_sum(v[i], v[i + N / 8]);
+    }
+}
+
 __device__ __forceinline__ float shfl_xor_f(float x, int mask) {
     return __shfl_xor(x, mask, 64);
 }

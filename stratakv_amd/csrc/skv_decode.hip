@@ -445,13 +445,18 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
             *reinterpret_cast<u32x4_t*>(p.v_pool_w + new_dst) = vnew;
         }
 
-        // ---- finalise the segment: combine row groups, broadcast (sum, max)
+        // ---- finalise the segment: sum the row groups by a reduce-scatter,
+        // after which lane (r, c) holds NF consecutive (head, element) values
+        // v = NF * r + i (head v / 8, dims 8c + v % 8), exactly what it stores.
+        constexpr int NV = G * 8;
+        constexpr int LO = CH == 8 ? 3 : 4;
+        constexpr int NF = NV >> (6 - LO);
+        float v[NV];
 #pragma unroll
-        for (int off = CH; off < 64; off <<= 1)
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] += shfl_xor_f(acc[g][e], off);
+            for (int e = 0; e < 8; ++e) v[g * 8 + e] = acc[g][e];
+        reduce_scatter_high_bits<NV, LO>(v);
         float ltot = lpart + shfl_xor_f(lpart, 16);
         ltot += shfl_xor_f(ltot, 32);
         if (j == 0) {
@@ -461,27 +466,56 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
         wave_lds_sync();
         const bool final_out = seg_lo >= range_lo && seg_hi <= range_hi;
         const int64_t prow = partial_row(range, seg_lo > range_lo, Hkv, kvh);
-        if (r == 0) {
+        const int v0 = NF * r;
+        if constexpr (NF >= 8) {
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
+            for (int gg = 0; gg < NF / 8; ++gg) {
+                const int g = v0 / 8 + gg;
                 const float lsum = h_s[0][g];
+                const float* x = v + 8 * gg;
+                float4* o;
+                float sc = 1.0f;
                 if (final_out) {
-                    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-                    float4* o = reinterpret_cast<float4*>(
-                        p.out + (static_cast<int64_t>(b) * p.Hq + h0 + g) * HD + 8 * c);
-                    o[0] = make_float4(acc[g][0] * inv, acc[g][1] * inv, acc[g][2] * inv, acc[g][3] * inv);
-                    o[1] = make_float4(acc[g][4] * inv, acc[g][5] * inv, acc[g][6] * inv, acc[g][7] * inv);
+                    sc = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+                    o = reinterpret_cast<float4*>(p.out + (static_cast<int64_t>(b) * p.Hq + h0 + g) * HD + 8 * c);
                 } else {
                     const int64_t row = prow * G + g;
-                    float4* o = reinterpret_cast<float4*>(p.ws_acc + row * HD + 8 * c);
-                    o[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-                    o[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+                    o = reinterpret_cast<float4*>(p.ws_acc + row * HD + 8 * c);
                     if (c == 0) {
                         p.ws_ml[row * 2 + 0] = h_s[1][g];
                         p.ws_ml[row * 2 + 1] = lsum;
                     }
                 }
+                if (final_out) {
+                    o[0] = make_float4(x[0] * sc, x[1] * sc, x[2] * sc, x[3] * sc);
+                    o[1] = make_float4(x[4] * sc, x[5] * sc, x[6] * sc, x[7] * sc);
+                } else {
+                    o[0] = make_float4(x[0], x[1], x[2], x[3]);
+                    o[1] = make_float4(x[4], x[5], x[6], x[7]);
+                }
             }
+        } else {
+            const int g = v0 / 8, e0 = v0 % 8;
+            const float lsum = h_s[0][g];
+            float* o;
+            float sc = 1.0f;
+            if (final_out) {
+                sc = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+                o = p.out + (static_cast<int64_t>(b) * p.Hq + h0 + g) * HD + 8 * c + e0;
+            } else {
+                const int64_t row = prow * G + g;
+                o = p.ws_acc + row * HD + 8 * c + e0;
+                if (c == 0 && e0 == 0) {
+                    p.ws_ml[row * 2 + 0] = h_s[1][g];
+                    p.ws_ml[row * 2 + 1] = lsum;
+                }
+            }
+            float x[NF];
+#pragma unroll
+            for (int i = 0; i < NF; ++i) x[i] = final_out ? v[i] * sc : v[i];
+            if constexpr (NF == 4) *reinterpret_cast<float4*>(o) = make_float4(x[0], x[1], x[2], x[3]);
+            else if constexpr (NF == 2) *reinterpret_cast<float2*>(o) = make_float2(x[0], x[1]);
+            else o[0] = x[0];
         }
         wave_lds_sync();
 
