@@ -184,7 +184,11 @@ __device__ __forceinline__ int64_t partial_row(int range, bool tail, int Hseg, i
 // also its register budget (launch bound).
 constexpr int mfma_waves_per_simd(int HD, int G) { return HD == 64 && G < 16 ? 2 : 1; }
 
-template <int HD, int G, bool QF32, int WPW, int NBUF>
+// SPLIT: short tables (at most WPW * NBUF blocks per sequence).  Workgroup
+// = one (sequence, kv head) segment; its WPW wavefronts take consecutive
+// sub-ranges of at most NBUF blocks, so every K/V load of the segment is in
+// flight at once, and merge their partials through LDS (no merge launch).
+template <int HD, int G, bool QF32, int WPW, int NBUF, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_mfma_kernel(DecodeParams p) {
     constexpr int BS = 16;
     constexpr int CH = HD / 8;      // 16-byte chunks per row
@@ -201,6 +205,8 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
     __shared__ u32x4_t k_all[WPW][BS * CH];  // one block of K for this kv head, swizzled
     __shared__ float p_all[WPW][BS * 16];    // probabilities [token][head]
     __shared__ float h_all[WPW][2][16];      // per-head (sum, max) at the end of a segment
+    __shared__ float part_acc[SPLIT ? WPW : 1][SPLIT ? G * HD : 1];  // SPLIT: per-wave partials
+    __shared__ float part_ml[SPLIT ? WPW : 1][2][16];
 
     const int wv = WPW == 1 ? 0 : __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
@@ -212,21 +218,28 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
     auto swz = [](int row) { return CH == 16 ? row : ((row >> 1) & 7); };
     const int Hkv = p.Hkv;
     const int w = blockIdx.x * WPW + wv;    // Hkv % WPW == 0: one range per workgroup
-    const int kvh = w % Hkv;
+    const int kvh = SPLIT ? static_cast<int>(blockIdx.x % Hkv) : w % Hkv;
     const int range = w / Hkv;
 
     const WorkSplit split = build_split(p, P_s);
-    if (range >= split.used) return;
+    if (!SPLIT && range >= split.used) return;
     const int per = split.per;
     const int64_t row_stride = static_cast<int64_t>(Hkv) * HD;
-    const int range_lo = range * per;
-    const int range_hi = range_lo + per;
+    int range_lo = range * per;
+    int range_hi = range_lo + per;
+    int b = 0;
+    if constexpr (SPLIT) {
+        // Wavefront wv: blocks [wv * NBUF, wv * NBUF + NBUF) of the segment.
+        b = static_cast<int>(blockIdx.x / Hkv);
+        range_lo = std::min(P_s[b] + wv * NBUF, P_s[b + 1]);
+        range_hi = std::min(range_lo + NBUF, P_s[b + 1]);
+    }
     int pos = range_lo;
-    const int end = std::min(range_hi, split.total);
-    int b = find_seq(P_s, p.B, pos);
+    const int end = SPLIT ? range_hi : std::min(range_hi, split.total);
+    if (!SPLIT) b = find_seq(P_s, p.B, pos);
     const int h0 = kvh * G;
 
-    while (true) {
+    while (!SPLIT || pos < end) {
         const int seg_lo = P_s[b], seg_hi = P_s[b + 1];
         const int nb = seg_hi - seg_lo;
         const int k0 = pos - seg_lo;
@@ -464,9 +477,23 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
             h_s[1][t] = m;
         }
         wave_lds_sync();
-        const bool final_out = seg_lo >= range_lo && seg_hi <= range_hi;
+        const bool final_out = !SPLIT && seg_lo >= range_lo && seg_hi <= range_hi;
         const int64_t prow = partial_row(range, seg_lo > range_lo, Hkv, kvh);
         const int v0 = NF * r;
+        // Partial of head g: ws (merge kernel) or, SPLIT, this wave's LDS slot.
+        auto partial_acc = [&](int g) -> float* {
+            if constexpr (SPLIT) return &part_acc[wv][g * HD];
+            return p.ws_acc + (prow * G + g) * HD;
+        };
+        auto partial_ml = [&](int g, float mg, float lg) {
+            if constexpr (SPLIT) {
+                part_ml[wv][0][g] = mg;
+                part_ml[wv][1][g] = lg;
+            } else {
+                p.ws_ml[(prow * G + g) * 2 + 0] = mg;
+                p.ws_ml[(prow * G + g) * 2 + 1] = lg;
+            }
+        };
         if constexpr (NF >= 8) {
 #pragma unroll
             for (int gg = 0; gg < NF / 8; ++gg) {
@@ -479,12 +506,8 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
                     sc = lsum > 0.0f ? 1.0f / lsum : 0.0f;
                     o = reinterpret_cast<float4*>(p.out + (static_cast<int64_t>(b) * p.Hq + h0 + g) * HD + 8 * c);
                 } else {
-                    const int64_t row = prow * G + g;
-                    o = reinterpret_cast<float4*>(p.ws_acc + row * HD + 8 * c);
-                    if (c == 0) {
-                        p.ws_ml[row * 2 + 0] = h_s[1][g];
-                        p.ws_ml[row * 2 + 1] = lsum;
-                    }
+                    o = reinterpret_cast<float4*>(partial_acc(g) + 8 * c);
+                    if (c == 0) partial_ml(g, h_s[1][g], lsum);
                 }
                 if (final_out) {
                     o[0] = make_float4(x[0] * sc, x[1] * sc, x[2] * sc, x[3] * sc);
@@ -503,12 +526,8 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
                 sc = lsum > 0.0f ? 1.0f / lsum : 0.0f;
                 o = p.out + (static_cast<int64_t>(b) * p.Hq + h0 + g) * HD + 8 * c + e0;
             } else {
-                const int64_t row = prow * G + g;
-                o = p.ws_acc + row * HD + 8 * c + e0;
-                if (c == 0 && e0 == 0) {
-                    p.ws_ml[row * 2 + 0] = h_s[1][g];
-                    p.ws_ml[row * 2 + 1] = lsum;
-                }
+                o = partial_acc(g) + 8 * c + e0;
+                if (c == 0 && e0 == 0) partial_ml(g, h_s[1][g], lsum);
             }
             float x[NF];
 #pragma unroll
@@ -520,10 +539,33 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
         wave_lds_sync();
 
         pos = stop;
-        if (pos >= end) break;
+        if (SPLIT || pos >= end) break;
         do {
             ++b;
         } while (P_s[b + 1] == P_s[b]);
+    }
+
+    if constexpr (SPLIT) {
+        // Merge the WPW sub-range partials of the segment (wavefronts past the
+        // segment's last sub-range hold none):
+        //   out = sum_w acc_w 2^(m_w - M) / sum_w l_w 2^(m_w - M),  M = max_w m_w.
+        const int nw = std::min(WPW, cdiv(P_s[b + 1] - P_s[b], NBUF));
+        __syncthreads();
+        float* out0 = p.out + (static_cast<int64_t>(b) * p.Hq + h0) * HD;
+        for (int col = threadIdx.x; col < G * HD; col += 64 * WPW) {
+            const int g = col / HD;
+            float M = -INFINITY;
+            for (int u = 0; u < nw; ++u) M = fmaxf(M, part_ml[u][0][g]);
+            float L = 0.0f, A = 0.0f;
+            if (M != -INFINITY) {
+                for (int u = 0; u < nw; ++u) {
+                    const float wgt = fast_exp2(part_ml[u][0][g] - M);
+                    L = fmaf(wgt, part_ml[u][1][g], L);
+                    A = fmaf(wgt, part_acc[u][col], A);
+                }
+            }
+            if (nw > 0) out0[col] = L > 0.0f ? A / L : 0.0f;
+        }
     }
 }
 
@@ -909,6 +951,14 @@ int launch_mfma_shape(const DecodeParams& p, hipStream_t s) {
     constexpr int NB = HD == 64 ? 3 : 2;
     constexpr int PER_SIMD = mfma_waves_per_simd(HD, G);
     const char* name = "decode_mfma_kernel";
+    if (p.max_blocks <= 4 * NB) {
+        // Short tables (cfg1-like decoding): one workgroup per (sequence, kv
+        // head), its 4 wavefronts splitting the blocks, merged in LDS.
+        const size_t lds = sizeof(int) * (static_cast<size_t>(p.B) + 1);
+        const unsigned groups = static_cast<unsigned>(p.B) * static_cast<unsigned>(p.Hkv);
+        decode_mfma_kernel<HD, G, QF32, 4, NB, true><<<groups, 256, lds, s>>>(p);
+        return check_launch(name);
+    }
     if (p.Hkv % 4 == 0) return launch_pair(decode_mfma_kernel<HD, G, QF32, 4, NB>, 4, PER_SIMD, p, s, name);
     if (p.Hkv % 2 == 0) return launch_pair(decode_mfma_kernel<HD, G, QF32, 2, NB>, 2, PER_SIMD, p, s, name);
     return launch_pair(decode_mfma_kernel<HD, G, QF32, 1, NB>, 1, PER_SIMD, p, s, name);

@@ -119,6 +119,25 @@ def test_group_sharing_identical_queries(gpu):
     assert np.array_equal(got, np.broadcast_to(got[:, :, :1, :], got.shape))
 
 
+@pytest.mark.parametrize("geom", [TL, L3, L70, (8, 8, 64), (16, 1, 128), (16, 1, 64), (4, 4, 128)],
+                         ids=["tl", "l3", "l70", "mha64", "g16_128", "g16_64", "mha128"])
+@pytest.mark.parametrize("q_dtype", ["bf16", "fp32"])
+def test_short_tables_one_workgroup_per_head(gpu, geom, q_dtype):
+    """Tables of at most 12 (head_dim 64) or 8 (head_dim 128) blocks: one
+    workgroup per (sequence, kv head) whose wavefronts split the blocks and
+    merge in LDS.  Ragged lengths cover 1..4 busy wavefronts, empty sequences
+    and table columns past a sequence."""
+    Hq, Hkv, hd = geom
+    cap = 16 * (12 if hd == 64 else 8)
+    lens = [1, 0, 16, 17, 48, 49, cap - 1, cap, 33, -2, 100 if hd == 64 else 97]
+    case = make_case(len(lens), Hq, Hkv, hd, 16, lens, layout="random", q_dtype=q_dtype, seed=hd + Hkv)
+    assert case["tables"].shape[1] * 16 == cap
+    got = gpu_decode(gpu, case)
+    assert np.all(got[1] == 0) and np.all(got[9] == 0)
+    ref = oracle_decode(dict(case, tables=np.where(case["tables"] < 0, -1, case["tables"])))
+    assert_close(got, ref, what=f"short tables geom={geom} q={q_dtype}")
+
+
 def test_long_context_split_merge(gpu):
     """One 32k-token sequence: many partitions merged with the log-sum-exp rule."""
     Hq, Hkv, hd = L3

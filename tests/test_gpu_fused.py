@@ -124,6 +124,19 @@ def test_fused_skipped_positions(gpu, q_dtype):
     _check(gpu, c, f"skips q={q_dtype}", no_oracle=(3, 6))
 
 
+@pytest.mark.parametrize("geom", [(32, 4, 64), (32, 8, 128)], ids=["tl", "l3"])
+def test_fused_short_tables(gpu, geom):
+    """Short tables (one workgroup per kv head, blocks split over its
+    wavefronts): the new row lands in whichever wavefront holds the last
+    block; skipped positions as in the separate append."""
+    Hq, Hkv, hd = geom
+    cap_blocks = 12 if hd == 64 else 8
+    lens = [1, 16, 17, 33, 48, 49, 16 * cap_blocks, 0, 40, 16 * cap_blocks + 5]
+    c = _case(Hq, Hkv, hd, 16, lens, "fp32", "fp32", seed=hd + 1, bad_last=(8,), max_blocks=cap_blocks)
+    # Sequence 9 needs one more block than the table has: its position is past the table.
+    _check(gpu, c, f"short tables {geom}", no_oracle=(8, 9))
+
+
 def test_fused_generic_path_and_misaligned_rows(gpu):
     """Shapes outside the MFMA kernel, and new rows not 16-byte aligned, take the
     append kernel before the decode; the result is the same contract."""
