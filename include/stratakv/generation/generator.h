@@ -94,6 +94,11 @@ private:
     // One decode step: embedding of ids_[in_index], all layers, final norm,
     // lm_head into `logits` (device [vocab]).
     void step(int in_index, float* logits);
+    // The prompt ids_[0 .. P): all P embeddings, every layer over the P rows
+    // at once (TransformerBlock::prefill_into), then the logits of the last row.
+    void prompt_pass(std::size_t P, float* logits);
+    // Final norm + lm_head of one hidden row into `logits`.
+    void logits_of(const float* x, float* logits);
     void raise_flags(std::int32_t flags) const;
 
     GeneratorConfig config_;
@@ -107,6 +112,7 @@ private:
     std::optional<layers::Linear> lm_head_;  // [hidden, vocab] view of BF16 [vocab, hidden] rows
     std::optional<Tensor> hidden_;           // [1, hidden] FP32: embedding, then the layer stream
     std::optional<Tensor> normed_;           // [1, hidden] FP32
+    std::optional<Tensor> prompt_rows_;      // [P, hidden] FP32 of the last prompt length
     std::optional<Tensor> logits_;           // [1, vocab] FP32
     std::int32_t* ids_ = nullptr;            // device token ids, capacity ids_capacity_
     std::size_t ids_capacity_ = 0;

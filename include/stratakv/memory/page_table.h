@@ -71,6 +71,8 @@ private:
     int staged_seq_id_ = 0;
     std::size_t staged_block_count_ = 0;
     bool device_table_dirty_ = true;
+    void* upload_event_ = nullptr;   // recorded after the last upload out of the mirror
+    void* upload_stream_ = nullptr;  // the stream of that upload
 };
 
 class DeviceBatch {

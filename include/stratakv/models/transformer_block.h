@@ -50,6 +50,18 @@ public:
     // the reference's CPU path, not provided by this build (throws).
     Tensor forward(const Tensor& hidden_states, int seq_id, memory::PageTable& page_table,
                    memory::BlockPool& block_pool, bool append_tokens = true);
+    // Runs the layer over hidden_states.shape()[0] new tokens of seq_id (a
+    // prompt, or a chunk of one), GPU only: appends their K/V at the next
+    // positions and attends causally over the whole context
+    // (skv_paged_prefill); output may alias hidden_states.  The reference's
+    // GPU forward_into takes one token (src/models/transformer_block.cpp:
+    // 348-351); its CPU forward computes these rows (:300-332).  Projection
+    // rows have the bits forward_into gives for each token; the attention of
+    // the chunk runs the prefill kernel instead of the decode kernel.
+    void prefill_into(const Tensor& hidden_states, Tensor& output, int seq_id,
+                      memory::PageTable& page_table, memory::BlockPool& block_pool);
+    // Tokens per prefill_into pass (longer inputs run in chunks of this many).
+    static constexpr int kPrefillChunk = 256;
     void forward_into(const Tensor& hidden_states, Tensor& output, int seq_id,
                       memory::PageTable& page_table, memory::BlockPool& block_pool,
                       bool append_tokens = true);
@@ -99,6 +111,13 @@ private:
     std::optional<Tensor> up_workspace_;
     std::optional<Tensor> down_workspace_;
     std::optional<Tensor> decode_workspace_;  // skv_paged_attention_decode scratch
+    // prefill_into scratch, [rows][dim] for up to prefill_rows_ tokens
+    // (allocated on first use, grown to kPrefillChunk at most).
+    void ensure_prefill_workspace(int rows);
+    int prefill_rows_ = 0;
+    std::optional<Tensor> pf_queries_, pf_keys_, pf_values_, pf_context_, pf_residual_, pf_act_;
+    std::optional<Tensor> pf_normalized_, pf_up_, pf_down_;
+    std::optional<Tensor> pf_meta_;  // 4 int32: position, chunk offsets {0, n}, context length
 };
 
 }  // namespace models

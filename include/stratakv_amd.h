@@ -98,6 +98,9 @@ int skv_memcpy_d2h_async(void* dst, const void* src, size_t bytes, void* stream)
 /* dst[pairs[2i]] = pairs[2i+1] for i < n: applies a batch of (index, value)
  * updates to a device int32 array (incremental block-table upload). */
 int skv_scatter_i32(int32_t* dst, const int32_t* pairs, int n, void* stream);
+/* dst[i] = values[i] for i < n (n <= 16), ordered on `stream`; the values are
+ * copied into the launch, so `values` (host memory) may be reused on return. */
+int skv_write_i32(int32_t* dst, const int32_t* values, int n, void* stream);
 
 /* ---- synthetic data ------------------------------------------------------ */
 /* dst[i] = bf16_rne(N(0,1) sample derived from (seed, first_index + i)) via a
@@ -273,6 +276,12 @@ int skv_linear_f32(const float* x, int rows, const void* weight, int weight_dtyp
 int skv_rope_f32(float* x, int heads, int head_dim, int position, void* stream);
 /* gate[i] = gate[i] * sigmoid(gate[i]) * up[i]. */
 int skv_swiglu_f32(float* gate, const float* up, int n, void* stream);
+/* skv_rope_f32 over `rows` rows of `heads` head vectors, row r at position
+ * first_position + r; cos/sin of each angle computed on the device in double
+ * from the same float inverse frequencies and rounded to float
+ * (src/layers/attention.cpp:96-135 per token). */
+int skv_rope_rows_f32(float* x, int rows, int heads, int head_dim, int first_position,
+                      void* stream);
 /* target[i] += source[i]. */
 int skv_add_f32(float* target, const float* source, int n, void* stream);
 
@@ -310,6 +319,36 @@ int skv_linear_residual_f32(const float* x, const void* weight, int weight_dtype
                             int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
                             const float* bias, const float* residual, float* y,
                             void* stream);
+
+/* The same three projections for `rows` consecutive tokens of one sequence
+ * (prompt prefill): hidden / x / residual / q / k / v / act / y are row-major
+ * [rows][dim].  Every row's outputs have the bits the one-token entry point
+ * gives for that row alone (token r of skv_fused_qkv_rows_f32 rotated at
+ * first_position + r); each weight row is read from HBM once for all rows.
+ * With gamma, `normalized` is caller scratch of rows * in_dim floats (the
+ * normalised inputs are written there; distinct from every other buffer).
+ * SKV_ERR_UNSUPPORTED (nothing launched) unless the weights are aligned
+ * output-major rows with in_dim a multiple of 512 and <= 6,144 (bf16) or of
+ * 256 and <= 2,048 (fp32).
+ * Replaces: the multi-token rows of the reference's CPU
+ * TransformerBlock::forward (src/models/transformer_block.cpp:300-332), whose
+ * GPU forward_into takes one token (:348-351). */
+int skv_fused_qkv_rows_f32(const float* hidden, int rows, const float* gamma, float epsilon,
+                           const void* wq, const void* wk, const void* wv, int weight_dtype,
+                           int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
+                           const float* bias_k, const float* bias_v, int hidden_dim,
+                           int num_heads, int num_kv_heads, int head_dim, int first_position,
+                           float* q, float* k, float* v, float* normalized, void* stream);
+int skv_fused_gate_up_swiglu_rows_f32(const float* x, int rows, const float* gamma, float epsilon,
+                                      const void* w_gate, const void* w_up, int weight_dtype,
+                                      int64_t stride_k, int64_t stride_n_gate,
+                                      int64_t stride_n_up, const float* bias_gate,
+                                      const float* bias_up, int in_dim, int out_dim,
+                                      float* act, float* normalized, void* stream);
+int skv_linear_residual_rows_f32(const float* x, int rows, const void* weight, int weight_dtype,
+                                 int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
+                                 const float* bias, const float* residual, float* y,
+                                 void* stream);
 
 /* ---- model boundary: checkpoint tensors, embedding, token choice --------
  * Checkpoint decode on the device (the host only moves file bytes).  src holds

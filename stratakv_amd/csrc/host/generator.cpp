@@ -276,7 +276,28 @@ void Generator::step(int in_index, float* logits) {
                   "Generator: embedding");
     for (std::size_t l = 0; l < blocks_.size(); ++l)
         blocks_[l].forward_into(*hidden_, *hidden_, 0, pages_[l], pools_[l], true);
-    if (logits == nullptr) return;
+    if (logits != nullptr) logits_of(x, logits);
+}
+
+void Generator::prompt_pass(std::size_t P, float* logits) {
+    const int dtype = embeddings_->dtype() == DataType::BF16 ? SKV_DTYPE_BF16 : SKV_DTYPE_FP32;
+    const int h = static_cast<int>(config_.hidden_dim);
+    const int vocab = static_cast<int>(config_.vocab_size);
+    if (!prompt_rows_ || prompt_rows_->shape()[0] != P)
+        prompt_rows_.emplace(std::vector<std::size_t>{P, config_.hidden_dim}, DataType::FP32, Device::GPU);
+    auto* rows = static_cast<float*>(prompt_rows_->raw_data());
+    for (std::size_t i = 0; i < P; ++i)
+        detail::check(skv_embedding_f32(embeddings_->raw_data(), dtype, vocab, h, ids_, static_cast<int>(i),
+                                        rows + i * config_.hidden_dim, flags_, stream_),
+                      "Generator: embedding");
+    for (std::size_t l = 0; l < blocks_.size(); ++l)
+        blocks_[l].prefill_into(*prompt_rows_, *prompt_rows_, 0, pages_[l], pools_[l]);
+    logits_of(rows + (P - 1) * config_.hidden_dim, logits);
+}
+
+void Generator::logits_of(const float* x, float* logits) {
+    const int h = static_cast<int>(config_.hidden_dim);
+    const int vocab = static_cast<int>(config_.vocab_size);
     detail::check(skv_rmsnorm_f32(x, static_cast<float*>(normed_->raw_data()),
                                   static_cast<const float*>(final_norm_->gamma().raw_data()), 1, h,
                                   final_norm_->epsilon(), stream_),
@@ -319,8 +340,8 @@ std::vector<int> Generator::generate(const std::vector<int>& prompt, int max_new
         detail::check(skv_memset_d8(flags_, 0, sizeof(std::int32_t), stream_), "Generator: flags");
         auto* logits = static_cast<float*>(logits_->raw_data());
         const int vocab = static_cast<int>(config_.vocab_size);
-        for (std::size_t i = 0; i + 1 < P; ++i) step(static_cast<int>(i), nullptr);
-        step(static_cast<int>(P - 1), logits);
+        if (P >= 2) prompt_pass(P, logits);
+        else step(0, logits);
 
         const int R = static_cast<int>(step_events_.size());
         int checked = 0;      // generated tokens the host has read
@@ -383,8 +404,9 @@ std::vector<float> Generator::forced_logits(const std::vector<int>& tokens, std:
         for (std::size_t i = 0; i < N; ++i) host_ids_[i] = tokens[i];
         detail::check(skv_memcpy_h2d_async(ids_, host_ids_, N * sizeof(std::int32_t), stream_), "Generator: tokens");
         detail::check(skv_memset_d8(flags_, 0, sizeof(std::int32_t), stream_), "Generator: flags");
-        for (std::size_t i = 0; i + 1 < n_prompt; ++i) step(static_cast<int>(i), nullptr);
-        for (std::size_t r = 0; r < rows; ++r) step(static_cast<int>(n_prompt - 1 + r), base + r * vocab);
+        if (n_prompt >= 2) prompt_pass(n_prompt, base);
+        else step(0, base);
+        for (std::size_t r = 1; r < rows; ++r) step(static_cast<int>(n_prompt - 1 + r), base + r * vocab);
         detail::check(skv_stream_synchronize(stream_), "Generator: forced_logits");
         detail::check(skv_memcpy_d2h(out.data(), base, out.size() * sizeof(float), stream_), "Generator: logits");
         std::int32_t flags = 0;

@@ -40,7 +40,9 @@ PageTable::PageTable(PageTable&& other) noexcept
       d_block_table_capacity_(std::exchange(other.d_block_table_capacity_, 0)),
       staged_seq_id_(other.staged_seq_id_),
       staged_block_count_(std::exchange(other.staged_block_count_, 0)),
-      device_table_dirty_(std::exchange(other.device_table_dirty_, true)) {}
+      device_table_dirty_(std::exchange(other.device_table_dirty_, true)),
+      upload_event_(std::exchange(other.upload_event_, nullptr)),
+      upload_stream_(std::exchange(other.upload_stream_, nullptr)) {}
 
 PageTable& PageTable::operator=(PageTable&& other) noexcept {
     if (this != &other) {
@@ -52,6 +54,8 @@ PageTable& PageTable::operator=(PageTable&& other) noexcept {
         staged_seq_id_ = other.staged_seq_id_;
         staged_block_count_ = std::exchange(other.staged_block_count_, 0);
         device_table_dirty_ = std::exchange(other.device_table_dirty_, true);
+        upload_event_ = std::exchange(other.upload_event_, nullptr);
+        upload_stream_ = std::exchange(other.upload_stream_, nullptr);
     }
     return *this;
 }
@@ -63,8 +67,11 @@ void PageTable::release_device_block_table() noexcept {
     if (d_block_table_ != nullptr || h_block_table_ != nullptr) (void)skv_device_synchronize();
     if (d_block_table_ != nullptr) (void)skv_free(d_block_table_);
     if (h_block_table_ != nullptr) (void)skv_host_free(h_block_table_);
+    if (upload_event_ != nullptr) (void)skv_event_destroy(upload_event_);
     d_block_table_ = nullptr;
     h_block_table_ = nullptr;
+    upload_event_ = nullptr;
+    upload_stream_ = nullptr;
     d_block_table_capacity_ = 0;
     staged_block_count_ = 0;
     device_table_dirty_ = true;
@@ -122,15 +129,24 @@ const int* PageTable::get_device_block_table(int seq_id, void* stream) {
     std::size_t first = 0;
     if (!device_table_dirty_ && staged_seq_id_ == seq_id && staged_block_count_ <= required)
         first = staged_block_count_;
-    else if (staged_block_count_ > 0)
+    else if (staged_block_count_ > 0) {
         // A full rewrite of the mirror: earlier copies out of it must be done.
-        detail::check(skv_device_synchronize(), "PageTable: block table upload");
+        // They are when the last one (on the same stream) is.
+        if (upload_event_ != nullptr && upload_stream_ == stream)
+            detail::check(skv_event_synchronize(upload_event_), "PageTable: block table upload");
+        else
+            detail::check(skv_device_synchronize(), "PageTable: block table upload");
+    }
     if (first < required) {
         std::copy(state.physical_blocks.begin() + static_cast<std::ptrdiff_t>(first),
                   state.physical_blocks.end(), h_block_table_ + first);
         detail::check(skv_memcpy_h2d_async(d_block_table_ + first, h_block_table_ + first,
                                            (required - first) * sizeof(int), stream),
                       "PageTable: block table upload");
+        if (upload_event_ == nullptr)
+            detail::check(skv_event_create(&upload_event_), "PageTable: block table upload");
+        detail::check(skv_event_record(upload_event_, stream), "PageTable: block table upload");
+        upload_stream_ = stream;
     }
     staged_seq_id_ = seq_id;
     staged_block_count_ = required;

@@ -7,7 +7,9 @@
 // output-major rows, else as the separate kernels of skv_layer_ops.hip.
 #include "stratakv/models/transformer_block.h"
 
+#include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -255,6 +257,181 @@ void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output,
         detail::check(skv_add_f32(fp(down), cfp(context), hidden, s), "forward_into: residual");
         detail::check(skv_memcpy_d2d(output.raw_data(), down.raw_data(), hidden_dim_ * sizeof(float), s),
                       "forward_into: output copy");
+    }
+}
+
+void TransformerBlock::ensure_prefill_workspace(int rows) {
+    if (rows <= prefill_rows_) return;
+    const std::size_t r = static_cast<std::size_t>(rows);
+    const std::size_t q_dim = attention_.num_heads() * attention_.head_dim();
+    const std::size_t kv_dim = attention_.num_kv_heads() * attention_.head_dim();
+    const std::size_t inter = gate_proj_.output_dim();
+    auto make = [&](std::optional<Tensor>& t, std::size_t dim) {
+        t.emplace(std::vector<std::size_t>{r, dim}, DataType::FP32, Device::GPU);
+    };
+    make(pf_queries_, q_dim);
+    make(pf_keys_, kv_dim);
+    make(pf_values_, kv_dim);
+    make(pf_context_, q_dim);
+    make(pf_residual_, hidden_dim_);
+    make(pf_act_, inter);
+    make(pf_normalized_, hidden_dim_);
+    make(pf_up_, inter);
+    make(pf_down_, hidden_dim_);
+    if (!pf_meta_) pf_meta_.emplace(std::vector<std::size_t>{4}, DataType::FP32, Device::GPU);
+    prefill_rows_ = rows;
+}
+
+void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output, int seq_id,
+                                    memory::PageTable& page_table, memory::BlockPool& block_pool) {
+    if (hidden_states.ndim() != 2 || hidden_states.shape()[1] != hidden_dim_ || hidden_states.shape()[0] == 0 ||
+        output.device() != hidden_states.device() || output.shape() != hidden_states.shape() ||
+        output.dtype() != DataType::FP32 || hidden_states.dtype() != DataType::FP32)
+        throw std::invalid_argument("TransformerBlock::prefill_into: output shape, dtype or device mismatch");
+    if (output.device() != Device::GPU)
+        throw std::runtime_error("TransformerBlock::prefill_into: GPU tensors required");
+    if (norm1_.gamma().dtype() != DataType::FP32 || norm2_.gamma().dtype() != DataType::FP32 ||
+        norm1_.gamma().device() != Device::GPU || norm2_.gamma().device() != Device::GPU)
+        throw std::runtime_error("TransformerBlock::prefill_into: RMSNorm weights are not on GPU");
+    if (attention_.query_projection().weight().device() != Device::GPU ||
+        attention_.key_projection().weight().device() != Device::GPU ||
+        attention_.value_projection().weight().device() != Device::GPU ||
+        attention_.output_projection().weight().device() != Device::GPU ||
+        gate_proj_.weight().device() != Device::GPU || up_proj_.weight().device() != Device::GPU ||
+        down_proj_.weight().device() != Device::GPU)
+        throw std::runtime_error("TransformerBlock::prefill_into: projection weights are not on GPU");
+    if (block_pool.device() != Device::GPU || block_pool.key_cache() == nullptr ||
+        block_pool.value_cache() == nullptr ||
+        block_pool.num_kv_heads() != static_cast<int>(attention_.num_kv_heads()) ||
+        block_pool.head_dim() != static_cast<int>(attention_.head_dim()))
+        throw std::invalid_argument(
+            "TransformerBlock::prefill_into: GPU BlockPool configuration does not match attention");
+    if (!page_table.has_sequence(seq_id))
+        throw std::runtime_error("TransformerBlock::prefill_into: seq_id is not registered");
+
+    const int tokens = static_cast<int>(hidden_states.shape()[0]);
+    const int block_size = block_pool.block_size();
+    const int head_dim = static_cast<int>(attention_.head_dim());
+    const int num_heads = static_cast<int>(attention_.num_heads());
+    const int num_kv_heads = static_cast<int>(attention_.num_kv_heads());
+    const int hidden = static_cast<int>(hidden_dim_);
+    const int inter = static_cast<int>(gate_proj_.output_dim());
+    const int q_dim = num_heads * head_dim;
+    ensure_prefill_workspace(std::min(tokens, kPrefillChunk));
+    void* s = stream_;
+
+    auto fp = [](Tensor& t) { return static_cast<float*>(t.raw_data()); };
+    auto cfp = [](const Tensor& t) { return static_cast<const float*>(t.raw_data()); };
+    auto wdtype = [](const layers::Linear& l) {
+        return l.weight().dtype() == DataType::BF16 ? SKV_DTYPE_BF16 : SKV_DTYPE_FP32;
+    };
+    auto stride_k = [](const layers::Linear& l) { return static_cast<int64_t>(l.weight().strides()[0]); };
+    auto stride_n = [](const layers::Linear& l) { return static_cast<int64_t>(l.weight().strides()[1]); };
+    auto bias_of = [&](const layers::Linear& l) { return l.bias() ? cfp(*l.bias()) : nullptr; };
+    auto fused = [](int rc, const char* what) {
+        if (rc == SKV_ERR_UNSUPPORTED) return false;
+        detail::check(rc, what);
+        return true;
+    };
+    auto linear = [&](const layers::Linear& layer, const float* x, int rows, float* y, const char* what) {
+        detail::check(skv_linear_f32(x, rows, layer.weight().raw_data(), wdtype(layer), stride_k(layer),
+                                     stride_n(layer), static_cast<int>(layer.input_dim()),
+                                     static_cast<int>(layer.output_dim()), bias_of(layer), y, s),
+                      what);
+    };
+    const layers::Linear& wq = attention_.query_projection();
+    const layers::Linear& wk = attention_.key_projection();
+    const layers::Linear& wv = attention_.value_projection();
+    const layers::Linear& wo = attention_.output_projection();
+    const bool same_dtype = wdtype(wq) == wdtype(wk) && wdtype(wq) == wdtype(wv) &&
+                            stride_k(wq) == stride_k(wk) && stride_k(wq) == stride_k(wv);
+    const bool ffn_same = wdtype(gate_proj_) == wdtype(up_proj_) && stride_k(gate_proj_) == stride_k(up_proj_);
+    const int64_t qkv_strides[3] = {stride_n(wq), stride_n(wk), stride_n(wv)};
+    float* q = fp(*pf_queries_);
+    float* k = fp(*pf_keys_);
+    float* v = fp(*pf_values_);
+    float* ctx = fp(*pf_context_);
+    float* h = fp(*pf_residual_);
+    float* act = fp(*pf_act_);
+    auto* meta = static_cast<std::int32_t*>(pf_meta_->raw_data());
+
+    for (int c0 = 0; c0 < tokens; c0 += kPrefillChunk) {
+        const int n = std::min(kPrefillChunk, tokens - c0);
+        const float* x = cfp(hidden_states) + static_cast<std::size_t>(c0) * hidden;
+        float* y = fp(output) + static_cast<std::size_t>(c0) * hidden;
+        const int p0 = page_table.get_state(seq_id).sequence_length;
+        for (int i = 0; i < n; ++i) page_table.append_token(seq_id, block_pool);
+        const memory::SequenceState& state = page_table.get_state(seq_id);
+        const int nblocks = static_cast<int>(state.physical_blocks.size());
+        const std::int32_t meta_h[4] = {p0, 0, n, p0 + n};
+        detail::check(skv_write_i32(meta, meta_h, 4, s), "prefill_into: chunk metadata");
+
+        // Input RMSNorm, q/k/v projections and RoPE at p0 + row.
+        if (!(same_dtype &&
+              fused(skv_fused_qkv_rows_f32(x, n, cfp(norm1_.gamma()), norm1_.epsilon(), wq.weight().raw_data(),
+                                           wk.weight().raw_data(), wv.weight().raw_data(), wdtype(wq),
+                                           stride_k(wq), qkv_strides, bias_of(wq), bias_of(wk), bias_of(wv),
+                                           hidden, num_heads, num_kv_heads, head_dim, p0, q, k, v,
+                                           fp(*pf_normalized_), s),
+                    "prefill_into: fused rmsnorm + q/k/v + rope"))) {
+            float* xn = fp(*pf_normalized_);
+            detail::check(skv_rmsnorm_f32(x, xn, cfp(norm1_.gamma()), n, hidden, norm1_.epsilon(), s),
+                          "prefill_into: input rmsnorm");
+            linear(wq, xn, n, q, "prefill_into: q_proj");
+            linear(wk, xn, n, k, "prefill_into: k_proj");
+            linear(wv, xn, n, v, "prefill_into: v_proj");
+            detail::check(skv_rope_rows_f32(q, n, num_heads, head_dim, p0, s), "prefill_into: rope q");
+            detail::check(skv_rope_rows_f32(k, n, num_kv_heads, head_dim, p0, s), "prefill_into: rope k");
+        }
+
+        // The chunk's K/V rows into the pools (fp32 rounded to bf16 like the
+        // decode path), then causal attention over the whole context.
+        const int* table = page_table.get_device_block_table(seq_id, s);
+        detail::check(skv_kv_append(k, v, SKV_DTYPE_FP32, block_pool.key_cache(), block_pool.value_cache(),
+                                    block_pool.total_blocks(), table, nblocks, meta, nullptr, 1, n, num_kv_heads,
+                                    head_dim, block_size, s),
+                      "prefill_into: KV append");
+        detail::check(skv_paged_prefill(q, SKV_DTYPE_FP32, block_pool.key_cache(), block_pool.value_cache(),
+                                        block_pool.total_blocks(), table, nblocks, meta + 1, meta + 3, 1, n,
+                                        num_heads, num_kv_heads, head_dim, block_size,
+                                        1.0f / std::sqrt(static_cast<float>(head_dim)), ctx, s),
+                      "prefill_into: paged prefill attention");
+
+        // o_proj + residual (reads x before y is written: aliasing-safe).
+        if (!fused(skv_linear_residual_rows_f32(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
+                                                stride_n(wo), q_dim, hidden, bias_of(wo), x, h, s),
+                   "prefill_into: fused o_proj + residual")) {
+            linear(wo, ctx, n, h, "prefill_into: o_proj");
+            detail::check(skv_add_f32(h, x, n * hidden, s), "prefill_into: residual");
+        }
+        // Post-attention RMSNorm, gate/up and SwiGLU.
+        if (!(ffn_same &&
+              fused(skv_fused_gate_up_swiglu_rows_f32(h, n, cfp(norm2_.gamma()), norm2_.epsilon(),
+                                                      gate_proj_.weight().raw_data(), up_proj_.weight().raw_data(),
+                                                      wdtype(gate_proj_), stride_k(gate_proj_),
+                                                      stride_n(gate_proj_), stride_n(up_proj_),
+                                                      bias_of(gate_proj_), bias_of(up_proj_), hidden, inter, act,
+                                                      fp(*pf_normalized_), s),
+                    "prefill_into: fused rmsnorm + gate/up + swiglu"))) {
+            float* hn = fp(*pf_normalized_);
+            float* up = fp(*pf_up_);
+            detail::check(skv_rmsnorm_f32(h, hn, cfp(norm2_.gamma()), n, hidden, norm2_.epsilon(), s),
+                          "prefill_into: post-attention rmsnorm");
+            linear(gate_proj_, hn, n, act, "prefill_into: gate_proj");
+            linear(up_proj_, hn, n, up, "prefill_into: up_proj");
+            detail::check(skv_swiglu_f32(act, up, n * inter, s), "prefill_into: swiglu");
+        }
+        // down_proj + residual into the output rows.
+        if (!fused(skv_linear_residual_rows_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
+                                                stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
+                                                bias_of(down_proj_), h, y, s),
+                   "prefill_into: fused down_proj + residual")) {
+            float* d = fp(*pf_down_);
+            linear(down_proj_, act, n, d, "prefill_into: down_proj");
+            detail::check(skv_add_f32(h, d, n * hidden, s), "prefill_into: residual");
+            detail::check(skv_memcpy_d2d(y, h, static_cast<std::size_t>(n) * hidden * sizeof(float), s),
+                          "prefill_into: output copy");
+        }
     }
 }
 

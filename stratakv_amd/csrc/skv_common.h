@@ -154,6 +154,24 @@ __device__ __forceinline__ float shfl_xor_f(float x, int mask) {
     return __shfl_xor(x, mask, 64);
 }
 
+// wave_sum of N values at once, scattered: afterwards lane l holds, in
+// v[0 .. N/8), the wave sums of values (l >> 3) * N/8 + i (all 8 lanes of the
+// group the same).  Each sum pairs and orders its additions exactly as
+// wave_sum does (lane bit 5 first, then 4, 3, 2, 1, 0, adding the two lanes'
+// partial sums at each step), so it has wave_sum's bits.
+template <int N>
+__device__ __forceinline__ void wave_sum_scatter(float (&v)[N]) {
+    reduce_scatter_high_bits<N, 3>(v);
+#pragma unroll
+    for (int i = 0; i < N / 8; ++i) {
+        float x = v[i];
+        x += __shfl_xor(x, 4, 64);
+        x += dpp_mov<DPP_QUAD_2301>(x);
+        x += dpp_mov<DPP_QUAD_1032>(x);
+        v[i] = x;
+    }
+}
+
 __device__ __forceinline__ float wave_max(float x) {
     for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
     return x;

@@ -146,6 +146,15 @@ struct PairPrefetch {
         }
     }
 
+    // Rows held whole by the constructor (K == npre * STEP): the dot products
+    // with another input, with finish()'s arithmetic; the registers are kept.
+    __device__ __forceinline__ void dot_resident(const float* xr, int lane, float& out0, float& out1) const {
+        float acc[2] = {0.0f, 0.0f};
+        accumulate(xr, 0, lane, npre, acc);
+        out0 = wave_sum(acc[0]);
+        out1 = wave_sum(acc[1]);
+    }
+
     __device__ __forceinline__ void finish(const float* xr, int K, int lane, float& out0, float& out1) {
         float acc[2] = {0.0f, 0.0f};
         accumulate(xr, 0, lane, npre, acc);
@@ -312,6 +321,28 @@ const RopeTable& rope_table(int hd, int position) {
     return table;
 }
 
+// Inverse frequencies 10000^(-2i/hd) rounded to float, as the reference's
+// rope_inv_freq_ (and rope_table above) hold them.
+const RopeTable& rope_inv_freq(int hd) {
+    thread_local RopeTable table;
+    thread_local int cached_hd = -1;
+    if (hd != cached_hd) {
+        for (int i = 0; i < hd / 2; ++i)
+            table.cs[i] = static_cast<float>(std::pow(10000.0, -2.0 * i / static_cast<double>(hd)));
+        cached_hd = hd;
+    }
+    return table;
+}
+
+// cos and sin of position * inv (angle in double, rounded to float): the
+// values rope_table computes on the host, for kernels that rotate several
+// positions.
+__device__ __forceinline__ void rope_cos_sin(int position, float inv, float& c, float& s) {
+    const double angle = static_cast<double>(position) * static_cast<double>(inv);
+    c = static_cast<float>(cos(angle));
+    s = static_cast<float>(sin(angle));
+}
+
 __device__ __forceinline__ float swiglu_of(float g, float u) {
     const float sig = g >= 0.0f ? 1.0f / (1.0f + expf(-g)) : expf(g) / (1.0f + expf(g));
     return g * sig * u;
@@ -334,6 +365,24 @@ __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ x, int he
     const int h = i / half, pair = i - h * half;
     const float c = rt.cs[2 * pair], s = rt.cs[2 * pair + 1];
     float* p = x + static_cast<int64_t>(h) * hd;
+    float a = p[pair], b = p[pair + half];
+    rotate_pair(a, b, c, s);
+    p[pair] = a;
+    p[pair + half] = b;
+}
+
+// Rows of `heads` head vectors, row r at position first + r (prompt prefill).
+__global__ __launch_bounds__(256) void rope_rows_kernel(float* __restrict__ x, int rows, int heads, int hd,
+                                                        int first, RopeTable inv) {
+    const int half = hd / 2;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(rows) * heads * half) return;
+    const int r = static_cast<int>(i / (heads * half));
+    const int rem = static_cast<int>(i - static_cast<int64_t>(r) * heads * half);
+    const int h = rem / half, pair = rem - h * half;
+    float c, s;
+    rope_cos_sin(first + r, inv.cs[pair], c, s);
+    float* p = x + (static_cast<int64_t>(r) * heads + h) * hd;
     float a = p[pair], b = p[pair + half];
     rotate_pair(a, b, c, s);
     p[pair] = a;
@@ -382,8 +431,46 @@ struct FusedGemv {
     int head_dim;             // QKV
     int position;             // QKV: RoPE position, < 0 = none
     const float* residual;    // RESIDUAL
-    RopeTable rope;           // QKV with position >= 0
+    RopeTable rope;           // QKV with position >= 0: cos/sin of `position` (one token),
+                              // or the inverse frequencies (fused_gemv_rows_kernel)
+    int rows;                 // tokens (fused_gemv_rows_kernel; x, y, residual row-major)
 };
+
+// The two rows of work item `item` (one wavefront): matrix ma row ra and
+// matrix mb row rb; an item past the end computes a valid row (live = false)
+// and stores nothing.  QKV with RoPE pairs rows (i, i + hd/2) of one head.
+struct FusedRowPair {
+    int ma, mb, ra, rb, seg, p;
+    bool live, rope;
+};
+
+template <int MODE>
+__device__ __forceinline__ FusedRowPair fused_row_pair(const FusedGemv& f, int item) {
+    FusedRowPair r{0, 0, 0, 0, 0, item, true, false};
+    if constexpr (MODE == FUSED_QKV) {
+        while (r.seg < 3 && r.p >= f.n[r.seg] / 2) r.p -= f.n[r.seg] / 2, ++r.seg;
+        r.live = r.seg < 3;
+        if (!r.live) r.seg = 2, r.p = f.n[2] / 2 - 1;
+        const int hd = f.head_dim, half = hd / 2;
+        r.rope = r.seg < 2 && f.position >= 0;
+        r.ma = r.mb = r.seg;
+        r.ra = r.rope ? (r.p / half) * hd + r.p % half : 2 * r.p;
+        r.rb = r.rope ? r.ra + half : 2 * r.p + 1;
+    } else if constexpr (MODE == FUSED_GATE_UP) {
+        r.live = item < f.n[0];
+        r.ra = r.rb = min(item, f.n[0] - 1);
+        r.mb = 1;
+    } else {
+        r.live = 2 * item < f.n[0];
+        r.ra = min(2 * item, f.n[0] - 1);
+        r.rb = min(r.ra + 1, f.n[0] - 1);
+    }
+    return r;
+}
+
+__device__ __forceinline__ const char* fused_row_ptr(const FusedGemv& f, int m, int r) {
+    return static_cast<const char*>(f.w[m]) + static_cast<int64_t>(r) * f.row_bytes[m];
+}
 
 template <bool BF16W, int MODE, int NU, int XU>
 __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
@@ -391,33 +478,10 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
     __shared__ float red[4];
     const int t = threadIdx.x, lane = t & 63;
     const int K = f.K;
-    const int item = blockIdx.x * 4 + (t >> 6);
-    auto row_ptr = [&](int m, int r) {
-        return static_cast<const char*>(f.w[m]) + static_cast<int64_t>(r) * f.row_bytes[m];
-    };
     auto bias_of = [&](int m, int r) { return f.bias[m] != nullptr ? f.bias[m][r] : 0.0f; };
-    // This wavefront's two rows (matrix ma row ra, matrix mb row rb); a wave
-    // past the end computes a valid row and stores nothing.
-    int ma = 0, mb = 0, ra = 0, rb = 0, seg = 0, p = item;
-    bool live = true, rope = false;
-    if constexpr (MODE == FUSED_QKV) {
-        while (seg < 3 && p >= f.n[seg] / 2) p -= f.n[seg] / 2, ++seg;
-        live = seg < 3;
-        if (!live) seg = 2, p = f.n[2] / 2 - 1;
-        const int hd = f.head_dim, half = hd / 2;
-        rope = seg < 2 && f.position >= 0;
-        ma = mb = seg;
-        ra = rope ? (p / half) * hd + p % half : 2 * p;
-        rb = rope ? ra + half : 2 * p + 1;
-    } else if constexpr (MODE == FUSED_GATE_UP) {
-        live = item < f.n[0];
-        ra = rb = min(item, f.n[0] - 1);
-        mb = 1;
-    } else {
-        live = 2 * item < f.n[0];
-        ra = min(2 * item, f.n[0] - 1);
-        rb = min(ra + 1, f.n[0] - 1);
-    }
+    const FusedRowPair rp = fused_row_pair<MODE>(f, blockIdx.x * 4 + (t >> 6));
+    const int ma = rp.ma, mb = rp.mb, ra = rp.ra, rb = rp.rb, seg = rp.seg, p = rp.p;
+    const bool live = rp.live, rope = rp.rope;
     // Loads in issue order: all of x (and gamma), XU per thread (K <= 256 XU),
     // then this wavefront's weights, so storing x to LDS waits only for x
     // (wait counts are in issue order) while the weights stay in flight.
@@ -428,7 +492,7 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
     if (norm)
 #pragma unroll
         for (int u = 0; u < XU; ++u) gv[u] = f.gamma[min(t + 256 * u, K - 1)];
-    PairPrefetch<BF16W, NU> pf(row_ptr(ma, ra), row_ptr(mb, rb), K, lane);
+    PairPrefetch<BF16W, NU> pf(fused_row_ptr(f, ma, ra), fused_row_ptr(f, mb, rb), K, lane);
 #pragma unroll
     for (int u = 0; u < XU; ++u) {
         const int i = t + 256 * u;
@@ -468,6 +532,127 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
     }
 }
 
+// Fused projections of `rows` tokens (prompt prefill), inputs already
+// normalised (rmsnorm_kernel on the host side of the call).  Each wavefront
+// keeps its two weight rows whole in registers (K = steps * STEP, steps <=
+// NU; the host checks), so the weights are read from HBM once for all
+// tokens.  Tokens go in tiles of 16: for each wave-wide step of k the
+// workgroup stages that step of the 16 inputs in LDS (two buffers, the next
+// step loaded while this one is computed, one barrier per step) and every
+// wavefront accumulates 16 x 2 dot products.  The per-token accumulation
+// order is PairPrefetch's and the final reduction wave_sum's, so each token's
+// outputs have the bits fused_gemv_kernel gives for that token alone; RoPE
+// rotates token m at position + m with rope_cos_sin (the host table's values).
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kRowsTile = 16;
+
+template <bool BF16W, int MODE, int NU, int WPG>
+__global__ __launch_bounds__(64 * WPG) void fused_gemv_rows_kernel(FusedGemv f) {
+    using PF = PairPrefetch<BF16W, NU>;
+    constexpr int STEP = PF::STEP, EPL = PF::EPL, T = kRowsTile;
+    constexpr int Q4 = STEP / 4;                  // float4 per staged input row
+    constexpr int LPT = T * Q4 / (64 * WPG);      // float4 staged per thread per step
+    static_assert(LPT * 64 * WPG == T * Q4, "step staging");
+    extern __shared__ f32x4_t xs4[];              // [2][T][Q4]
+    const int t = threadIdx.x, lane = t & 63;
+    const int K = f.K, steps = K / STEP, rows = f.rows;
+    const int ntiles = cdiv(rows, T);
+    auto bias_of = [&](int m, int r) { return f.bias[m] != nullptr ? f.bias[m][r] : 0.0f; };
+    const FusedRowPair rp = fused_row_pair<MODE>(f, blockIdx.x * WPG + (t >> 6));
+    f32x4_t st[LPT];
+    auto load_step = [&](int tile, int c) __attribute__((always_inline)) {  // rows past the end repeat the last row
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) {
+            const int idx = t + i * 64 * WPG, m = idx / Q4;
+            const int64_t row = min(tile * T + m, rows - 1);
+            st[i] = reinterpret_cast<const f32x4_t*>(f.x + row * K + c * STEP)[idx - m * Q4];
+        }
+    };
+    // Issue order: the first input step, then the weights; the empty asm
+    // reads every weight register here, so the compiler keeps the whole rows
+    // resident instead of sinking the loads to their uses (one wait for all).
+    load_step(0, 0);
+    const PF pf(fused_row_ptr(f, rp.ma, rp.ra), fused_row_ptr(f, rp.mb, rp.rb), K, lane);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+            asm volatile("" ::"v"(pf.q[j][u].x), "v"(pf.q[j][u].y), "v"(pf.q[j][u].z), "v"(pf.q[j][u].w));
+    int g = 0;
+    for (int tile = 0; tile < ntiles; ++tile) {
+        float acc[T][2];
+#pragma unroll
+        for (int m = 0; m < T; ++m) acc[m][0] = acc[m][1] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NU; ++c) {
+            if (c >= steps) continue;  // (not break: the loop must unroll, pf.q[.][c] stays in registers)
+            f32x4_t* buf = xs4 + (g & 1) * T * Q4;
+#pragma unroll
+            for (int i = 0; i < LPT; ++i) buf[t + i * 64 * WPG] = st[i];
+            __syncthreads();
+            // Next step (the next tile's first after the last; past the end,
+            // this tile's last again: every load is issued unconditionally).
+            int nt = tile, nc = c + 1;
+            if (nc == steps) nt = tile + 1, nc = 0;
+            if (nt == ntiles) nt = ntiles - 1, nc = steps - 1;
+            load_step(nt, nc);
+            float w[2][EPL];
+            widen16<BF16W>(pf.q[0][c], w[0]);
+            widen16<BF16W>(pf.q[1][c], w[1]);
+#pragma unroll
+            for (int m = 0; m < T; ++m) {
+                float xv[EPL];
+#pragma unroll
+                for (int q = 0; q < EPL / 4; ++q) {
+                    const f32x4_t x4 = buf[m * Q4 + lane * (EPL / 4) + q];
+                    xv[4 * q + 0] = x4[0];
+                    xv[4 * q + 1] = x4[1];
+                    xv[4 * q + 2] = x4[2];
+                    xv[4 * q + 3] = x4[3];
+                }
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) acc[m][j] = fmaf(xv[e], w[j][e], acc[m][j]);
+            }
+            ++g;
+        }
+        // Lane (r, .) = (lane >> 3, .) ends with tokens 2r and 2r + 1.
+        float v[2 * T];
+#pragma unroll
+        for (int m = 0; m < T; ++m) {
+            v[2 * m] = acc[m][0];
+            v[2 * m + 1] = acc[m][1];
+        }
+        wave_sum_scatter<2 * T>(v);
+        if (!rp.live || (lane & 7) != 0) continue;
+        auto emit = [&](int m, float a, float b) __attribute__((always_inline)) {
+            if (m >= rows) return;
+            if constexpr (MODE == FUSED_QKV) {
+                a += bias_of(rp.seg, rp.ra);
+                b += bias_of(rp.seg, rp.rb);
+                if (rp.rope) {
+                    float cs, sn;
+                    rope_cos_sin(f.position + m, f.rope.cs[rp.p % (f.head_dim / 2)], cs, sn);
+                    rotate_pair(a, b, cs, sn);
+                }
+                float* y = f.y[rp.seg] + static_cast<int64_t>(m) * f.n[rp.seg];
+                y[rp.ra] = a;
+                y[rp.rb] = b;
+            } else if constexpr (MODE == FUSED_GATE_UP) {
+                f.y[0][static_cast<int64_t>(m) * f.n[0] + rp.ra] =
+                    swiglu_of(a + bias_of(0, rp.ra), b + bias_of(1, rp.ra));
+            } else {
+                const int64_t row = static_cast<int64_t>(m) * f.n[0];
+                f.y[0][row + rp.ra] = (a + bias_of(0, rp.ra)) + f.residual[row + rp.ra];
+                if (rp.rb != rp.ra) f.y[0][row + rp.rb] = (b + bias_of(0, rp.rb)) + f.residual[row + rp.rb];
+            }
+        };
+        emit(tile * T + 2 * (lane >> 3), v[0], v[1]);
+        emit(tile * T + 2 * (lane >> 3) + 1, v[2], v[3]);
+    }
+}
+
 // Common checks of the fused entry points: output-major rows, 16-byte aligned,
 // input staged in LDS.
 bool fused_rows_ok(const void* w, int64_t stride_k, int64_t stride_n, int K, int esz) {
@@ -493,6 +678,39 @@ int launch_fused(const FusedGemv& f, bool bf16, int items, hipStream_t s) {
     else SKV_FUSED(12, 12, 32)
 #undef SKV_FUSED
     return check_launch("fused_gemv_kernel");
+}
+
+bool rows_supported(bool bf16, int K) {
+    return bf16 ? K % 512 == 0 && K <= 6144 : K % 256 == 0 && K <= 2048;
+}
+
+// fused_gemv_rows_kernel needs every weight row whole in registers: K a
+// multiple of the wave-wide step and at most 12 steps (bf16: K <= 6,144,
+// fp32: K <= 2,048).  Otherwise SKV_ERR_UNSUPPORTED (nothing launched).
+// The wide gate/up launch uses 8-wavefront workgroups (each staged input
+// serves 16 rows), the narrower projections 4 (more workgroups).
+template <int MODE>
+int launch_fused_rows(const FusedGemv& f, bool bf16, int items, hipStream_t s) {
+    constexpr int WPG = MODE == FUSED_GATE_UP ? 8 : 4;
+    const unsigned grid = static_cast<unsigned>(cdiv(items, WPG));
+    auto go = [&](auto kern, int step) {
+        const size_t lds = 2 * sizeof(float) * static_cast<size_t>(kRowsTile) * step;
+        const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                    static_cast<int>(lds));
+        if (attr != hipSuccess) return set_error(SKV_ERR_HIP, "fused_gemv_rows_kernel: %s", hipGetErrorString(attr));
+        kern<<<grid, 64 * WPG, lds, s>>>(f);
+        return check_launch("fused_gemv_rows_kernel");
+    };
+    if (bf16 && f.K % 512 == 0) {
+        if (f.K <= 2048) return go(fused_gemv_rows_kernel<true, MODE, 4, WPG>, 512);
+        if (f.K <= 4096) return go(fused_gemv_rows_kernel<true, MODE, 8, WPG>, 512);
+        if (f.K <= 6144) return go(fused_gemv_rows_kernel<true, MODE, 12, WPG>, 512);
+    }
+    if (!bf16 && f.K % 256 == 0 && f.K <= 2048) return go(fused_gemv_rows_kernel<false, MODE, 8, WPG>, 256);
+    return set_error(SKV_ERR_UNSUPPORTED,
+                     "fused projections of several tokens need K a multiple of %d and at most %d", bf16 ? 512 : 256,
+                     bf16 ? 6144 : 2048);
 }
 
 }  // namespace skv
@@ -552,6 +770,18 @@ extern "C" int skv_rope_f32(float* x, int heads, int head_dim, int position, voi
     return check_launch("rope_kernel");
 }
 
+extern "C" int skv_rope_rows_f32(float* x, int rows, int heads, int head_dim, int first_position,
+                                 void* stream) {
+    SKV_REQUIRE(x && rows > 0 && heads > 0 && head_dim > 0 && head_dim % 2 == 0 && first_position >= 0,
+                "skv_rope_rows_f32: invalid pointers or sizes");
+    SKV_REQUIRE(head_dim / 2 <= kMaxRopePairs, "skv_rope_rows_f32: head_dim %d exceeds %d", head_dim,
+                2 * kMaxRopePairs);
+    const int64_t n = static_cast<int64_t>(rows) * heads * (head_dim / 2);
+    rope_rows_kernel<<<static_cast<unsigned>(cdiv<int64_t>(n, 256)), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        x, rows, heads, head_dim, first_position, rope_inv_freq(head_dim));
+    return check_launch("rope_rows_kernel");
+}
+
 extern "C" int skv_swiglu_f32(float* gate, const float* up, int n, void* stream) {
     SKV_REQUIRE(gate && up && n > 0, "skv_swiglu_f32: invalid pointers or sizes");
     swiglu_kernel<<<cdiv(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(gate, up, n);
@@ -564,30 +794,46 @@ extern "C" int skv_add_f32(float* target, const float* source, int n, void* stre
     return check_launch("add_kernel");
 }
 
-extern "C" int skv_fused_qkv_f32(const float* hidden, const float* gamma, float epsilon,
-                                 const void* wq, const void* wk, const void* wv, int weight_dtype,
-                                 int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
-                                 const float* bias_k, const float* bias_v, int hidden_dim,
-                                 int num_heads, int num_kv_heads, int head_dim, int position,
-                                 float* q, float* k, float* v, void* stream) {
-    SKV_REQUIRE(hidden && stride_n && q && k && v && hidden_dim > 0 && num_heads > 0 &&
+namespace {
+
+// Shared by the one-token entry points and their *_rows variants (rows
+// tokens, row-major x / y / residual); `fn` names the entry point in errors.
+// Several tokens with gamma: rmsnorm_kernel writes the normalised rows into
+// `normalized` (the bits the one-token kernels normalise to), which the
+// projections then read.
+int normalize_rows(const char* fn, const float*& x, int rows, const float* gamma, float epsilon, int K,
+                   float* normalized, hipStream_t s) {
+    if (gamma == nullptr) return SKV_OK;
+    SKV_REQUIRE(normalized != nullptr, "%s: normalized scratch required with gamma", fn);
+    rmsnorm_kernel<<<rows, 256, 2 * sizeof(float) * K, s>>>(x, normalized, gamma, K, epsilon);
+    if (int rc = check_launch("rmsnorm_kernel")) return rc;
+    x = normalized;
+    return SKV_OK;
+}
+
+int fused_qkv(const char* fn, const float* hidden, int rows, const float* gamma, float epsilon,
+              const void* wq, const void* wk, const void* wv, int weight_dtype, int64_t stride_k,
+              const int64_t stride_n[3], const float* bias_q, const float* bias_k, const float* bias_v,
+              int hidden_dim, int num_heads, int num_kv_heads, int head_dim, int position, float* q,
+              float* k, float* v, float* normalized, void* stream) {
+    SKV_REQUIRE(hidden && stride_n && q && k && v && rows > 0 && hidden_dim > 0 && num_heads > 0 &&
                     num_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
-                "skv_fused_qkv_f32: invalid pointers or sizes");
+                "%s: invalid pointers or sizes", fn);
     SKV_REQUIRE(weight_dtype == SKV_DTYPE_BF16 || weight_dtype == SKV_DTYPE_FP32,
-                "skv_fused_qkv_f32: unknown weight dtype %d", weight_dtype);
+                "%s: unknown weight dtype %d", fn, weight_dtype);
     const int esz = weight_dtype == SKV_DTYPE_BF16 ? 2 : 4;
     const void* ws[3] = {wq, wk, wv};
     for (int m = 0; m < 3; ++m)
         if (!fused_rows_ok(ws[m], stride_k, stride_n[m], hidden_dim, esz))
             return set_error(SKV_ERR_UNSUPPORTED,
-                             "skv_fused_qkv_f32: weights must be 16-byte aligned output-major rows "
-                             "and hidden_dim <= %d",
+                             "%s: weights must be 16-byte aligned output-major rows and hidden_dim <= %d", fn,
                              kGemvMaxLdsK);
     FusedGemv f{};
     f.x = hidden;
     f.gamma = gamma;
     f.eps = epsilon;
     f.K = hidden_dim;
+    f.rows = rows;
     const int ns[3] = {num_heads * head_dim, num_kv_heads * head_dim, num_kv_heads * head_dim};
     const float* bs[3] = {bias_q, bias_k, bias_v};
     float* ys[3] = {q, k, v};
@@ -600,38 +846,42 @@ extern "C" int skv_fused_qkv_f32(const float* hidden, const float* gamma, float 
     }
     f.head_dim = head_dim;
     f.position = position;
-    if (position >= 0) {
-        if (head_dim / 2 > kMaxRopePairs)
-            return set_error(SKV_ERR_UNSUPPORTED, "skv_fused_qkv_f32: head_dim %d exceeds %d", head_dim,
-                             2 * kMaxRopePairs);
-        f.rope = rope_table(head_dim, position);
+    if (position >= 0 && head_dim / 2 > kMaxRopePairs)
+        return set_error(SKV_ERR_UNSUPPORTED, "%s: head_dim %d exceeds %d", fn, head_dim, 2 * kMaxRopePairs);
+    const int items = (ns[0] + ns[1] + ns[2]) / 2;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (rows == 1) {
+        if (position >= 0) f.rope = rope_table(head_dim, position);
+        return launch_fused<FUSED_QKV>(f, esz == 2, items, s);
     }
-    return launch_fused<FUSED_QKV>(f, esz == 2, (ns[0] + ns[1] + ns[2]) / 2,
-                                   static_cast<hipStream_t>(stream));
+    if (position >= 0) f.rope = rope_inv_freq(head_dim);
+    if (!rows_supported(esz == 2, hidden_dim))
+        return set_error(SKV_ERR_UNSUPPORTED, "%s: hidden_dim %d is not a supported multi-token size", fn,
+                         hidden_dim);
+    if (int rc = normalize_rows(fn, f.x, rows, gamma, epsilon, hidden_dim, normalized, s)) return rc;
+    f.gamma = nullptr;
+    return launch_fused_rows<FUSED_QKV>(f, esz == 2, items, s);
 }
 
-extern "C" int skv_fused_gate_up_swiglu_f32(const float* x, const float* gamma, float epsilon,
-                                            const void* w_gate, const void* w_up, int weight_dtype,
-                                            int64_t stride_k, int64_t stride_n_gate,
-                                            int64_t stride_n_up, const float* bias_gate,
-                                            const float* bias_up, int in_dim, int out_dim,
-                                            float* act, void* stream) {
-    SKV_REQUIRE(x && act && in_dim > 0 && out_dim > 0,
-                "skv_fused_gate_up_swiglu_f32: invalid pointers or sizes");
+int fused_gate_up(const char* fn, const float* x, int rows, const float* gamma, float epsilon,
+                  const void* w_gate, const void* w_up, int weight_dtype, int64_t stride_k,
+                  int64_t stride_n_gate, int64_t stride_n_up, const float* bias_gate, const float* bias_up,
+                  int in_dim, int out_dim, float* act, float* normalized, void* stream) {
+    SKV_REQUIRE(x && act && rows > 0 && in_dim > 0 && out_dim > 0, "%s: invalid pointers or sizes", fn);
     SKV_REQUIRE(weight_dtype == SKV_DTYPE_BF16 || weight_dtype == SKV_DTYPE_FP32,
-                "skv_fused_gate_up_swiglu_f32: unknown weight dtype %d", weight_dtype);
+                "%s: unknown weight dtype %d", fn, weight_dtype);
     const int esz = weight_dtype == SKV_DTYPE_BF16 ? 2 : 4;
     if (!fused_rows_ok(w_gate, stride_k, stride_n_gate, in_dim, esz) ||
         !fused_rows_ok(w_up, stride_k, stride_n_up, in_dim, esz))
         return set_error(SKV_ERR_UNSUPPORTED,
-                         "skv_fused_gate_up_swiglu_f32: weights must be 16-byte aligned "
-                         "output-major rows and in_dim <= %d",
+                         "%s: weights must be 16-byte aligned output-major rows and in_dim <= %d", fn,
                          kGemvMaxLdsK);
     FusedGemv f{};
     f.x = x;
     f.gamma = gamma;
     f.eps = epsilon;
     f.K = in_dim;
+    f.rows = rows;
     f.w[0] = w_gate;
     f.w[1] = w_up;
     f.row_bytes[0] = stride_n_gate * esz;
@@ -640,33 +890,101 @@ extern "C" int skv_fused_gate_up_swiglu_f32(const float* x, const float* gamma, 
     f.bias[1] = bias_up;
     f.n[0] = f.n[1] = out_dim;
     f.y[0] = act;
-    return launch_fused<FUSED_GATE_UP>(f, esz == 2, out_dim, static_cast<hipStream_t>(stream));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (rows == 1) return launch_fused<FUSED_GATE_UP>(f, esz == 2, out_dim, s);
+    if (!rows_supported(esz == 2, in_dim))
+        return set_error(SKV_ERR_UNSUPPORTED, "%s: in_dim %d is not a supported multi-token size", fn, in_dim);
+    if (int rc = normalize_rows(fn, f.x, rows, gamma, epsilon, in_dim, normalized, s)) return rc;
+    f.gamma = nullptr;
+    return launch_fused_rows<FUSED_GATE_UP>(f, esz == 2, out_dim, s);
 }
 
-extern "C" int skv_linear_residual_f32(const float* x, const void* weight, int weight_dtype,
-                                       int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
-                                       const float* bias, const float* residual, float* y,
-                                       void* stream) {
-    SKV_REQUIRE(x && residual && y && in_dim > 0 && out_dim > 0,
-                "skv_linear_residual_f32: invalid pointers or sizes");
+int linear_residual(const char* fn, const float* x, int rows, const void* weight, int weight_dtype,
+                    int64_t stride_k, int64_t stride_n, int in_dim, int out_dim, const float* bias,
+                    const float* residual, float* y, void* stream) {
+    SKV_REQUIRE(x && residual && y && rows > 0 && in_dim > 0 && out_dim > 0, "%s: invalid pointers or sizes",
+                fn);
     SKV_REQUIRE(weight_dtype == SKV_DTYPE_BF16 || weight_dtype == SKV_DTYPE_FP32,
-                "skv_linear_residual_f32: unknown weight dtype %d", weight_dtype);
+                "%s: unknown weight dtype %d", fn, weight_dtype);
     const int esz = weight_dtype == SKV_DTYPE_BF16 ? 2 : 4;
     if (!fused_rows_ok(weight, stride_k, stride_n, in_dim, esz))
         return set_error(SKV_ERR_UNSUPPORTED,
-                         "skv_linear_residual_f32: weights must be 16-byte aligned output-major "
-                         "rows and in_dim <= %d",
+                         "%s: weights must be 16-byte aligned output-major rows and in_dim <= %d", fn,
                          kGemvMaxLdsK);
     FusedGemv f{};
     f.x = x;
     f.gamma = nullptr;
     f.K = in_dim;
+    f.rows = rows;
     f.w[0] = weight;
     f.row_bytes[0] = stride_n * esz;
     f.bias[0] = bias;
     f.n[0] = out_dim;
     f.y[0] = y;
     f.residual = residual;
-    return launch_fused<FUSED_RESIDUAL>(f, esz == 2, cdiv(out_dim, 2),
-                                        static_cast<hipStream_t>(stream));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (rows == 1) return launch_fused<FUSED_RESIDUAL>(f, esz == 2, cdiv(out_dim, 2), s);
+    return launch_fused_rows<FUSED_RESIDUAL>(f, esz == 2, cdiv(out_dim, 2), s);
+}
+
+}  // namespace
+
+extern "C" int skv_fused_qkv_f32(const float* hidden, const float* gamma, float epsilon,
+                                 const void* wq, const void* wk, const void* wv, int weight_dtype,
+                                 int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
+                                 const float* bias_k, const float* bias_v, int hidden_dim,
+                                 int num_heads, int num_kv_heads, int head_dim, int position,
+                                 float* q, float* k, float* v, void* stream) {
+    return fused_qkv("skv_fused_qkv_f32", hidden, 1, gamma, epsilon, wq, wk, wv, weight_dtype, stride_k,
+                     stride_n, bias_q, bias_k, bias_v, hidden_dim, num_heads, num_kv_heads, head_dim, position,
+                     q, k, v, nullptr, stream);
+}
+
+extern "C" int skv_fused_qkv_rows_f32(const float* hidden, int rows, const float* gamma, float epsilon,
+                                      const void* wq, const void* wk, const void* wv, int weight_dtype,
+                                      int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
+                                      const float* bias_k, const float* bias_v, int hidden_dim,
+                                      int num_heads, int num_kv_heads, int head_dim, int first_position,
+                                      float* q, float* k, float* v, float* normalized, void* stream) {
+    return fused_qkv("skv_fused_qkv_rows_f32", hidden, rows, gamma, epsilon, wq, wk, wv, weight_dtype,
+                     stride_k, stride_n, bias_q, bias_k, bias_v, hidden_dim, num_heads, num_kv_heads, head_dim,
+                     first_position, q, k, v, normalized, stream);
+}
+
+extern "C" int skv_fused_gate_up_swiglu_f32(const float* x, const float* gamma, float epsilon,
+                                            const void* w_gate, const void* w_up, int weight_dtype,
+                                            int64_t stride_k, int64_t stride_n_gate,
+                                            int64_t stride_n_up, const float* bias_gate,
+                                            const float* bias_up, int in_dim, int out_dim,
+                                            float* act, void* stream) {
+    return fused_gate_up("skv_fused_gate_up_swiglu_f32", x, 1, gamma, epsilon, w_gate, w_up, weight_dtype,
+                         stride_k, stride_n_gate, stride_n_up, bias_gate, bias_up, in_dim, out_dim, act, nullptr,
+                         stream);
+}
+
+extern "C" int skv_fused_gate_up_swiglu_rows_f32(const float* x, int rows, const float* gamma, float epsilon,
+                                                 const void* w_gate, const void* w_up, int weight_dtype,
+                                                 int64_t stride_k, int64_t stride_n_gate,
+                                                 int64_t stride_n_up, const float* bias_gate,
+                                                 const float* bias_up, int in_dim, int out_dim,
+                                                 float* act, float* normalized, void* stream) {
+    return fused_gate_up("skv_fused_gate_up_swiglu_rows_f32", x, rows, gamma, epsilon, w_gate, w_up,
+                         weight_dtype, stride_k, stride_n_gate, stride_n_up, bias_gate, bias_up, in_dim,
+                         out_dim, act, normalized, stream);
+}
+
+extern "C" int skv_linear_residual_f32(const float* x, const void* weight, int weight_dtype,
+                                       int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
+                                       const float* bias, const float* residual, float* y,
+                                       void* stream) {
+    return linear_residual("skv_linear_residual_f32", x, 1, weight, weight_dtype, stride_k, stride_n, in_dim,
+                           out_dim, bias, residual, y, stream);
+}
+
+extern "C" int skv_linear_residual_rows_f32(const float* x, int rows, const void* weight, int weight_dtype,
+                                            int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
+                                            const float* bias, const float* residual, float* y,
+                                            void* stream) {
+    return linear_residual("skv_linear_residual_rows_f32", x, rows, weight, weight_dtype, stride_k, stride_n,
+                           in_dim, out_dim, bias, residual, y, stream);
 }

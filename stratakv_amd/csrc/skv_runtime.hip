@@ -94,6 +94,17 @@ __global__ void gather_blocks_kernel(const uint16_t* __restrict__ pool, int64_t 
         out[e] = ok ? in[e] : uint16_t(0);
 }
 
+// Up to kWriteI32Max int32 values carried in the kernel arguments (copied at
+// launch, so the caller's host array is free as soon as the call returns).
+constexpr int kWriteI32Max = 16;
+struct SmallI32 {
+    int32_t x[kWriteI32Max];
+};
+
+__global__ void write_i32_kernel(int32_t* __restrict__ dst, SmallI32 v, int n) {
+    if (static_cast<int>(threadIdx.x) < n) dst[threadIdx.x] = v.x[threadIdx.x];
+}
+
 __global__ void scatter_i32_kernel(int32_t* __restrict__ dst, const int32_t* __restrict__ pairs,
                                    int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -264,6 +275,16 @@ int skv_scatter_i32(int32_t* dst, const int32_t* pairs, int n, void* stream) {
     SKV_REQUIRE(dst && pairs && n > 0, "skv_scatter_i32: invalid arguments");
     scatter_i32_kernel<<<cdiv(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(dst, pairs, n);
     return check_launch("scatter_i32_kernel");
+}
+
+int skv_write_i32(int32_t* dst, const int32_t* values, int n, void* stream) {
+    if (n == 0) return SKV_OK;
+    SKV_REQUIRE(dst && values && n > 0 && n <= kWriteI32Max, "skv_write_i32: invalid arguments (n <= %d)",
+                kWriteI32Max);
+    SmallI32 v{};
+    for (int i = 0; i < n; ++i) v.x[i] = values[i];
+    write_i32_kernel<<<1, 64, 0, static_cast<hipStream_t>(stream)>>>(dst, v, n);
+    return check_launch("write_i32_kernel");
 }
 
 int skv_event_elapsed_ms(float* ms, void* start, void* stop) {

@@ -7,7 +7,10 @@
 //    crossing block boundaries: the appended K/V rows must be the bf16
 //    rounding of the reference rows, the attention is the oracle's over the
 //    device pool's own bits, and every layer output must match; plus
-//    append_tokens=false and input/output aliasing.
+//    append_tokens=false and input/output aliasing;
+//  * TransformerBlock::prefill_into (several tokens per call, chunked) against
+//    the same float64 layer with causal attention per token, then decode
+//    steps on the cache it wrote.
 // Exit status 77 when no GPU is visible (the reference's skip convention).
 #include <cmath>
 #include <cstdio>
@@ -145,12 +148,12 @@ void rope(std::vector<double>& x, int heads, int hd, int pos) {
 
 uint16_t bf16_of(double v) { return oracle_f32_to_bf16_rne(static_cast<float>(v)); }
 
-void transformer_block_parity() {
-    const int H = 512, I = 768, Hq = 8, Hkv = 2, hd = H / Hq, bs = 16, total = 12, T = 40;
-    std::mt19937 rng(2024);
+// Fills a block's weights (bf16 checkpoint rows behind a transpose view for
+// the attention projections, fp32 GEMM-ready FFN) and the same values as
+// float64 into `ref`.
+void build_layer(stratakv::models::TransformerBlock& block, HostLayer& ref, std::mt19937& rng) {
+    const int H = ref.H;
     std::normal_distribution<float> nd(0.0f, 1.0f);
-    stratakv::models::TransformerBlock block(H, I, Hq, Hkv, total, bs);
-    HostLayer ref{H, I, Hq, Hkv, hd, {}, {}, {}, {}, {}, {}, {}, {}, {}};
     auto gamma = [&](stratakv::layers::RMSNorm& norm, std::vector<double>& g) {
         g.resize(H);
         for (int i = 0; i < H; ++i) {
@@ -161,8 +164,6 @@ void transformer_block_parity() {
     };
     gamma(block.input_norm(), ref.g1);
     gamma(block.post_attention_norm(), ref.g2);
-    // Attention projections: bf16 checkpoint rows [out][in] behind a
-    // transpose_2d view (the reference's checkpoint layout).
     auto bf16_rows = [&](stratakv::layers::Linear& layer, std::vector<double>& w) {
         const int in = static_cast<int>(layer.input_dim()), out = static_cast<int>(layer.output_dim());
         Tensor rows({static_cast<std::size_t>(out), static_cast<std::size_t>(in)}, DataType::BF16);
@@ -178,7 +179,6 @@ void transformer_block_parity() {
     bf16_rows(block.attention().key_projection(), ref.wk);
     bf16_rows(block.attention().value_projection(), ref.wv);
     bf16_rows(block.attention().output_projection(), ref.wo);
-    // FFN: fp32 GEMM-ready [in][out].
     auto fp32_cols = [&](stratakv::layers::Linear& layer, std::vector<double>& w) {
         const std::size_t n = layer.input_dim() * layer.output_dim();
         w.resize(n);
@@ -191,6 +191,42 @@ void transformer_block_parity() {
     fp32_cols(block.gate_proj(), ref.wg);
     fp32_cols(block.up_proj(), ref.wu);
     fp32_cols(block.down_proj(), ref.wd);
+}
+
+// The float64 layer output of one token at `pos`, attending through `table`
+// over the first `len` positions of the pools as the device holds them.
+std::vector<double> ref_layer_token(const HostLayer& ref, const std::vector<double>& xd, int pos,
+                                    const std::vector<uint16_t>& kp, const std::vector<uint16_t>& vp, int total,
+                                    const std::vector<int32_t>& table, int32_t len, int bs) {
+    const int H = ref.H, I = ref.I, Hq = ref.Hq, Hkv = ref.Hkv, hd = ref.hd;
+    std::vector<double> n1 = rmsnorm(xd, ref.g1);
+    std::vector<double> q = matvec(n1, ref.wq, H, H);
+    rope(q, Hq, hd, pos);
+    std::vector<float> qf(q.begin(), q.end()), ctx(H);
+    check(oracle_paged_decode_f32(qf.data(), kp.data(), vp.data(), total, table.data(),
+                                  static_cast<int>(table.size()), &len, 1, Hq, Hkv, hd, bs,
+                                  1.0f / std::sqrt(static_cast<float>(hd)), ctx.data()) == 0,
+          "oracle attention");
+    std::vector<double> c(ctx.begin(), ctx.end());
+    std::vector<double> o = matvec(c, ref.wo, H, H);
+    std::vector<double> h(H);
+    for (int i = 0; i < H; ++i) h[i] = xd[i] + o[i];
+    std::vector<double> n2 = rmsnorm(h, ref.g2);
+    std::vector<double> g = matvec(n2, ref.wg, H, I), u = matvec(n2, ref.wu, H, I);
+    for (int i = 0; i < I; ++i) g[i] = g[i] / (1.0 + std::exp(-g[i])) * u[i];
+    std::vector<double> d = matvec(g, ref.wd, I, H);
+    std::vector<double> y(H);
+    for (int i = 0; i < H; ++i) y[i] = h[i] + d[i];
+    return y;
+}
+
+void transformer_block_parity() {
+    const int H = 512, I = 768, Hq = 8, Hkv = 2, hd = H / Hq, bs = 16, total = 12, T = 40;
+    std::mt19937 rng(2024);
+    std::normal_distribution<float> nd(0.0f, 1.0f);
+    stratakv::models::TransformerBlock block(H, I, Hq, Hkv, total, bs);
+    HostLayer ref{H, I, Hq, Hkv, hd, {}, {}, {}, {}, {}, {}, {}, {}, {}};
+    build_layer(block, ref, rng);
     block.to(Device::GPU);
 
     BlockPool pool(total, bs, Hkv, hd, Device::GPU);
@@ -294,6 +330,106 @@ void transformer_block_parity() {
     check(threw, "mismatched pool geometry is rejected");
 }
 
+// TransformerBlock::prefill_into: several tokens per call (a 300-token prompt
+// = two internal chunks, then a second 21-token chunk with aliased
+// input/output), then decode steps through forward_into on the cache the
+// prefill wrote.  Every output row against the float64 layer with causal
+// attention over the pools as the device holds them; the prefill's K/V rows
+// against the bf16 rounding of the float64 K/V.
+void prefill_parity() {
+    const int H = 512, I = 768, Hq = 8, Hkv = 2, hd = H / Hq, bs = 16, total = 24;
+    std::mt19937 rng(77);
+    std::normal_distribution<float> nd(0.0f, 1.0f);
+    stratakv::models::TransformerBlock block(H, I, Hq, Hkv, total, bs);
+    HostLayer ref{H, I, Hq, Hkv, hd, {}, {}, {}, {}, {}, {}, {}, {}, {}};
+    build_layer(block, ref, rng);
+    block.to(Device::GPU);
+    BlockPool pool(total, bs, Hkv, hd, Device::GPU);
+    ok_or_die(skv_fill_u16(pool.key_cache(), total * pool.block_elements(), 0xFFFF, nullptr), "poison");
+    ok_or_die(skv_fill_u16(pool.value_cache(), total * pool.block_elements(), 0xFFFF, nullptr), "poison");
+    PageTable pt;
+    pt.allocate_sequence(3, pool);
+    const std::size_t pool_n = total * pool.block_elements();
+    double worst = 0.0, worst_kv = 0.0;
+    std::vector<std::vector<double>> inputs;  // every token's layer input, by position
+
+    // Runs `n` new tokens (prefill_into when prefill, else forward_into per
+    // token) and checks their outputs and appended K/V.
+    auto run = [&](int n, bool prefill, bool alias) {
+        const int p0 = pt.get_state(3).sequence_length;
+        std::vector<float> x(static_cast<std::size_t>(n) * H);
+        for (float& v : x) v = nd(rng);
+        for (int t = 0; t < n; ++t) inputs.emplace_back(x.begin() + t * H, x.begin() + (t + 1) * H);
+        std::vector<float> y;
+        if (prefill) {
+            Tensor xd({static_cast<std::size_t>(n), static_cast<std::size_t>(H)}, DataType::FP32, Device::GPU);
+            Tensor yd({static_cast<std::size_t>(n), static_cast<std::size_t>(H)}, DataType::FP32, Device::GPU);
+            ok_or_die(skv_memcpy_h2d(xd.raw_data(), x.data(), x.size() * sizeof(float), nullptr), "upload");
+            if (alias) block.prefill_into(xd, xd, 3, pt, pool);
+            else block.prefill_into(xd, yd, 3, pt, pool);
+            ok_or_die(skv_device_synchronize(), "sync");
+            y = download<float>(alias ? xd.raw_data() : yd.raw_data(), x.size());
+        } else {
+            Tensor xd({1, static_cast<std::size_t>(H)}, DataType::FP32, Device::GPU);
+            for (int t = 0; t < n; ++t) {
+                ok_or_die(skv_memcpy_h2d(xd.raw_data(), x.data() + t * H, H * sizeof(float), nullptr), "upload");
+                block.forward_into(xd, xd, 3, pt, pool, true);
+                ok_or_die(skv_device_synchronize(), "sync");
+                const std::vector<float> yt = download<float>(xd.raw_data(), H);
+                y.insert(y.end(), yt.begin(), yt.end());
+            }
+        }
+        const auto& st = pt.get_state(3);
+        check(st.sequence_length == p0 + n, "every token appended");
+        const std::vector<uint16_t> kp = download<uint16_t>(pool.key_cache(), pool_n);
+        const std::vector<uint16_t> vp = download<uint16_t>(pool.value_cache(), pool_n);
+        const std::vector<int32_t> table(st.physical_blocks.begin(), st.physical_blocks.end());
+        for (int t = 0; t < n; ++t) {
+            const int pos = p0 + t;
+            const std::vector<double>& xt = inputs[pos];
+            // Appended K/V: the bf16 rounding of the float64 rows (one bf16 ulp of slack).
+            std::vector<double> n1 = rmsnorm(xt, ref.g1);
+            std::vector<double> k = matvec(n1, ref.wk, H, Hkv * hd), v = matvec(n1, ref.wv, H, Hkv * hd);
+            rope(k, Hkv, hd, pos);
+            const std::size_t row = (static_cast<std::size_t>(table[pos / bs]) * bs + pos % bs) * Hkv * hd;
+            for (int e = 0; e < Hkv * hd; ++e) {
+                const double gk = oracle_bf16_to_f32(kp[row + e]), gv = oracle_bf16_to_f32(vp[row + e]);
+                worst_kv = std::max(worst_kv, std::fabs(gk - oracle_bf16_to_f32(bf16_of(k[e]))) / (std::fabs(k[e]) + 1e-3));
+                worst_kv = std::max(worst_kv, std::fabs(gv - oracle_bf16_to_f32(bf16_of(v[e]))) / (std::fabs(v[e]) + 1e-3));
+            }
+            const std::vector<double> want = ref_layer_token(ref, xt, pos, kp, vp, total, table, pos + 1, bs);
+            for (int i = 0; i < H; ++i)
+                worst = std::max(worst, std::fabs(y[static_cast<std::size_t>(t) * H + i] - want[i]) /
+                                            (1e-3 + 1e-3 * std::fabs(want[i])));
+        }
+    };
+    run(300, true, false);   // prompt: 256 + 44 tokens inside prefill_into
+    run(21, true, true);     // a later chunk, input and output aliased
+    run(2, false, false);    // decode on the prefilled cache
+    check(pt.get_state(3).sequence_length == 323, "prefill + decode length");
+    check(worst <= 1.0, "prefill_into matches the float64 layer (worst error / bound = " + std::to_string(worst) + ")");
+    check(worst_kv <= 1.0 / 64, "prefill K/V are the bf16 rounding of the rows (" + std::to_string(worst_kv) + ")");
+    std::printf("prefill_into: worst error/bound %.3g, worst K/V rel diff %.3g\n", worst, worst_kv);
+
+    bool threw = false;
+    try {
+        Tensor xd({2, static_cast<std::size_t>(H)}, DataType::FP32, Device::GPU);
+        Tensor yd({3, static_cast<std::size_t>(H)}, DataType::FP32, Device::GPU);
+        block.prefill_into(xd, yd, 3, pt, pool);
+    } catch (const std::invalid_argument&) {
+        threw = true;
+    }
+    check(threw, "prefill_into rejects mismatched shapes");
+    threw = false;
+    try {
+        Tensor xd({2, static_cast<std::size_t>(H)}, DataType::FP32, Device::GPU);
+        block.prefill_into(xd, xd, 8, pt, pool);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    check(threw, "prefill_into rejects an unknown sequence");
+}
+
 }  // namespace
 
 int main() {
@@ -306,6 +442,7 @@ int main() {
         device_tables();
         pool_copy();
         transformer_block_parity();
+        prefill_parity();
     } catch (const std::exception& e) {
         std::fprintf(stderr, "FAIL: unexpected exception %s\n", e.what());
         return 1;

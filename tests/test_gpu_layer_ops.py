@@ -194,3 +194,124 @@ def test_fused_projections_refuse_unsupported_layouts(gpu):
     assert rc == gpu.SKV_ERR_UNSUPPORTED
     gpu.synchronize()
     assert np.array_equal(y.download(np.float32, (H,)), np.full(H, 7.0, np.float32))
+
+
+def _fused_calls(gpu, lib, dims, W, dW, bp, x_rows, position, rows_api):
+    """Run the three fused projections over x_rows [n][H]: one call with
+    rows_api, else one single-token call per row; returns host arrays."""
+    H, Hq, Hkv, hd, inter = dims
+    D = gpu.DeviceBuffer
+    n = x_rows.shape[0]
+    rng = np.random.default_rng(5)
+    gamma = D.from_numpy((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    ctx = rng.standard_normal((n, Hq * hd)).astype(np.float32)
+    act_in = rng.standard_normal((n, inter)).astype(np.float32)
+    res = rng.standard_normal((n, H)).astype(np.float32)
+    dt = W["dtype"]
+    strides = (ctypes.c_int64 * 3)(H, H, H)
+    out = {k: D(4 * n * m) for k, m in (("q", Hq * hd), ("k", Hkv * hd), ("v", Hkv * hd), ("act", inter),
+                                        ("o", H), ("d", H))}
+    dx, dctx, dact, dres = D.from_numpy(x_rows), D.from_numpy(ctx), D.from_numpy(act_in), D.from_numpy(res)
+    eps = ctypes.c_float(1e-5)
+    if rows_api:
+        scratch = D(4 * n * H)
+        gpu._check(lib.skv_fused_qkv_rows_f32(dx.ptr, n, gamma.ptr, eps, dW["q"].ptr, dW["k"].ptr, dW["v"].ptr,
+                                              dt, 1, strides, bp("q"), bp("k"), bp("v"), H, Hq, Hkv, hd,
+                                              position, out["q"].ptr, out["k"].ptr, out["v"].ptr, scratch.ptr,
+                                              None))
+        gpu._check(lib.skv_fused_gate_up_swiglu_rows_f32(dx.ptr, n, gamma.ptr, eps, dW["g"].ptr, dW["u"].ptr, dt,
+                                                         1, H, H, bp("g"), bp("u"), H, inter, out["act"].ptr,
+                                                         scratch.ptr, None))
+        gpu._check(lib.skv_linear_residual_rows_f32(dctx.ptr, n, dW["o"].ptr, dt, 1, Hq * hd, Hq * hd, H,
+                                                    bp("o"), dres.ptr, out["o"].ptr, None))
+        gpu._check(lib.skv_linear_residual_rows_f32(dact.ptr, n, dW["d"].ptr, dt, 1, inter, inter, H,
+                                                    bp("d"), dres.ptr, out["d"].ptr, None))
+    else:
+        for r in range(n):
+            off = lambda buf, dim: buf.ptr + 4 * r * dim
+            pos = position + r if position >= 0 else -1
+            gpu._check(lib.skv_fused_qkv_f32(off(dx, H), gamma.ptr, eps, dW["q"].ptr, dW["k"].ptr, dW["v"].ptr,
+                                             dt, 1, strides, bp("q"), bp("k"), bp("v"), H, Hq, Hkv, hd, pos,
+                                             off(out["q"], Hq * hd), off(out["k"], Hkv * hd),
+                                             off(out["v"], Hkv * hd), None))
+            gpu._check(lib.skv_fused_gate_up_swiglu_f32(off(dx, H), gamma.ptr, eps, dW["g"].ptr, dW["u"].ptr, dt,
+                                                        1, H, H, bp("g"), bp("u"), H, inter,
+                                                        off(out["act"], inter), None))
+            gpu._check(lib.skv_linear_residual_f32(off(dctx, Hq * hd), dW["o"].ptr, dt, 1, Hq * hd, Hq * hd, H,
+                                                   bp("o"), off(dres, H), off(out["o"], H), None))
+            gpu._check(lib.skv_linear_residual_f32(off(dact, inter), dW["d"].ptr, dt, 1, inter, inter, H,
+                                                   bp("d"), off(dres, H), off(out["d"], H), None))
+    gpu.synchronize()
+    sizes = {"q": Hq * hd, "k": Hkv * hd, "v": Hkv * hd, "act": inter, "o": H, "d": H}
+    return {k: out[k].download(np.uint32, (n, sizes[k])) for k in out}
+
+
+@pytest.mark.parametrize("dims,dtype", [((1024, 16, 4, 64, 2048), "bf16"), ((1024, 16, 4, 64, 2048), "fp32"),
+                                        ((2048, 16, 2, 128, 5632), "bf16"), ((3072, 24, 8, 128, 3584), "bf16")],
+                         ids=["k1024_bf16", "k1024_fp32", "tinyllama_ffn", "k3072"])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_fused_rows_match_one_token_calls(gpu, dims, dtype, with_bias):
+    """skv_*_rows_f32 over n tokens == the one-token entry points on each row,
+    bit for bit (weights read once for all rows; RoPE at first_position + r)."""
+    H, Hq, Hkv, hd, inter = dims
+    rng = np.random.default_rng(H + inter + with_bias)
+    lib, D = gpu.lib(), gpu.DeviceBuffer
+    shapes = (("q", Hq * hd, H), ("k", Hkv * hd, H), ("v", Hkv * hd, H), ("o", H, Hq * hd),
+              ("g", inter, H), ("u", inter, H), ("d", H, inter))
+    if dtype == "bf16":
+        W = {n: _bf16_rows(rng, o, i) for n, o, i in shapes}
+        W["dtype"] = gpu.DTYPE_BF16
+    else:
+        W = {n: (0.03 * rng.standard_normal((o, i))).astype(np.float32) for n, o, i in shapes}
+        W["dtype"] = gpu.DTYPE_FP32
+    dW = {n: D.from_numpy(W[n]) for n, _, _ in shapes}
+    B = {n: (D.from_numpy(rng.standard_normal(o).astype(np.float32)) if with_bias else None) for n, o, _ in shapes}
+    bp = lambda n: B[n].ptr if B[n] is not None else None
+    for n_rows, position in ((2, 0), (5, 1000), (16, 7), (37, 16381), (3, -1)):
+        x = rng.standard_normal((n_rows, H)).astype(np.float32)
+        got = _fused_calls(gpu, lib, dims, W, dW, bp, x, position, rows_api=True)
+        want = _fused_calls(gpu, lib, dims, W, dW, bp, x, position, rows_api=False)
+        for k in got:
+            assert np.array_equal(got[k], want[k]), f"{k}: rows={n_rows} position={position}"
+
+
+def test_fused_rows_refuse_unsupported_shapes(gpu):
+    """in_dim not a multiple of the wave-wide step, or too long to keep the
+    rows in registers: SKV_ERR_UNSUPPORTED and nothing written."""
+    lib, D = gpu.lib(), gpu.DeviceBuffer
+    for K, dt in ((1000, gpu.DTYPE_BF16), (8192, gpu.DTYPE_BF16), (4096, gpu.DTYPE_FP32)):
+        esz = 2 if dt == gpu.DTYPE_BF16 else 4
+        w = D(64 * K * esz)
+        x = D.from_numpy(np.ones((3, K), np.float32))
+        res = D.from_numpy(np.zeros((3, 64), np.float32))
+        y = D.from_numpy(np.full((3, 64), 7.0, np.float32))
+        rc = lib.skv_linear_residual_rows_f32(x.ptr, 3, w.ptr, dt, 1, K, K, 64, None, res.ptr, y.ptr, None)
+        assert rc == gpu.SKV_ERR_UNSUPPORTED, (K, dt)
+    gpu.synchronize()
+    assert np.array_equal(y.download(np.float32, (3, 64)), np.full((3, 64), 7.0, np.float32))
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_rope_rows_cos_sin_equal_host_libm(gpu, hd):
+    """skv_rope_rows_f32 on (1, 0) pairs returns (cos, sin) exactly; over
+    positions 0..32767 they equal the host's libm values rounded to float
+    (the table skv_rope_f32 and the one-token fused projection use)."""
+    import math
+    lib, D = gpu.lib(), gpu.DeviceBuffer
+    half, rows = hd // 2, 32768
+    x = np.zeros((rows, hd), np.float32)
+    x[:, :half] = 1.0
+    dx = D.from_numpy(x)
+    gpu._check(lib.skv_rope_rows_f32(dx.ptr, rows, 1, hd, 0, None))
+    got = dx.download(np.float32, (rows, hd))
+    inv = [float(np.float32(10000.0 ** (-2.0 * i / hd))) for i in range(half)]
+    want_c = np.array([[math.cos(p * f) for f in inv] for p in range(rows)], np.float64).astype(np.float32)
+    want_s = np.array([[math.sin(p * f) for f in inv] for p in range(rows)], np.float64).astype(np.float32)
+    bad_c = np.count_nonzero(got[:, :half].view(np.uint32) != want_c.view(np.uint32))
+    bad_s = np.count_nonzero(got[:, half:].view(np.uint32) != want_s.view(np.uint32))
+    assert bad_c == 0 and bad_s == 0, f"{bad_c} cos and {bad_s} sin values differ from libm"
+    # and the one-position kernel (host table) agrees at a few positions
+    for p in (0, 1, 777, 32767):
+        y = D.from_numpy(x[:1])
+        gpu._check(lib.skv_rope_f32(y.ptr, 1, hd, p, None))
+        assert np.array_equal(y.download(np.uint32, (1, hd))[0], got[p].view(np.uint32))
