@@ -201,6 +201,13 @@ __device__ double block_excl_scan_d(double x, PickShared& sh) {
 // SKV_FLAG_NONFINITE_LOGITS (the reference aborts on one,
 // src/generation/generator.cpp:720-732).
 // ---------------------------------------------------------------------------
+// VEC: logits 16-byte aligned; each thread reads float4s, kArgmaxBatch of
+// them in flight (unconditional, clamped), then a scalar tail.  Every thread
+// scans its own elements in increasing index, so the first index of the
+// maximum wins as in the scalar loop.
+constexpr int kArgmaxBatch = 8;
+
+template <bool VEC>
 __global__ __launch_bounds__(kPickThreads) void argmax_kernel(const float* __restrict__ logits, int n,
                                                              int32_t* __restrict__ ids, int out_index,
                                                              int32_t* __restrict__ flags) {
@@ -208,11 +215,32 @@ __global__ __launch_bounds__(kPickThreads) void argmax_kernel(const float* __res
     float best = -INFINITY;
     int bi = n;                      // "none": loses every comparison
     bool bad = false;
-    for (int i = threadIdx.x; i < n; i += kPickThreads) {
-        const float v = logits[i];
+    auto consider = [&](float v, int i) {
         bad |= !(fabsf(v) <= 3.402823466e38f);
         if (bi == n || v > best) { best = v; bi = i; }
+    };
+    int tail = 0;
+    if constexpr (VEC) {
+        const int n4 = n / 4;
+        const float4* l4 = reinterpret_cast<const float4*>(logits);
+        for (int b0 = threadIdx.x; b0 < n4; b0 += kPickThreads * kArgmaxBatch) {
+            float4 v[kArgmaxBatch];
+#pragma unroll
+            for (int u = 0; u < kArgmaxBatch; ++u) v[u] = l4[min(b0 + u * kPickThreads, n4 - 1)];
+#pragma unroll
+            for (int u = 0; u < kArgmaxBatch; ++u) {
+                const int q = b0 + u * kPickThreads;
+                if (q < n4) {
+                    consider(v[u].x, 4 * q);
+                    consider(v[u].y, 4 * q + 1);
+                    consider(v[u].z, 4 * q + 2);
+                    consider(v[u].w, 4 * q + 3);
+                }
+            }
+        }
+        tail = 4 * n4;
     }
+    for (int i = tail + static_cast<int>(threadIdx.x); i < n; i += kPickThreads) consider(logits[i], i);
     // Reduce (value, index): larger value wins, equal values -> smaller index.
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(best, o, 64);
@@ -566,12 +594,19 @@ extern "C" int skv_embedding_f32(const void* table, int table_dtype, int vocab, 
     return check_launch("skv_embedding_f32");
 }
 
+namespace {
+int launch_argmax(const float* logits, int n, int32_t* ids, int index, int32_t* flags, hipStream_t s) {
+    if (aligned16(logits)) argmax_kernel<true><<<1, kPickThreads, 0, s>>>(logits, n, ids, index, flags);
+    else argmax_kernel<false><<<1, kPickThreads, 0, s>>>(logits, n, ids, index, flags);
+    return check_launch("argmax_kernel");
+}
+}  // namespace
+
 extern "C" int skv_argmax_f32(const float* logits, int n, int32_t* token_ids, int index, int32_t* flags,
                               void* stream) {
     SKV_REQUIRE(logits && token_ids, "skv_argmax_f32: NULL pointer");
     SKV_REQUIRE(n > 0 && index >= 0, "skv_argmax_f32: invalid dimensions");
-    argmax_kernel<<<1, kPickThreads, 0, static_cast<hipStream_t>(stream)>>>(logits, n, token_ids, index, flags);
-    return check_launch("skv_argmax_f32");
+    return launch_argmax(logits, n, token_ids, index, flags, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int skv_sample_f32(const float* logits, int n, float temperature, int top_k, float top_p,
@@ -586,8 +621,7 @@ extern "C" int skv_sample_f32(const float* logits, int n, float temperature, int
     SKV_REQUIRE(uniform >= 0.0 && uniform < 1.0, "skv_sample_f32: uniform must be in [0, 1)");
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (temperature == 0.0f) {
-        argmax_kernel<<<1, kPickThreads, 0, s>>>(logits, n, token_ids, index, flags);
-        return check_launch("skv_sample_f32 (greedy)");
+        return launch_argmax(logits, n, token_ids, index, flags, s);
     }
     SampleArgs a{logits, n, temperature, top_k, top_p, uniform, token_ids, index, flags};
     sample_kernel<<<1, kPickThreads, 0, s>>>(a);

@@ -104,11 +104,19 @@ def test_argmax_first_index(gpu):
     cases[1][[5, 900]] = 1.0
     cases[4][[49999, 40000]] = 2.0
     cases.append(np.array([-0.0, 0.0, -0.0], np.float32))
-    ids = skv.DeviceBuffer(4 * len(cases))
-    for i, x in enumerate(cases):
-        skv.argmax(skv.DeviceBuffer.from_numpy(x), x.size, ids, i)
-    got = ids.download(np.int32, len(cases))
-    assert list(got) == [osamp.argmax_first(x) for x in cases]
+    tail = np.zeros(32003, np.float32)
+    tail[[32001, 32002]] = 5.0       # the maximum only in the elements past the last float4
+    cases.append(tail)
+    ties = np.full(40961, 1.0, np.float32)
+    ties[[3, 4, 4099, 40960]] = 7.0  # ties across float4s, batches and the tail
+    cases.append(ties)
+    want = [osamp.argmax_first(x) for x in cases]
+    for shift in (0, 1):             # 16-byte aligned (vector loads) and not (scalar loop)
+        ids = skv.DeviceBuffer(4 * len(cases))
+        for i, x in enumerate(cases):
+            buf = skv.DeviceBuffer.from_numpy(np.concatenate([np.zeros(shift, np.float32), x]))
+            skv.lib().skv_argmax_f32(buf.ptr + 4 * shift, x.size, ids.ptr, i, None, None)
+        assert list(ids.download(np.int32, len(cases))) == want, f"shift {shift}"
 
 
 def _device_sample(logits_row, temp, k, p, u):
