@@ -89,3 +89,36 @@ def test_fused_decode_append_rejects_invalid_arguments():
     for bad in (dict(context_len=0), dict(key_row=None), dict(kv_dtype=3), dict(num_q_heads=6)):
         with pytest.raises(skv.SkvInvalidArgument):
             skv.paged_attention_decode_append(**dict(single, **bad))
+
+
+def test_multi_token_entry_points_reject_invalid_arguments():
+    """The *_rows_f32 projections, skv_rope_rows_f32 and skv_write_i32 validate
+    before any device work (INVALID_ARGUMENT), and refuse shapes the register
+    tiling does not cover with UNSUPPORTED."""
+    lib = skv.lib()
+    eps = ctypes.c_float(1e-5)
+    strides = (ctypes.c_int64 * 3)(2048, 2048, 2048)
+    qkv = lambda rows, gamma, K, hd, normalized: lib.skv_fused_qkv_rows_f32(
+        FAKE, rows, gamma, eps, FAKE, FAKE, FAKE, skv.DTYPE_BF16, 1, strides, None, None, None, K, 32, 4, hd,
+        0, FAKE, FAKE, FAKE, normalized, None)
+    assert qkv(0, FAKE, 2048, 64, FAKE) == skv.SKV_ERR_INVALID_ARGUMENT        # no rows
+    assert qkv(4, FAKE, 2048, 63, FAKE) == skv.SKV_ERR_INVALID_ARGUMENT        # odd head_dim
+    assert qkv(4, FAKE, 2048, 64, None) == skv.SKV_ERR_INVALID_ARGUMENT        # gamma without scratch
+    assert "scratch" in skv.lib().skv_last_error().decode()
+    assert qkv(4, FAKE, 2000, 64, FAKE) == skv.SKV_ERR_UNSUPPORTED             # K not a multiple of 512
+    gate_up = lambda rows, K: lib.skv_fused_gate_up_swiglu_rows_f32(
+        FAKE, rows, FAKE, eps, FAKE, FAKE, skv.DTYPE_BF16, 1, K, K, None, None, K, 5632, FAKE, FAKE, None)
+    assert gate_up(0, 2048) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert gate_up(3, 8192) == skv.SKV_ERR_UNSUPPORTED                         # rows too long for registers
+    res = lambda rows, dt, K: lib.skv_linear_residual_rows_f32(FAKE, rows, FAKE, dt, 1, K, K, 2048, None, FAKE,
+                                                               FAKE, None)
+    assert res(-1, skv.DTYPE_BF16, 2048) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert res(2, 9, 2048) == skv.SKV_ERR_INVALID_ARGUMENT                     # unknown dtype
+    assert res(2, skv.DTYPE_FP32, 4096) == skv.SKV_ERR_UNSUPPORTED
+    assert lib.skv_rope_rows_f32(FAKE, 3, 4, 63, 0, None) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert lib.skv_rope_rows_f32(FAKE, 3, 4, 1026, 0, None) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert lib.skv_rope_rows_f32(FAKE, 3, 4, 64, -1, None) == skv.SKV_ERR_INVALID_ARGUMENT
+    vals = (ctypes.c_int32 * 17)(*range(17))
+    assert lib.skv_write_i32(FAKE, vals, 17, None) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert lib.skv_write_i32(None, vals, 2, None) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert lib.skv_write_i32(FAKE, vals, 0, None) == skv.SKV_OK             # nothing to write
