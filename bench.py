@@ -628,8 +628,8 @@ def main() -> int:
         return copy_calibration(args.copy_calibration)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}). The paged "
-              f"decode path shards by sequence or KV head with no exchange; the multi-GPU design is "
-              f"described in DESIGN.md but not built or measured.", file=sys.stderr)
+              f"decode path shards by sequence or KV head with no exchange inside attention; that "
+              f"design is not built or measured here.", file=sys.stderr)
         return 2
     if args.prefill:
         if args.config != 5:
