@@ -88,6 +88,7 @@ enum : int {
     DPP_QUAD_2301 = 0x4E,   // quad_perm [2,3,0,1]
     DPP_ROW_MIRROR = 0x140, // lane i <- lane 15-i within a row of 16
     DPP_ROW_HALF_MIRROR = 0x141, // lane i <- lane 7-i within each half-row of 8
+    DPP_ROW_ROR8 = 0x128,   // lane i <- lane i ^ 8 within a row of 16 (rotation by 8)
 };
 
 template <int CTRL>
@@ -172,13 +173,48 @@ __device__ __forceinline__ void wave_sum_scatter(float (&v)[N]) {
     }
 }
 
+// Lane l combined with lane l ^ 32 (xor32_*) or l ^ 16 (xor16_*) without the
+// LDS crossbar: the permlane swap of x with itself hands each lane its
+// partner's value in one of the two results and its own in the other, and the
+// operation is commutative (fmaxf and + give the same bits either way round),
+// so every lane gets exactly op(x, __shfl_xor(x, 32 or 16)).
+__device__ __forceinline__ float xor32_sum(float x) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float xor32_max(float x) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float xor16_max(float x) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+
+// Butterflies over the 64 lanes, partner lane ^ 32, ^ 16, ^ 8, ^ 4, ^ 2, ^ 1
+// in that order, each step combining the lane's and its partner's partial
+// result: the bits of `for (o = 32; o > 0; o >>= 1) x op= __shfl_xor(x, o)`.
+// Only the ^ 4 step goes through the LDS crossbar (GFX9 DPP has no such
+// pattern); the others are permlane swaps and DPP moves.
 __device__ __forceinline__ float wave_max(float x) {
-    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
-    return x;
+    x = xor32_max(x);
+    x = xor16_max(x);
+    x = fmaxf(x, dpp_mov<DPP_ROW_ROR8>(x));
+    x = fmaxf(x, __shfl_xor(x, 4, 64));
+    x = fmaxf(x, dpp_mov<DPP_QUAD_2301>(x));
+    return fmaxf(x, dpp_mov<DPP_QUAD_1032>(x));
 }
 __device__ __forceinline__ float wave_sum(float x) {
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-    return x;
+    x = xor32_sum(x);
+    x = xor16_sum(x);
+    x += dpp_mov<DPP_ROW_ROR8>(x);
+    x += __shfl_xor(x, 4, 64);
+    x += dpp_mov<DPP_QUAD_2301>(x);
+    return x + dpp_mov<DPP_QUAD_1032>(x);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) {

@@ -386,6 +386,8 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
 #pragma unroll
             for (int i = 0; i < 4; ++i) s[i] = tok + i < Leff ? sacc[i] * p.qscale : -INFINITY;
             float mb = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+            // (ds_bpermute: on the LDS pipe beside the VALU work of the block,
+            // measurably faster here than the VALU permlane swaps)
             mb = fmaxf(mb, shfl_xor_f(mb, 16));
             mb = fmaxf(mb, shfl_xor_f(mb, 32));
 
@@ -470,8 +472,7 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[g * 8 + e] = acc[g][e];
         reduce_scatter_high_bits<NV, LO>(v);
-        float ltot = lpart + shfl_xor_f(lpart, 16);
-        ltot += shfl_xor_f(ltot, 32);
+        const float ltot = xor32_sum(xor16_sum(lpart));
         if (j == 0) {
             h_s[0][t] = ltot;
             h_s[1][t] = m;

@@ -348,8 +348,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
             float mb = sc[0];
 #pragma unroll
             for (int e = 1; e < KS / 4; ++e) mb = fmaxf(mb, sc[e]);
-            mb = fmaxf(mb, shfl_xor_f(mb, 16));
-            mb = fmaxf(mb, shfl_xor_f(mb, 32));
+            mb = xor32_max(xor16_max(mb));
             if (mb > m[c] + kPrefillLazy) {   // lane-local: the row's state lives in this lane
                 const float alpha = m[c] == -INFINITY ? 0.0f : fast_exp2(m[c] - mb);
                 m[c] = mb;
@@ -417,8 +416,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
     // ---- output: O[row][dims 16 dt + 4j + i] = acc / l
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-        float ltot = lsum[c] + shfl_xor_f(lsum[c], 16);
-        ltot += shfl_xor_f(ltot, 32);
+        const float ltot = xor32_sum(xor16_sum(lsum[c]));
         if (live[c]) {
             const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
             float* o = p.out + qrow[c] * HD;
