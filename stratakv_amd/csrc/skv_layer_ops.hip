@@ -104,7 +104,10 @@ constexpr int kGemvMaxLdsK = 8192;     // x staged in LDS up to this many inputs
 // NU at a time.  Each lane accumulates its elements in increasing k whatever
 // NU is, so every caller computes a row with exactly the same arithmetic and
 // fused and separate projections give the same bits.
-template <bool BF16W, int NU = kGemvUnroll>
+// FULL: the caller guarantees K >= STEP, so the constructor issues its loads
+// without a branch (a branch around them makes the compiler's wait counts
+// after it assume the worst and wait for the weights before anything else).
+template <bool BF16W, int NU = kGemvUnroll, bool FULL = false>
 struct PairPrefetch {
     static constexpr int EPL = BF16W ? 8 : 4;    // elements per 16-byte load
     static constexpr int STEP = 64 * EPL;        // elements per wave-wide load
@@ -120,7 +123,7 @@ struct PairPrefetch {
         // Every one of the NU loads is issued (steps past npre repeat step
         // npre - 1, in bounds, and are never accumulated), so all of them are
         // in flight together.
-        if (npre > 0) {
+        if (FULL || npre > 0) {
 #pragma unroll
             for (int u = 0; u < NU; ++u)
 #pragma unroll
@@ -412,11 +415,13 @@ __global__ __launch_bounds__(256) void add_kernel(float* __restrict__ t, const f
 //             a wavefront of q or k takes rows (i, i + hd/2) of one head and
 //             rotates them (rope_kernel's arithmetic) before storing;
 //   GATE_UP   gate row n and up row n of the normalised input -> swiglu;
-//   RESIDUAL  y = W x + residual (o_proj and down_proj with their residual add).
+//   RESIDUAL  y = W x + residual (o_proj and down_proj with their residual add);
+//   LINEAR    y = W x (+ bias): skv_linear_f32 of one row (the same rows and
+//             arithmetic as gemv_rows_vec_kernel, staged without branches).
 // Bias, when present, is added before the rotation, as Linear::forward_into
 // does before the RoPE step.
 // ---------------------------------------------------------------------------
-enum FusedMode : int { FUSED_QKV = 0, FUSED_GATE_UP = 1, FUSED_RESIDUAL = 2 };
+enum FusedMode : int { FUSED_QKV = 0, FUSED_GATE_UP = 1, FUSED_RESIDUAL = 2, FUSED_LINEAR = 3 };
 
 struct FusedGemv {
     const float* x;
@@ -444,6 +449,9 @@ struct FusedRowPair {
     bool live, rope;
 };
 
+// `item` must be wave-uniform (the callers pass the wave index through
+// readfirstlane), so the matrix choice and the row pointers are scalar values
+// and the weight addresses never wait on a vector load of the arguments.
 template <int MODE>
 __device__ __forceinline__ FusedRowPair fused_row_pair(const FusedGemv& f, int item) {
     FusedRowPair r{0, 0, 0, 0, 0, item, true, false};
@@ -472,39 +480,46 @@ __device__ __forceinline__ const char* fused_row_ptr(const FusedGemv& f, int m, 
     return static_cast<const char*>(f.w[m]) + static_cast<int64_t>(r) * f.row_bytes[m];
 }
 
-template <bool BF16W, int MODE, int NU, int XU>
+template <bool BF16W, int MODE, int NU, int XU, bool NORM>
 __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
-    extern __shared__ float x_s[];  // [K] input (+ [K] gamma while normalising)
+    extern __shared__ float x_s[];  // [256 XU] input, normalised when NORM (padding past K unused)
     __shared__ float red[4];
     const int t = threadIdx.x, lane = t & 63;
     const int K = f.K;
     auto bias_of = [&](int m, int r) { return f.bias[m] != nullptr ? f.bias[m][r] : 0.0f; };
-    const FusedRowPair rp = fused_row_pair<MODE>(f, blockIdx.x * 4 + (t >> 6));
+    const FusedRowPair rp = fused_row_pair<MODE>(f, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(t >> 6));
     const int ma = rp.ma, mb = rp.mb, ra = rp.ra, rb = rp.rb, seg = rp.seg, p = rp.p;
     const bool live = rp.live, rope = rp.rope;
     // Loads in issue order: all of x (and gamma), XU per thread (K <= 256 XU),
-    // then this wavefront's weights, so storing x to LDS waits only for x
-    // (wait counts are in issue order) while the weights stay in flight.
+    // then this wavefront's weights.  Everything up to the dot products is
+    // straight-line code on registers and unconditional LDS stores (elements
+    // past K land in padding), so the waits before it count only the x and
+    // gamma loads and the weights stay in flight through the normalisation.
     float xv[XU], gv[XU];
-    const bool norm = f.gamma != nullptr;
 #pragma unroll
     for (int u = 0; u < XU; ++u) xv[u] = f.x[min(t + 256 * u, K - 1)];
-    if (norm)
+    if constexpr (NORM)
 #pragma unroll
         for (int u = 0; u < XU; ++u) gv[u] = f.gamma[min(t + 256 * u, K - 1)];
-    PairPrefetch<BF16W, NU> pf(fused_row_ptr(f, ma, ra), fused_row_ptr(f, mb, rb), K, lane);
+    __builtin_amdgcn_sched_barrier(0);  // keep the weight loads after x's
+    PairPrefetch<BF16W, NU, true> pf(fused_row_ptr(f, ma, ra), fused_row_ptr(f, mb, rb), K, lane);
+    if constexpr (NORM) {
+        // rms_inverse's arithmetic on the registers: thread t sums x[t],
+        // x[t + 256], ... (below K) in that order with fma, then the wave and
+        // the 4 wavefronts.
+        float ss = 0.0f;
 #pragma unroll
-    for (int u = 0; u < XU; ++u) {
-        const int i = t + 256 * u;
-        if (i < K) {
-            x_s[i] = xv[u];
-            if (norm) x_s[K + i] = gv[u];
-        }
-    }
-    if (norm) {
+        for (int u = 0; u < XU; ++u) ss = t + 256 * u < K ? fmaf(xv[u], xv[u], ss) : ss;
+        ss = wave_sum(ss);
+        if (lane == 0) red[t >> 6] = ss;
         __syncthreads();
-        const float inv = rms_inverse([&](int i) { return x_s[i]; }, K, f.eps, red);
-        for (int i = t; i < K; i += 256) x_s[i] = x_s[i] * inv * x_s[K + i];
+        const float total = (red[0] + red[1]) + (red[2] + red[3]);
+        const float inv = 1.0f / sqrtf(total / static_cast<float>(K) + f.eps);
+#pragma unroll
+        for (int u = 0; u < XU; ++u) x_s[t + 256 * u] = xv[u] * inv * gv[u];
+    } else {
+#pragma unroll
+        for (int u = 0; u < XU; ++u) x_s[t + 256 * u] = xv[u];
     }
     __syncthreads();
     if (!live) return;
@@ -524,10 +539,15 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
         }
     } else if constexpr (MODE == FUSED_GATE_UP) {
         if (lane == 0) f.y[0][ra] = swiglu_of(a + bias_of(0, ra), b + bias_of(1, ra));
-    } else {
+    } else if constexpr (MODE == FUSED_RESIDUAL) {
         if (lane == 0) {
             f.y[0][ra] = (a + bias_of(0, ra)) + f.residual[ra];
             if (rb != ra) f.y[0][rb] = (b + bias_of(0, rb)) + f.residual[rb];
+        }
+    } else {
+        if (lane == 0) {
+            f.y[0][ra] = a + bias_of(0, ra);
+            if (rb != ra) f.y[0][rb] = b + bias_of(0, rb);
         }
     }
 }
@@ -558,7 +578,7 @@ __global__ __launch_bounds__(64 * WPG) void fused_gemv_rows_kernel(FusedGemv f) 
     const int K = f.K, steps = K / STEP, rows = f.rows;
     const int ntiles = cdiv(rows, T);
     auto bias_of = [&](int m, int r) { return f.bias[m] != nullptr ? f.bias[m][r] : 0.0f; };
-    const FusedRowPair rp = fused_row_pair<MODE>(f, blockIdx.x * WPG + (t >> 6));
+    const FusedRowPair rp = fused_row_pair<MODE>(f, blockIdx.x * WPG + __builtin_amdgcn_readfirstlane(t >> 6));
     f32x4_t st[LPT];
     auto load_step = [&](int tile, int c) __attribute__((always_inline)) {  // rows past the end repeat the last row
 #pragma unroll
@@ -656,21 +676,25 @@ __global__ __launch_bounds__(64 * WPG) void fused_gemv_rows_kernel(FusedGemv f) 
 // Common checks of the fused entry points: output-major rows, 16-byte aligned,
 // input staged in LDS.
 bool fused_rows_ok(const void* w, int64_t stride_k, int64_t stride_n, int K, int esz) {
+    const int step = esz == 2 ? 512 : 256;  // one wave-wide load of a row
     return w != nullptr && stride_k == 1 && stride_n >= K && aligned16(w) &&
-           (stride_n * esz) % 16 == 0 && K <= kGemvMaxLdsK;
+           (stride_n * esz) % 16 == 0 && K >= step && K <= kGemvMaxLdsK;
 }
 
 template <int MODE>
 int launch_fused(const FusedGemv& f, bool bf16, int items, hipStream_t s) {
     const unsigned grid = static_cast<unsigned>(cdiv(items, 4));
-    const size_t lds = sizeof(float) * static_cast<size_t>(f.K) * (f.gamma != nullptr ? 2 : 1);
-    // The whole input is preloaded (XU elements per thread) and up to 12
-    // wave-wide steps of each weight row are requested at once.
-    auto go = [&](auto kern) { kern<<<grid, 256, lds, s>>>(f); };
-#define SKV_FUSED(NU_B, NU_F, XU_)                                                  \
-    {                                                                               \
-        if (bf16) go(fused_gemv_kernel<true, MODE, NU_B, XU_>);                     \
-        else go(fused_gemv_kernel<false, MODE, NU_F, XU_>);                         \
+    // The whole input is preloaded (XU elements per thread, staged into
+    // 256 XU floats of LDS) and up to 12 wave-wide steps of each weight row are
+    // requested at once.
+    const bool norm = f.gamma != nullptr;
+    auto go = [&](auto kern, int xu) { kern<<<grid, 256, sizeof(float) * 256 * static_cast<size_t>(xu), s>>>(f); };
+#define SKV_FUSED(NU_B, NU_F, XU_)                                                              \
+    {                                                                                           \
+        if (bf16 && norm) go(fused_gemv_kernel<true, MODE, NU_B, XU_, MODE <= FUSED_GATE_UP>, XU_);  \
+        else if (bf16) go(fused_gemv_kernel<true, MODE, NU_B, XU_, false>, XU_);                \
+        else if (norm) go(fused_gemv_kernel<false, MODE, NU_F, XU_, MODE <= FUSED_GATE_UP>, XU_);    \
+        else go(fused_gemv_kernel<false, MODE, NU_F, XU_, false>, XU_);                         \
     }
     if (f.K <= 2048) SKV_FUSED(4, 8, 8)
     else if (f.K <= 4096) SKV_FUSED(8, 12, 16)
@@ -740,6 +764,17 @@ extern "C" int skv_linear_f32(const float* x, int rows, const void* weight, int 
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool bf16 = weight_dtype == SKV_DTYPE_BF16;
     const int64_t esz = bf16 ? 2 : 4;
+    if (rows == 1 && fused_rows_ok(weight, stride_k, stride_n, in_dim, static_cast<int>(esz))) {
+        FusedGemv f{};
+        f.x = x;
+        f.K = in_dim;
+        f.w[0] = weight;
+        f.row_bytes[0] = stride_n * esz;
+        f.bias[0] = bias;
+        f.n[0] = out_dim;
+        f.y[0] = y;
+        return launch_fused<FUSED_LINEAR>(f, bf16, cdiv(out_dim, 2), s);
+    }
     if (stride_k == 1 && aligned16(weight) && (stride_n * esz) % 16 == 0 && rows <= 64) {
         const unsigned grid = static_cast<unsigned>(cdiv(out_dim, 4 * kGemvRowsPerWave));
         const bool lds_x = static_cast<int64_t>(rows) * in_dim <= kGemvMaxLdsK;
