@@ -568,7 +568,7 @@ constexpr int kRowsTile = 16;
 
 template <bool BF16W, int MODE, int NU, int WPG>
 __global__ __launch_bounds__(64 * WPG) void fused_gemv_rows_kernel(FusedGemv f) {
-    using PF = PairPrefetch<BF16W, NU>;
+    using PF = PairPrefetch<BF16W, NU, true>;  // K is a nonzero multiple of STEP
     constexpr int STEP = PF::STEP, EPL = PF::EPL, T = kRowsTile;
     constexpr int Q4 = STEP / 4;                  // float4 per staged input row
     constexpr int LPT = T * Q4 / (64 * WPG);      // float4 staged per thread per step
