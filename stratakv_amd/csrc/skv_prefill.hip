@@ -140,6 +140,7 @@ template <int HD, int G, bool QF32>
 __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(PrefillParams p) {
     using Lds = PrefillLds<HD>;
     constexpr int KS = kPrefillKeys;
+    static_assert(KS == 64, "one validity bit per key of a step in a 64-bit mask");
     constexpr int CH = HD / 8;              // 16-byte chunks per row
     constexpr int NKC = HD / 32;            // 32-dim steps of S
     constexpr int NDT = HD / 16;            // 16-dim tiles of O
@@ -183,6 +184,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
     const int keys_end = min(last_pos + 1, nb_seq * 16);  // keys [0, keys_end) may be read
     const int32_t* table = p.tables + static_cast<int64_t>(b) * p.max_blocks;
     const int64_t row_stride = static_cast<int64_t>(p.Hkv) * HD;
+    // Position of this wave's first query row (its rows' positions only grow).
+    const int wave_first_pos = base_pos + (wv * 32) / G;
 
     // This lane's two query rows (column t of the two column groups).
     int qpos[2];
@@ -332,7 +335,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
             }
         }
 
-        // ---- online softmax per row, P^T operands (hi + lo bf16 parts)
+        // ---- online softmax per row, P^T operands (hi + lo bf16 parts).
+        // Scores stay unscaled: qscale > 0, so max(s) * qscale is the max of
+        // the scaled scores, and the exponent is one fma.  Steps whose keys
+        // all exist and precede the wave's first query position (all but the
+        // diagonal steps of a tile) skip the mask.
+        const bool need_mask = !(valid_cur == ~0ull && k0 + KS - 1 <= wave_first_pos);
         bf16x8_t phi[2][KS / 32], plo[2][KS / 32];
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
@@ -340,15 +348,21 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
 #pragma unroll
             for (int kt = 0; kt < KS / 16; ++kt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int kl = kt * 16 + 4 * j + i;
-                    const bool keep = ((valid_cur >> kl) & 1u) && (k0 + kl <= qpos[c]);
-                    sc[kt * 4 + i] = keep ? s[c][kt][i] * p.qscale : -INFINITY;
-                }
+                for (int i = 0; i < 4; ++i) sc[kt * 4 + i] = s[c][kt][i];
+            if (need_mask) {
+#pragma unroll
+                for (int kt = 0; kt < KS / 16; ++kt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int kl = kt * 16 + 4 * j + i;
+                        const bool keep = ((valid_cur >> kl) & 1u) && (k0 + kl <= qpos[c]);
+                        sc[kt * 4 + i] = keep ? sc[kt * 4 + i] : -INFINITY;
+                    }
+            }
             float mb = sc[0];
 #pragma unroll
             for (int e = 1; e < KS / 4; ++e) mb = fmaxf(mb, sc[e]);
-            mb = xor32_max(xor16_max(mb));
+            mb = xor32_max(xor16_max(mb)) * p.qscale;
             if (mb > m[c] + kPrefillLazy) {   // lane-local: the row's state lives in this lane
                 const float alpha = m[c] == -INFINITY ? 0.0f : fast_exp2(m[c] - mb);
                 m[c] = mb;
@@ -362,7 +376,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
             float pr[KS / 4];
 #pragma unroll
             for (int e = 0; e < KS / 4; ++e) {
-                pr[e] = fast_exp2(sc[e] - ms);
+                pr[e] = fast_exp2(fmaf(sc[e], p.qscale, -ms));
                 lsum[c] += pr[e];
             }
             // 32-key chunk h: keys {4j..4j+3} = kt 2h, {16+4j..} = kt 2h+1.
