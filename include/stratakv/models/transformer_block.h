@@ -55,13 +55,17 @@ public:
     // positions and attends causally over the whole context
     // (skv_paged_prefill); output may alias hidden_states.  The reference's
     // GPU forward_into takes one token (src/models/transformer_block.cpp:
-    // 348-351); its CPU forward computes these rows (:300-332).  Projection
-    // rows have the bits forward_into gives for each token; the attention of
-    // the chunk runs the prefill kernel instead of the decode kernel.
+    // 348-351); its CPU forward computes these rows (:300-332).  Chunks of
+    // fewer than kPrefillMmRows tokens give every projection row the bits
+    // forward_into gives for that token; longer ones (bf16 weights) run the
+    // projections on the matrix cores, equal to fp32 rounding.  The attention
+    // of the chunk runs the prefill kernel instead of the decode kernel.
     void prefill_into(const Tensor& hidden_states, Tensor& output, int seq_id,
                       memory::PageTable& page_table, memory::BlockPool& block_pool);
     // Tokens per prefill_into pass (longer inputs run in chunks of this many).
     static constexpr int kPrefillChunk = 256;
+    // Chunk length from which the projections run on the matrix cores.
+    static constexpr int kPrefillMmRows = 32;
     void forward_into(const Tensor& hidden_states, Tensor& output, int seq_id,
                       memory::PageTable& page_table, memory::BlockPool& block_pool,
                       bool append_tokens = true);
@@ -117,6 +121,7 @@ private:
     int prefill_rows_ = 0;
     std::optional<Tensor> pf_queries_, pf_keys_, pf_values_, pf_context_, pf_residual_, pf_act_;
     std::optional<Tensor> pf_normalized_, pf_up_, pf_down_;
+    std::optional<Tensor> pf_split_;  // bf16 hi/lo parts of a projection input (matrix-core path)
     std::optional<Tensor> pf_meta_;  // 4 int32: position, chunk offsets {0, n}, context length
 };
 

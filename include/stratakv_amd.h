@@ -350,6 +350,39 @@ int skv_linear_residual_rows_f32(const float* x, int rows, const void* weight, i
                                  const float* bias, const float* residual, float* y,
                                  void* stream);
 
+/* The same three projections for `rows` tokens on the matrix cores, for long
+ * prompts.  The inputs (normalised first with gamma, with the arithmetic of
+ * skv_rmsnorm_f32) are split into bf16 hi = bf16(x) and lo = bf16(x - hi)
+ * parts in `scratch` (rows * in_dim floats, 16-byte aligned, distinct from
+ * every other buffer; its contents are overwritten), and each output is
+ * W hi + W lo with fp32 accumulation: every product is exact and x keeps
+ * ~16 significant bits, so the results agree with the one-token entry points
+ * to fp32 rounding but are not bit-identical to them.  RoPE, bias, SwiGLU
+ * and the residual are applied as in the rows variants (y may alias
+ * residual).  SKV_ERR_UNSUPPORTED (nothing launched) unless the weights are
+ * bf16 aligned output-major rows, in_dim is a multiple of 128 from 512 to 8,192,
+ * every output count is a multiple of 32 (gate/up: 16), head_dim is a
+ * multiple of 32 when rotating, and the outputs (and residual) are 16-byte
+ * aligned.
+ * Replaces: the same reference code as the rows variants
+ * (src/models/transformer_block.cpp:300-332); no counterpart of its own. */
+int skv_fused_qkv_mm_f32(const float* hidden, int rows, const float* gamma, float epsilon,
+                         const void* wq, const void* wk, const void* wv, int weight_dtype,
+                         int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
+                         const float* bias_k, const float* bias_v, int hidden_dim,
+                         int num_heads, int num_kv_heads, int head_dim, int first_position,
+                         float* q, float* k, float* v, float* scratch, void* stream);
+int skv_fused_gate_up_swiglu_mm_f32(const float* x, int rows, const float* gamma, float epsilon,
+                                    const void* w_gate, const void* w_up, int weight_dtype,
+                                    int64_t stride_k, int64_t stride_n_gate,
+                                    int64_t stride_n_up, const float* bias_gate,
+                                    const float* bias_up, int in_dim, int out_dim,
+                                    float* act, float* scratch, void* stream);
+int skv_linear_residual_mm_f32(const float* x, int rows, const void* weight, int weight_dtype,
+                               int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
+                               const float* bias, const float* residual, float* y,
+                               float* scratch, void* stream);
+
 /* ---- model boundary: checkpoint tensors, embedding, token choice --------
  * Checkpoint decode on the device (the host only moves file bytes).  src holds
  * `count` little-endian elements of src_dtype (SKV_DTYPE_BF16 / F16 / FP32).

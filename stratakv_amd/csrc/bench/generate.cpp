@@ -6,9 +6,12 @@
 // Weights: bf16 N(0, 0.02) generated on the device from a seed (norm gammas
 // 1.0), or a safetensors checkpoint loaded with io::load_safetensors_device
 // (then the load is timed too).  Prints one JSON line.
-//   bench_generate [--checkpoint PATH] [--repeat N] [--new N]
+//   bench_generate [--checkpoint PATH] [--repeat N] [--new N] [--prompt N]
+// --prompt N: N prompt tokens (the 16 below, then ids from a fixed 32-bit LCG)
+// instead of 16, to time the prompt pass on long prompts.
 #include <algorithm>
 #include <chrono>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <stdexcept>
@@ -74,12 +77,13 @@ double median(std::vector<double> v) {
 int main(int argc, char** argv) {
     try {
         std::string checkpoint;
-        int repeat = 5, n_new = 128;
+        int repeat = 5, n_new = 128, n_prompt = 16;
         for (int i = 1; i < argc; ++i) {
             const std::string a = argv[i];
             if (a == "--checkpoint" && i + 1 < argc) checkpoint = argv[++i];
             else if (a == "--repeat" && i + 1 < argc) repeat = std::max(1, std::atoi(argv[++i]));
             else if (a == "--new" && i + 1 < argc) n_new = std::max(1, std::atoi(argv[++i]));
+            else if (a == "--prompt" && i + 1 < argc) n_prompt = std::max(1, std::atoi(argv[++i]));
         }
         int devices = 0;
         if (skv_device_count(&devices) != SKV_OK || devices == 0) {
@@ -100,8 +104,13 @@ int main(int argc, char** argv) {
         generation::GeneratorConfig cfg(kHidden, kInter, kHeads, kKv, kLayers, 1024, 16, kVocab, -1);
         generation::Generator gen(cfg, std::move(weights));
         // 16 prompt ids as numpy default_rng(42).integers(0, 32000, 16).
-        const std::vector<int> prompt = {2856, 24766, 20946, 14044, 13856, 27475, 2750, 22315,
-                                         6447, 3013,  16847, 31219, 23544, 24356, 22959, 25154};
+        std::vector<int> prompt = {2856, 24766, 20946, 14044, 13856, 27475, 2750, 22315,
+                                   6447, 3013,  16847, 31219, 23544, 24356, 22959, 25154};
+        prompt.resize(std::min<std::size_t>(prompt.size(), static_cast<std::size_t>(n_prompt)));
+        for (std::uint32_t x = 12345u; prompt.size() < static_cast<std::size_t>(n_prompt);) {
+            x = x * 1664525u + 1013904223u;
+            prompt.push_back(static_cast<int>((x >> 8) % kVocab));
+        }
         std::vector<int> out = gen.generate(prompt, n_new);  // warmup
         std::vector<double> full, one;
         for (int r = 0; r < repeat; ++r) {

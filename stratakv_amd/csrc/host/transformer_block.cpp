@@ -278,6 +278,7 @@ void TransformerBlock::ensure_prefill_workspace(int rows) {
     make(pf_normalized_, hidden_dim_);
     make(pf_up_, inter);
     make(pf_down_, hidden_dim_);
+    make(pf_split_, std::max({static_cast<std::size_t>(hidden_dim_), q_dim, inter}));
     if (!pf_meta_) pf_meta_.emplace(std::vector<std::size_t>{4}, DataType::FP32, Device::GPU);
     prefill_rows_ = rows;
 }
@@ -353,6 +354,7 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
     float* ctx = fp(*pf_context_);
     float* h = fp(*pf_residual_);
     float* act = fp(*pf_act_);
+    float* split = fp(*pf_split_);
     auto* meta = static_cast<std::int32_t*>(pf_meta_->raw_data());
 
     for (int c0 = 0; c0 < tokens; c0 += kPrefillChunk) {
@@ -365,15 +367,20 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
         const int nblocks = static_cast<int>(state.physical_blocks.size());
         const std::int32_t meta_h[4] = {p0, 0, n, p0 + n};
         detail::check(skv_write_i32(meta, meta_h, 4, s), "prefill_into: chunk metadata");
+        // Each projection: the matrix-core entry point for long chunks, else
+        // (or when it does not take the shape) the rows kernels, else the
+        // separate kernels.
+        const bool mm = n >= kPrefillMmRows;
 
         // Input RMSNorm, q/k/v projections and RoPE at p0 + row.
+        auto qkv = [&](auto entry, float* scratch) {
+            return entry(x, n, cfp(norm1_.gamma()), norm1_.epsilon(), wq.weight().raw_data(), wk.weight().raw_data(),
+                         wv.weight().raw_data(), wdtype(wq), stride_k(wq), qkv_strides, bias_of(wq), bias_of(wk),
+                         bias_of(wv), hidden, num_heads, num_kv_heads, head_dim, p0, q, k, v, scratch, s);
+        };
         if (!(same_dtype &&
-              fused(skv_fused_qkv_rows_f32(x, n, cfp(norm1_.gamma()), norm1_.epsilon(), wq.weight().raw_data(),
-                                           wk.weight().raw_data(), wv.weight().raw_data(), wdtype(wq),
-                                           stride_k(wq), qkv_strides, bias_of(wq), bias_of(wk), bias_of(wv),
-                                           hidden, num_heads, num_kv_heads, head_dim, p0, q, k, v,
-                                           fp(*pf_normalized_), s),
-                    "prefill_into: fused rmsnorm + q/k/v + rope"))) {
+              ((mm && fused(qkv(skv_fused_qkv_mm_f32, split), "prefill_into: q/k/v on the matrix cores")) ||
+               fused(qkv(skv_fused_qkv_rows_f32, fp(*pf_normalized_)), "prefill_into: fused rmsnorm + q/k/v + rope")))) {
             float* xn = fp(*pf_normalized_);
             detail::check(skv_rmsnorm_f32(x, xn, cfp(norm1_.gamma()), n, hidden, norm1_.epsilon(), s),
                           "prefill_into: input rmsnorm");
@@ -398,21 +405,26 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                       "prefill_into: paged prefill attention");
 
         // o_proj + residual (reads x before y is written: aliasing-safe).
-        if (!fused(skv_linear_residual_rows_f32(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
-                                                stride_n(wo), q_dim, hidden, bias_of(wo), x, h, s),
-                   "prefill_into: fused o_proj + residual")) {
+        if (!((mm && fused(skv_linear_residual_mm_f32(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
+                                                      stride_n(wo), q_dim, hidden, bias_of(wo), x, h, split, s),
+                           "prefill_into: o_proj on the matrix cores")) ||
+              fused(skv_linear_residual_rows_f32(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
+                                                 stride_n(wo), q_dim, hidden, bias_of(wo), x, h, s),
+                    "prefill_into: fused o_proj + residual"))) {
             linear(wo, ctx, n, h, "prefill_into: o_proj");
             detail::check(skv_add_f32(h, x, n * hidden, s), "prefill_into: residual");
         }
         // Post-attention RMSNorm, gate/up and SwiGLU.
+        auto gate_up = [&](auto entry, float* scratch) {
+            return entry(h, n, cfp(norm2_.gamma()), norm2_.epsilon(), gate_proj_.weight().raw_data(),
+                         up_proj_.weight().raw_data(), wdtype(gate_proj_), stride_k(gate_proj_), stride_n(gate_proj_),
+                         stride_n(up_proj_), bias_of(gate_proj_), bias_of(up_proj_), hidden, inter, act, scratch, s);
+        };
         if (!(ffn_same &&
-              fused(skv_fused_gate_up_swiglu_rows_f32(h, n, cfp(norm2_.gamma()), norm2_.epsilon(),
-                                                      gate_proj_.weight().raw_data(), up_proj_.weight().raw_data(),
-                                                      wdtype(gate_proj_), stride_k(gate_proj_),
-                                                      stride_n(gate_proj_), stride_n(up_proj_),
-                                                      bias_of(gate_proj_), bias_of(up_proj_), hidden, inter, act,
-                                                      fp(*pf_normalized_), s),
-                    "prefill_into: fused rmsnorm + gate/up + swiglu"))) {
+              ((mm && fused(gate_up(skv_fused_gate_up_swiglu_mm_f32, split),
+                            "prefill_into: gate/up on the matrix cores")) ||
+               fused(gate_up(skv_fused_gate_up_swiglu_rows_f32, fp(*pf_normalized_)),
+                     "prefill_into: fused rmsnorm + gate/up + swiglu")))) {
             float* hn = fp(*pf_normalized_);
             float* up = fp(*pf_up_);
             detail::check(skv_rmsnorm_f32(h, hn, cfp(norm2_.gamma()), n, hidden, norm2_.epsilon(), s),
@@ -422,10 +434,14 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
             detail::check(skv_swiglu_f32(act, up, n * inter, s), "prefill_into: swiglu");
         }
         // down_proj + residual into the output rows.
-        if (!fused(skv_linear_residual_rows_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
-                                                stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
-                                                bias_of(down_proj_), h, y, s),
-                   "prefill_into: fused down_proj + residual")) {
+        if (!((mm && fused(skv_linear_residual_mm_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
+                                                      stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
+                                                      bias_of(down_proj_), h, y, split, s),
+                           "prefill_into: down_proj on the matrix cores")) ||
+              fused(skv_linear_residual_rows_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
+                                                 stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
+                                                 bias_of(down_proj_), h, y, s),
+                    "prefill_into: fused down_proj + residual"))) {
             float* d = fp(*pf_down_);
             linear(down_proj_, act, n, d, "prefill_into: down_proj");
             detail::check(skv_add_f32(h, d, n * hidden, s), "prefill_into: residual");

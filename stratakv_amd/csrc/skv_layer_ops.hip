@@ -737,6 +737,262 @@ int launch_fused_rows(const FusedGemv& f, bool bf16, int items, hipStream_t s) {
                      bf16 ? 6144 : 2048);
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core projections of a block of tokens (long prompts).  The input
+// rows (fp32, normalised first when gamma is given, with rmsnorm_kernel's
+// arithmetic) are split once into two bf16 planes, hi = bf16(x) and
+// lo = bf16(x - hi), so that W x = W hi + W lo on v_mfma_f32_16x16x32_bf16
+// with fp32 accumulation: every product of a bf16 weight with a part is exact
+// and x is carried to ~16 significant bits, close to the fp32 dot products
+// of the one-token kernels (not bit-identical to them: the summation order
+// differs).
+//
+// split_rows_kernel: one workgroup per row; the planes go to the caller's
+// scratch of rows * K floats (hi plane, then lo plane, rows * K bf16 each).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ in,
+                                                         const float* __restrict__ gamma, int n, float eps,
+                                                         uint16_t* __restrict__ hi, uint16_t* __restrict__ lo) {
+    extern __shared__ float xg_s[];  // [2][n]: the row and gamma
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const float* x = in + row * n;
+    stage_to_lds(x, xg_s, n);
+    if (gamma != nullptr) stage_to_lds(gamma, xg_s + n, n);
+    __syncthreads();
+    float inv = 1.0f;
+    if (gamma != nullptr) inv = rms_inverse([&](int i) { return xg_s[i]; }, n, eps, red);
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = gamma != nullptr ? xg_s[i] * inv * xg_s[n + i] : xg_s[i];
+        const __bf16 h = static_cast<__bf16>(v);
+        const __bf16 l = static_cast<__bf16>(v - static_cast<float>(h));
+        hi[row * n + i] = __builtin_bit_cast(uint16_t, h);
+        lo[row * n + i] = __builtin_bit_cast(uint16_t, l);
+    }
+}
+
+typedef __bf16 mm_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef uint32_t mm_u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMmTokens = 64;   // tokens per workgroup (4 column tiles of 16)
+constexpr int kMmSplitK = 4;    // wavefronts per workgroup, each a quarter of K
+
+struct MmArgs {
+    FusedGemv f;
+    const uint16_t* x_hi;       // [rows][K] bf16 planes of the input
+    const uint16_t* x_lo;
+    int groups;                 // 32-feature groups
+    int token_tiles;            // cdiv(rows, kMmTokens)
+};
+
+// Feature group `g` (32 outputs as two 16-row tiles) of a projection:
+// matrix, first row of each tile, and whether the pair (tile 0 row r, tile 1
+// row r) is rotated together.  QKV with RoPE pairs rows (r, r + hd/2) of one
+// head (hd a multiple of 32); GATE_UP takes rows r of gate and of up; the
+// others 32 consecutive rows.
+struct MmGroup {
+    int m, r0, r1;
+    bool rope;
+};
+
+template <int MODE>
+__device__ __forceinline__ MmGroup mm_group(const FusedGemv& f, int g) {
+    MmGroup q{0, 0, 0, false};
+    if constexpr (MODE == FUSED_QKV) {
+        while (q.m < 2 && g >= f.n[q.m] / 32) g -= f.n[q.m] / 32, ++q.m;
+        q.rope = q.m < 2 && f.position >= 0;
+        if (q.rope) {
+            const int half = f.head_dim / 2, per_head = half / 16;
+            q.r0 = (g / per_head) * f.head_dim + (g % per_head) * 16;
+            q.r1 = q.r0 + half;
+        } else {
+            q.r0 = 32 * g;
+            q.r1 = q.r0 + 16;
+        }
+    } else if constexpr (MODE == FUSED_GATE_UP) {
+        q.r0 = q.r1 = 16 * g;
+    } else {
+        q.r0 = 32 * g;
+        q.r1 = q.r0 + 16;
+    }
+    return q;
+}
+
+// One workgroup = one feature group x kMmTokens tokens.  Wavefront w computes
+// the 32 x 64 tile over k in [w K/4, (w + 1) K/4) with operands loaded
+// straight from global memory in the MFMA layouts (lane (t, j): A = weight
+// row t of a tile, k chunk 8j..8j+7; B = token t of a column tile, the same
+// chunk), RING k-steps ahead (RING divides the wavefront's step count, so
+// the loop has no branch around a load and never waits for all of them); the
+// four partial tiles are summed through LDS in a fixed order and wavefront 0
+// applies the epilogue.  Output lane layout: acc[a][c][i] = feature (tile a)
+// 4j + i, token 16c + t.
+template <int MODE, int RING>
+__global__ __launch_bounds__(64 * kMmSplitK) void proj_mm_kernel(MmArgs args) {
+    const FusedGemv& f = args.f;
+    __shared__ f32x4_t part[kMmSplitK - 1][8][64];
+    const int lane = threadIdx.x & 63, t = lane & 15, j = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Workgroups are dealt to the 8 XCDs round-robin: the token tiles of one
+    // feature group go to the same XCD, one after another, so its weight rows
+    // are read from HBM once and then from that XCD's L2.
+    const int id = blockIdx.x, xcd = id & 7, local = id >> 3;
+    const int g = (local / args.token_tiles) * 8 + xcd;
+    const int tile = local % args.token_tiles;
+    if (g >= args.groups) return;
+    const MmGroup grp = mm_group<MODE>(f, g);
+    const int K = f.K, rows = f.rows;
+    const int ksteps = K / 32 / kMmSplitK, kbase = w * ksteps * 32;
+    const int tok0 = tile * kMmTokens;
+
+    const int mb = MODE == FUSED_GATE_UP ? 1 : grp.m;
+    const char* wa = static_cast<const char*>(f.w[grp.m]) + static_cast<int64_t>(grp.r0 + t) * f.row_bytes[grp.m];
+    const char* wb = static_cast<const char*>(f.w[mb]) + static_cast<int64_t>(grp.r1 + t) * f.row_bytes[mb];
+    const uint16_t* xh[4];
+    const uint16_t* xl[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int64_t tok = min(tok0 + 16 * c + t, rows - 1);
+        xh[c] = args.x_hi + tok * K;
+        xl[c] = args.x_lo + tok * K;
+    }
+
+    struct Ops {
+        mm_u32x4_t a[2], h[4], l[4];
+    };
+    auto load = [&](int s, Ops& o) __attribute__((always_inline)) {
+        const int k = kbase + 32 * s + 8 * j;
+        o.a[0] = *reinterpret_cast<const mm_u32x4_t*>(wa + 2 * k);
+        o.a[1] = *reinterpret_cast<const mm_u32x4_t*>(wb + 2 * k);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            o.h[c] = *reinterpret_cast<const mm_u32x4_t*>(xh[c] + k);
+            o.l[c] = *reinterpret_cast<const mm_u32x4_t*>(xl[c] + k);
+        }
+    };
+    f32x4_t acc[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[a][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    auto mfma = [&](const Ops& o) __attribute__((always_inline)) {
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const mm_bf16x8_t av = __builtin_bit_cast(mm_bf16x8_t, o.a[a]);
+                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(mm_bf16x8_t, o.h[c]),
+                                                                    acc[a][c], 0, 0, 0);
+                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(mm_bf16x8_t, o.l[c]),
+                                                                    acc[a][c], 0, 0, 0);
+            }
+    };
+    // Steps 0 .. RING - 1 loaded up front; each later step's operands are
+    // loaded when its ring slot is consumed; the last RING steps load nothing.
+    Ops ring[RING];
+#pragma unroll
+    for (int u = 0; u < RING; ++u) load(u, ring[u]);
+    for (int s0 = 0; s0 < ksteps - RING; s0 += RING) {
+#pragma unroll
+        for (int u = 0; u < RING; ++u) {
+            const Ops o = ring[u];
+            load(s0 + u + RING, ring[u]);
+            __builtin_amdgcn_sched_barrier(0);   // issue order kept: the loads stay RING steps ahead
+            mfma(o);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < RING; ++u) mfma(ring[u]);
+
+    // Sum of the K quarters in the order 0 + 1 + 2 + 3.
+    if (w > 0) {
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) part[w - 1][4 * a + c][lane] = acc[a][c];
+    }
+    __syncthreads();
+    if (w > 0) return;
+#pragma unroll
+    for (int q = 0; q < kMmSplitK - 1; ++q)
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[a][c] += part[q][4 * a + c][lane];
+
+    auto bias4 = [&](int m, int r) {
+        const float* b = f.bias[m];
+        return b != nullptr ? f32x4_t{b[r], b[r + 1], b[r + 2], b[r + 3]} : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    };
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int tok = tok0 + 16 * c + t;
+        if (tok >= rows) continue;
+        const int ra = grp.r0 + 4 * j, rb = grp.r1 + 4 * j;
+        if constexpr (MODE == FUSED_QKV) {
+            f32x4_t ya = acc[0][c] + bias4(grp.m, ra), yb = acc[1][c] + bias4(grp.m, rb);
+            if (grp.rope) {
+                const int half = f.head_dim / 2;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float cs, sn, va = ya[i], vb = yb[i];
+                    rope_cos_sin(f.position + tok, f.rope.cs[(ra + i) % f.head_dim % half], cs, sn);
+                    rotate_pair(va, vb, cs, sn);
+                    ya[i] = va;
+                    yb[i] = vb;
+                }
+            }
+            float* y = f.y[grp.m] + static_cast<int64_t>(tok) * f.n[grp.m];
+            *reinterpret_cast<f32x4_t*>(y + ra) = ya;
+            *reinterpret_cast<f32x4_t*>(y + rb) = yb;
+        } else if constexpr (MODE == FUSED_GATE_UP) {
+            const f32x4_t gv = acc[0][c] + bias4(0, ra), uv = acc[1][c] + bias4(1, ra);
+            const f32x4_t act = {swiglu_of(gv[0], uv[0]), swiglu_of(gv[1], uv[1]), swiglu_of(gv[2], uv[2]),
+                                 swiglu_of(gv[3], uv[3])};
+            *reinterpret_cast<f32x4_t*>(f.y[0] + static_cast<int64_t>(tok) * f.n[0] + ra) = act;
+        } else {
+            const int64_t row = static_cast<int64_t>(tok) * f.n[0];
+            const f32x4_t res_a = *reinterpret_cast<const f32x4_t*>(f.residual + row + ra);
+            const f32x4_t res_b = *reinterpret_cast<const f32x4_t*>(f.residual + row + rb);
+            *reinterpret_cast<f32x4_t*>(f.y[0] + row + ra) = (acc[0][c] + bias4(0, ra)) + res_a;
+            *reinterpret_cast<f32x4_t*>(f.y[0] + row + rb) = (acc[1][c] + bias4(0, rb)) + res_b;
+        }
+    }
+}
+
+// Shapes the matrix-core projections take: bf16 weights in 16-byte aligned
+// output-major rows, K a multiple of 128 (32-wide k-steps split four ways),
+// every matrix's output count a multiple of 32 (16 for gate/up), and for
+// RoPE head_dim a multiple of 32.
+bool mm_supported(const FusedGemv& f, int nmat, int esz, int64_t stride_k) {
+    if (esz != 2 || stride_k != 1 || f.K < 128 || f.K % 128 != 0) return false;
+    for (int m = 0; m < nmat; ++m)
+        if (f.w[m] == nullptr || !aligned16(f.w[m]) || f.row_bytes[m] % 16 != 0 || f.row_bytes[m] < 2 * f.K ||
+            f.n[m] % 16 != 0 || (nmat != 2 && f.n[m] % 32 != 0))
+            return false;
+    return true;
+}
+
+// Splits x (normalised when gamma != nullptr) into the scratch planes and
+// launches proj_mm_kernel over `groups` feature groups.
+template <int MODE>
+int launch_mm(FusedGemv f, int groups, const float* gamma, float eps, float* scratch, hipStream_t s) {
+    const int64_t elems = static_cast<int64_t>(f.rows) * f.K;
+    uint16_t* hi = reinterpret_cast<uint16_t*>(scratch);
+    uint16_t* lo = hi + elems;
+    split_rows_kernel<<<f.rows, 256, 2 * sizeof(float) * f.K, s>>>(f.x, gamma, f.K, eps, hi, lo);
+    if (int rc = check_launch("split_rows_kernel")) return rc;
+    MmArgs a{f, hi, lo, groups, cdiv(f.rows, kMmTokens)};
+    const int64_t wgs = static_cast<int64_t>(cdiv(groups, 8)) * 8 * a.token_tiles;
+    SKV_REQUIRE(wgs <= INT32_MAX, "proj_mm_kernel: grid of %lld workgroups is too large", static_cast<long long>(wgs));
+    const int ksteps = f.K / 32 / kMmSplitK;
+    const dim3 grid(static_cast<unsigned>(wgs)), block(64 * kMmSplitK);
+    // Two k-steps in flight (a deeper ring runs out of registers).
+    if (ksteps % 2 == 0) proj_mm_kernel<MODE, 2><<<grid, block, 0, s>>>(a);
+    else proj_mm_kernel<MODE, 1><<<grid, block, 0, s>>>(a);
+    return check_launch("proj_mm_kernel");
+}
+
 }  // namespace skv
 
 using namespace skv;
@@ -850,7 +1106,7 @@ int fused_qkv(const char* fn, const float* hidden, int rows, const float* gamma,
               const void* wq, const void* wk, const void* wv, int weight_dtype, int64_t stride_k,
               const int64_t stride_n[3], const float* bias_q, const float* bias_k, const float* bias_v,
               int hidden_dim, int num_heads, int num_kv_heads, int head_dim, int position, float* q,
-              float* k, float* v, float* normalized, void* stream) {
+              float* k, float* v, float* normalized, void* stream, bool mm = false) {
     SKV_REQUIRE(hidden && stride_n && q && k && v && rows > 0 && hidden_dim > 0 && num_heads > 0 &&
                     num_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
                 "%s: invalid pointers or sizes", fn);
@@ -885,6 +1141,17 @@ int fused_qkv(const char* fn, const float* hidden, int rows, const float* gamma,
         return set_error(SKV_ERR_UNSUPPORTED, "%s: head_dim %d exceeds %d", fn, head_dim, 2 * kMaxRopePairs);
     const int items = (ns[0] + ns[1] + ns[2]) / 2;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (mm) {
+        SKV_REQUIRE(normalized != nullptr && aligned16(normalized), "%s: 16-byte aligned scratch required", fn);
+        if (!mm_supported(f, 3, esz, stride_k) || (position >= 0 && head_dim % 32 != 0) || !aligned16(q) ||
+            !aligned16(k) || !aligned16(v))
+            return set_error(SKV_ERR_UNSUPPORTED,
+                             "%s: needs bf16 weights, hidden_dim a multiple of 128, outputs and head_dim multiples "
+                             "of 32 and 16-byte aligned outputs", fn);
+        if (position >= 0) f.rope = rope_inv_freq(head_dim);
+        f.gamma = nullptr;
+        return launch_mm<FUSED_QKV>(f, (ns[0] + ns[1] + ns[2]) / 32, gamma, epsilon, normalized, s);
+    }
     if (rows == 1) {
         if (position >= 0) f.rope = rope_table(head_dim, position);
         return launch_fused<FUSED_QKV>(f, esz == 2, items, s);
@@ -901,7 +1168,7 @@ int fused_qkv(const char* fn, const float* hidden, int rows, const float* gamma,
 int fused_gate_up(const char* fn, const float* x, int rows, const float* gamma, float epsilon,
                   const void* w_gate, const void* w_up, int weight_dtype, int64_t stride_k,
                   int64_t stride_n_gate, int64_t stride_n_up, const float* bias_gate, const float* bias_up,
-                  int in_dim, int out_dim, float* act, float* normalized, void* stream) {
+                  int in_dim, int out_dim, float* act, float* normalized, void* stream, bool mm = false) {
     SKV_REQUIRE(x && act && rows > 0 && in_dim > 0 && out_dim > 0, "%s: invalid pointers or sizes", fn);
     SKV_REQUIRE(weight_dtype == SKV_DTYPE_BF16 || weight_dtype == SKV_DTYPE_FP32,
                 "%s: unknown weight dtype %d", fn, weight_dtype);
@@ -926,6 +1193,15 @@ int fused_gate_up(const char* fn, const float* x, int rows, const float* gamma, 
     f.n[0] = f.n[1] = out_dim;
     f.y[0] = act;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (mm) {
+        SKV_REQUIRE(normalized != nullptr && aligned16(normalized), "%s: 16-byte aligned scratch required", fn);
+        if (!mm_supported(f, 2, esz, stride_k) || !aligned16(act))
+            return set_error(SKV_ERR_UNSUPPORTED,
+                             "%s: needs bf16 weights, in_dim a multiple of 128, out_dim a multiple of 16 and a "
+                             "16-byte aligned output", fn);
+        f.gamma = nullptr;
+        return launch_mm<FUSED_GATE_UP>(f, out_dim / 16, gamma, epsilon, normalized, s);
+    }
     if (rows == 1) return launch_fused<FUSED_GATE_UP>(f, esz == 2, out_dim, s);
     if (!rows_supported(esz == 2, in_dim))
         return set_error(SKV_ERR_UNSUPPORTED, "%s: in_dim %d is not a supported multi-token size", fn, in_dim);
@@ -936,7 +1212,7 @@ int fused_gate_up(const char* fn, const float* x, int rows, const float* gamma, 
 
 int linear_residual(const char* fn, const float* x, int rows, const void* weight, int weight_dtype,
                     int64_t stride_k, int64_t stride_n, int in_dim, int out_dim, const float* bias,
-                    const float* residual, float* y, void* stream) {
+                    const float* residual, float* y, void* stream, float* scratch = nullptr, bool mm = false) {
     SKV_REQUIRE(x && residual && y && rows > 0 && in_dim > 0 && out_dim > 0, "%s: invalid pointers or sizes",
                 fn);
     SKV_REQUIRE(weight_dtype == SKV_DTYPE_BF16 || weight_dtype == SKV_DTYPE_FP32,
@@ -958,6 +1234,14 @@ int linear_residual(const char* fn, const float* x, int rows, const void* weight
     f.y[0] = y;
     f.residual = residual;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (mm) {
+        SKV_REQUIRE(scratch != nullptr && aligned16(scratch), "%s: 16-byte aligned scratch required", fn);
+        if (!mm_supported(f, 1, esz, stride_k) || !aligned16(y) || !aligned16(residual))
+            return set_error(SKV_ERR_UNSUPPORTED,
+                             "%s: needs bf16 weights, in_dim a multiple of 128, out_dim a multiple of 32 and "
+                             "16-byte aligned residual and output", fn);
+        return launch_mm<FUSED_RESIDUAL>(f, out_dim / 32, nullptr, 0.0f, scratch, s);
+    }
     if (rows == 1) return launch_fused<FUSED_RESIDUAL>(f, esz == 2, cdiv(out_dim, 2), s);
     return launch_fused_rows<FUSED_RESIDUAL>(f, esz == 2, cdiv(out_dim, 2), s);
 }
@@ -1022,4 +1306,33 @@ extern "C" int skv_linear_residual_rows_f32(const float* x, int rows, const void
                                             void* stream) {
     return linear_residual("skv_linear_residual_rows_f32", x, rows, weight, weight_dtype, stride_k, stride_n,
                            in_dim, out_dim, bias, residual, y, stream);
+}
+
+extern "C" int skv_fused_qkv_mm_f32(const float* hidden, int rows, const float* gamma, float epsilon,
+                                    const void* wq, const void* wk, const void* wv, int weight_dtype,
+                                    int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
+                                    const float* bias_k, const float* bias_v, int hidden_dim, int num_heads,
+                                    int num_kv_heads, int head_dim, int first_position, float* q, float* k,
+                                    float* v, float* scratch, void* stream) {
+    return fused_qkv("skv_fused_qkv_mm_f32", hidden, rows, gamma, epsilon, wq, wk, wv, weight_dtype, stride_k,
+                     stride_n, bias_q, bias_k, bias_v, hidden_dim, num_heads, num_kv_heads, head_dim,
+                     first_position, q, k, v, scratch, stream, true);
+}
+
+extern "C" int skv_fused_gate_up_swiglu_mm_f32(const float* x, int rows, const float* gamma, float epsilon,
+                                               const void* w_gate, const void* w_up, int weight_dtype,
+                                               int64_t stride_k, int64_t stride_n_gate, int64_t stride_n_up,
+                                               const float* bias_gate, const float* bias_up, int in_dim,
+                                               int out_dim, float* act, float* scratch, void* stream) {
+    return fused_gate_up("skv_fused_gate_up_swiglu_mm_f32", x, rows, gamma, epsilon, w_gate, w_up, weight_dtype,
+                         stride_k, stride_n_gate, stride_n_up, bias_gate, bias_up, in_dim, out_dim, act, scratch,
+                         stream, true);
+}
+
+extern "C" int skv_linear_residual_mm_f32(const float* x, int rows, const void* weight, int weight_dtype,
+                                          int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
+                                          const float* bias, const float* residual, float* y, float* scratch,
+                                          void* stream) {
+    return linear_residual("skv_linear_residual_mm_f32", x, rows, weight, weight_dtype, stride_k, stride_n,
+                           in_dim, out_dim, bias, residual, y, stream, scratch, true);
 }

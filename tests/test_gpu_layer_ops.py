@@ -315,3 +315,102 @@ def test_rope_rows_cos_sin_equal_host_libm(gpu, hd):
         y = D.from_numpy(x[:1])
         gpu._check(lib.skv_rope_f32(y.ptr, 1, hd, p, None))
         assert np.array_equal(y.download(np.uint32, (1, hd))[0], got[p].view(np.uint32))
+
+
+def _mm_reference(W, B, x, gamma, ctx, act_in, res, dims, position, eps=1e-5):
+    """float64 restatement of the three projections of several tokens:
+    rmsnorm, W x + bias, RoPE at position + r with the device's float32
+    cos/sin (angle in double from the float32 inverse frequency), SwiGLU,
+    residual."""
+    H, Hq, Hkv, hd, inter = dims
+    w = {k: oracle.bf16_to_f32(W[k]).astype(np.float64) for k in "qkvogud"}
+    b = {k: (B[k].astype(np.float64) if B[k] is not None else 0.0) for k in "qkvogud"}
+    x = x.astype(np.float64)
+    xn = x / np.sqrt((x * x).mean(axis=1, keepdims=True) + eps) * gamma.astype(np.float64)
+    out = {k: xn @ w[k].T + b[k] for k in "qkv"}
+    if position >= 0:
+        half = hd // 2
+        inv = np.array([np.float32(10000.0 ** (-2.0 * i / hd)) for i in range(half)], np.float64)
+        ang = (position + np.arange(x.shape[0], dtype=np.float64))[:, None] * inv[None, :]
+        c, s = np.cos(ang).astype(np.float32).astype(np.float64), np.sin(ang).astype(np.float32).astype(np.float64)
+        for k, nh in (("q", Hq), ("k", Hkv)):
+            y = out[k].reshape(x.shape[0], nh, hd)
+            a0, b0 = y[:, :, :half].copy(), y[:, :, half:].copy()
+            y[:, :, :half] = a0 * c[:, None, :] - b0 * s[:, None, :]
+            y[:, :, half:] = a0 * s[:, None, :] + b0 * c[:, None, :]
+            out[k] = y.reshape(x.shape[0], nh * hd)
+    g, u = xn @ w["g"].T + b["g"], xn @ w["u"].T + b["u"]
+    out["act"] = g / (1.0 + np.exp(-g)) * u
+    out["o"] = ctx.astype(np.float64) @ w["o"].T + b["o"] + res
+    out["d"] = act_in.astype(np.float64) @ w["d"].T + b["d"] + res
+    return out
+
+
+@pytest.mark.parametrize("dims", [(2048, 32, 4, 64, 5632), (1024, 8, 2, 128, 1536)], ids=["tinyllama", "hd128"])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_mm_projections_match_float64(gpu, dims, with_bias):
+    """skv_*_mm_f32 (matrix cores, inputs split into bf16 hi + lo) against the
+    float64 restatement: every output within 1e-4 of its matrix's rms (a
+    dropped lo part errs by ~2e-3 relative, a wrong RoPE pair or token by
+    O(1)); tokens 1 .. 300 (partial 64-token tiles), RoPE positions up to
+    16,381 and none."""
+    H, Hq, Hkv, hd, inter = dims
+    rng = np.random.default_rng(H + inter + with_bias)
+    lib, D = gpu.lib(), gpu.DeviceBuffer
+    shapes = (("q", Hq * hd, H), ("k", Hkv * hd, H), ("v", Hkv * hd, H), ("o", H, Hq * hd),
+              ("g", inter, H), ("u", inter, H), ("d", H, inter))
+    W = {n: _bf16_rows(rng, o, i, 0.03) for n, o, i in shapes}
+    dW = {n: D.from_numpy(W[n]) for n, _, _ in shapes}
+    B = {n: (rng.standard_normal(o).astype(np.float32) if with_bias else None) for n, o, _ in shapes}
+    dB = {n: (D.from_numpy(B[n]) if B[n] is not None else None) for n, _, _ in shapes}
+    bp = lambda n: dB[n].ptr if dB[n] is not None else None
+    strides = (ctypes.c_int64 * 3)(H, H, H)
+    eps = ctypes.c_float(1e-5)
+    for n, position in ((1, 0), (16, 7), (37, 1000), (64, -1), (300, 16381)):
+        x = rng.standard_normal((n, H)).astype(np.float32)
+        gamma = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+        ctx = rng.standard_normal((n, Hq * hd)).astype(np.float32)
+        act_in = rng.standard_normal((n, inter)).astype(np.float32)
+        res = rng.standard_normal((n, H)).astype(np.float32)
+        dx, dg, dctx, dact, dres = (D.from_numpy(a) for a in (x, gamma, ctx, act_in, res))
+        sizes = {"q": Hq * hd, "k": Hkv * hd, "v": Hkv * hd, "act": inter, "o": H, "d": H}
+        out = {k: D(4 * n * m) for k, m in sizes.items()}
+        for buf in out.values():
+            buf.upload(np.full(buf.nbytes // 4, np.nan, np.float32))
+        scratch = D(4 * n * max(H, inter, Hq * hd))
+        gpu._check(lib.skv_fused_qkv_mm_f32(dx.ptr, n, dg.ptr, eps, dW["q"].ptr, dW["k"].ptr, dW["v"].ptr,
+                                            gpu.DTYPE_BF16, 1, strides, bp("q"), bp("k"), bp("v"), H, Hq, Hkv,
+                                            hd, position, out["q"].ptr, out["k"].ptr, out["v"].ptr, scratch.ptr,
+                                            None))
+        gpu._check(lib.skv_fused_gate_up_swiglu_mm_f32(dx.ptr, n, dg.ptr, eps, dW["g"].ptr, dW["u"].ptr,
+                                                       gpu.DTYPE_BF16, 1, H, H, bp("g"), bp("u"), H, inter,
+                                                       out["act"].ptr, scratch.ptr, None))
+        gpu._check(lib.skv_linear_residual_mm_f32(dctx.ptr, n, dW["o"].ptr, gpu.DTYPE_BF16, 1, Hq * hd, Hq * hd,
+                                                  H, bp("o"), dres.ptr, out["o"].ptr, scratch.ptr, None))
+        gpu._check(lib.skv_linear_residual_mm_f32(dact.ptr, n, dW["d"].ptr, gpu.DTYPE_BF16, 1, inter, inter, H,
+                                                  bp("d"), dres.ptr, out["d"].ptr, scratch.ptr, None))
+        gpu.synchronize()
+        ref = _mm_reference(W, B, x, gamma, ctx, act_in, res, dims, position)
+        for k, m in sizes.items():
+            got = out[k].download(np.float32, (n, m)).astype(np.float64)
+            err = np.abs(got - ref[k]).max()
+            bound = 1e-4 * np.sqrt((ref[k] ** 2).mean())
+            assert np.isfinite(got).all() and err <= bound, f"{k}: rows={n} position={position} err={err:.3g} bound={bound:.3g}"
+
+
+def test_mm_projections_refuse_unsupported_shapes(gpu):
+    """fp32 weights, in_dim not a multiple of 128, an output count not a
+    multiple of 32: SKV_ERR_UNSUPPORTED and nothing written."""
+    lib, D = gpu.lib(), gpu.DeviceBuffer
+    y = D.from_numpy(np.full((3, 64), 7.0, np.float32))
+    res = D.from_numpy(np.zeros((3, 64), np.float32))
+    for K, out_dim, dt in ((1024, 64, gpu.DTYPE_FP32), (1000, 64, gpu.DTYPE_BF16), (1024, 48, gpu.DTYPE_BF16)):
+        esz = 2 if dt == gpu.DTYPE_BF16 else 4
+        w = D(64 * K * esz)
+        x = D.from_numpy(np.ones((3, K), np.float32))
+        scratch = D(4 * 3 * K)
+        rc = lib.skv_linear_residual_mm_f32(x.ptr, 3, w.ptr, dt, 1, K, K, out_dim, None, res.ptr, y.ptr,
+                                            scratch.ptr, None)
+        assert rc == gpu.SKV_ERR_UNSUPPORTED, (K, out_dim, dt)
+    gpu.synchronize()
+    assert np.array_equal(y.download(np.float32, (3, 64)), np.full((3, 64), 7.0, np.float32))
