@@ -121,7 +121,6 @@ private:
     int prefill_rows_ = 0;
     std::optional<Tensor> pf_queries_, pf_keys_, pf_values_, pf_context_, pf_residual_, pf_act_;
     std::optional<Tensor> pf_normalized_, pf_up_, pf_down_;
-    std::optional<Tensor> pf_split_;  // bf16 hi/lo parts of a projection input (matrix-core path)
     std::optional<Tensor> pf_meta_;  // 4 int32: position, chunk offsets {0, n}, context length
 };
 

@@ -351,19 +351,18 @@ int skv_linear_residual_rows_f32(const float* x, int rows, const void* weight, i
                                  void* stream);
 
 /* The same three projections for `rows` tokens on the matrix cores, for long
- * prompts.  The inputs (normalised first with gamma, with the arithmetic of
- * skv_rmsnorm_f32) are split into bf16 hi = bf16(x) and lo = bf16(x - hi)
- * parts in `scratch` (rows * in_dim floats, 16-byte aligned, distinct from
- * every other buffer; its contents are overwritten), and each output is
- * W hi + W lo with fp32 accumulation: every product is exact and x keeps
+ * prompts.  With gamma, the inputs are first normalised into `normalized`
+ * (rows * in_dim floats, as in the rows variants).  Each input value v is
+ * split into bf16 parts hi = bf16(v) and lo = bf16(v - hi), and each output
+ * is W hi + W lo with fp32 accumulation: every product is exact and v keeps
  * ~16 significant bits, so the results agree with the one-token entry points
  * to fp32 rounding but are not bit-identical to them.  RoPE, bias, SwiGLU
  * and the residual are applied as in the rows variants (y may alias
  * residual).  SKV_ERR_UNSUPPORTED (nothing launched) unless the weights are
- * bf16 aligned output-major rows, in_dim is a multiple of 128 from 512 to 8,192,
- * every output count is a multiple of 32 (gate/up: 16), head_dim is a
- * multiple of 32 when rotating, and the outputs (and residual) are 16-byte
- * aligned.
+ * bf16 aligned output-major rows, in_dim is a multiple of 128 from 512 to
+ * 8,192, every output count is a multiple of 32 (gate/up: 16), head_dim is a
+ * multiple of 32 when rotating, and the input (the normalised rows with
+ * gamma), outputs and residual are 16-byte aligned.
  * Replaces: the same reference code as the rows variants
  * (src/models/transformer_block.cpp:300-332); no counterpart of its own. */
 int skv_fused_qkv_mm_f32(const float* hidden, int rows, const float* gamma, float epsilon,
@@ -371,17 +370,17 @@ int skv_fused_qkv_mm_f32(const float* hidden, int rows, const float* gamma, floa
                          int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
                          const float* bias_k, const float* bias_v, int hidden_dim,
                          int num_heads, int num_kv_heads, int head_dim, int first_position,
-                         float* q, float* k, float* v, float* scratch, void* stream);
+                         float* q, float* k, float* v, float* normalized, void* stream);
 int skv_fused_gate_up_swiglu_mm_f32(const float* x, int rows, const float* gamma, float epsilon,
                                     const void* w_gate, const void* w_up, int weight_dtype,
                                     int64_t stride_k, int64_t stride_n_gate,
                                     int64_t stride_n_up, const float* bias_gate,
                                     const float* bias_up, int in_dim, int out_dim,
-                                    float* act, float* scratch, void* stream);
+                                    float* act, float* normalized, void* stream);
 int skv_linear_residual_mm_f32(const float* x, int rows, const void* weight, int weight_dtype,
                                int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
                                const float* bias, const float* residual, float* y,
-                               float* scratch, void* stream);
+                               void* stream);
 
 /* ---- model boundary: checkpoint tensors, embedding, token choice --------
  * Checkpoint decode on the device (the host only moves file bytes).  src holds
@@ -410,6 +409,12 @@ int skv_check_finite(const void* src, int src_dtype, size_t count, int32_t* nonf
 int skv_embedding_f32(const void* table, int table_dtype, int vocab, int hidden,
                       const int32_t* token_ids, int index, float* out, int32_t* flags,
                       void* stream);
+/* The same for `rows` consecutive ids (a prompt): out[r][i] =
+ * table[token_ids[first_index + r] * hidden + i], r < rows <= 65,535, in one
+ * launch. */
+int skv_embedding_rows_f32(const void* table, int table_dtype, int vocab, int hidden,
+                           const int32_t* token_ids, int first_index, int rows, float* out,
+                           int32_t* flags, void* stream);
 
 /* token_ids[index] = the first index of the maximum of logits[0..n) (greedy,
  * src/generation/sampler.cpp:57-62).  A non-finite logit sets

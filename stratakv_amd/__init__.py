@@ -119,13 +119,14 @@ _PROTOS = {
     "skv_fused_gate_up_swiglu_mm_f32": (_i32, [_vp, _i32, _vp, _f32, _vp, _vp, _i32, _i64, _i64,
                                                _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
     "skv_linear_residual_mm_f32": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp,
-                                          _vp, _vp, _vp]),
+                                          _vp, _vp]),
     "skv_rope_rows_f32": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
     "skv_write_i32": (_i32, [_vp, _c.POINTER(_c.c_int32), _i32, _vp]),
     "skv_convert_to_bf16": (_i32, [_vp, _i32, _sz, _vp, _vp, _vp]),
     "skv_convert_to_f32": (_i32, [_vp, _i32, _sz, _vp, _vp, _vp]),
     "skv_check_finite": (_i32, [_vp, _i32, _sz, _vp, _vp]),
     "skv_embedding_f32": (_i32, [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "skv_embedding_rows_f32": (_i32, [_vp, _i32, _i32, _i32, _vp, _i32, _i32, _vp, _vp, _vp]),
     "skv_argmax_f32": (_i32, [_vp, _i32, _vp, _i32, _vp, _vp]),
     "skv_sample_f32": (_i32, [_vp, _i32, _f32, _i32, _f32, _c.c_double, _vp, _i32, _vp, _vp]),
 }
@@ -331,6 +332,12 @@ def embedding(table, table_dtype: int, vocab: int, hidden: int, token_ids, index
                                    _ptr(flags), stream))
 
 
+def embedding_rows(table, table_dtype: int, vocab: int, hidden: int, token_ids, first_index: int, rows: int, out,
+                   flags=None, stream=None) -> None:
+    _check(lib().skv_embedding_rows_f32(_ptr(table), table_dtype, vocab, hidden, _ptr(token_ids), first_index, rows,
+                                        _ptr(out), _ptr(flags), stream))
+
+
 def argmax(logits, n: int, token_ids, index: int, flags=None, stream=None) -> None:
     _check(lib().skv_argmax_f32(_ptr(logits), n, _ptr(token_ids), index, _ptr(flags), stream))
 
@@ -392,5 +399,5 @@ __all__ = [
     "header_symbols", "lib", "device_count", "require_gpu", "synchronize", "DeviceBuffer",
     "fill_normal_bf16", "kv_append", "decode_workspace_bytes", "paged_decode",
     "paged_attention_decode", "gather_blocks", "Event", "Stream", "convert_to_bf16", "convert_to_f32",
-    "check_finite", "embedding", "argmax", "sample",
+    "check_finite", "embedding", "embedding_rows", "argmax", "sample",
 ]

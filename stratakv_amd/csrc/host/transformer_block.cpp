@@ -278,7 +278,6 @@ void TransformerBlock::ensure_prefill_workspace(int rows) {
     make(pf_normalized_, hidden_dim_);
     make(pf_up_, inter);
     make(pf_down_, hidden_dim_);
-    make(pf_split_, std::max({static_cast<std::size_t>(hidden_dim_), q_dim, inter}));
     if (!pf_meta_) pf_meta_.emplace(std::vector<std::size_t>{4}, DataType::FP32, Device::GPU);
     prefill_rows_ = rows;
 }
@@ -354,7 +353,6 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
     float* ctx = fp(*pf_context_);
     float* h = fp(*pf_residual_);
     float* act = fp(*pf_act_);
-    float* split = fp(*pf_split_);
     auto* meta = static_cast<std::int32_t*>(pf_meta_->raw_data());
 
     for (int c0 = 0; c0 < tokens; c0 += kPrefillChunk) {
@@ -379,7 +377,7 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                          bias_of(wv), hidden, num_heads, num_kv_heads, head_dim, p0, q, k, v, scratch, s);
         };
         if (!(same_dtype &&
-              ((mm && fused(qkv(skv_fused_qkv_mm_f32, split), "prefill_into: q/k/v on the matrix cores")) ||
+              ((mm && fused(qkv(skv_fused_qkv_mm_f32, fp(*pf_normalized_)), "prefill_into: q/k/v on the matrix cores")) ||
                fused(qkv(skv_fused_qkv_rows_f32, fp(*pf_normalized_)), "prefill_into: fused rmsnorm + q/k/v + rope")))) {
             float* xn = fp(*pf_normalized_);
             detail::check(skv_rmsnorm_f32(x, xn, cfp(norm1_.gamma()), n, hidden, norm1_.epsilon(), s),
@@ -406,7 +404,7 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
 
         // o_proj + residual (reads x before y is written: aliasing-safe).
         if (!((mm && fused(skv_linear_residual_mm_f32(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
-                                                      stride_n(wo), q_dim, hidden, bias_of(wo), x, h, split, s),
+                                                      stride_n(wo), q_dim, hidden, bias_of(wo), x, h, s),
                            "prefill_into: o_proj on the matrix cores")) ||
               fused(skv_linear_residual_rows_f32(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
                                                  stride_n(wo), q_dim, hidden, bias_of(wo), x, h, s),
@@ -421,7 +419,7 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                          stride_n(up_proj_), bias_of(gate_proj_), bias_of(up_proj_), hidden, inter, act, scratch, s);
         };
         if (!(ffn_same &&
-              ((mm && fused(gate_up(skv_fused_gate_up_swiglu_mm_f32, split),
+              ((mm && fused(gate_up(skv_fused_gate_up_swiglu_mm_f32, fp(*pf_normalized_)),
                             "prefill_into: gate/up on the matrix cores")) ||
                fused(gate_up(skv_fused_gate_up_swiglu_rows_f32, fp(*pf_normalized_)),
                      "prefill_into: fused rmsnorm + gate/up + swiglu")))) {
@@ -436,7 +434,7 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
         // down_proj + residual into the output rows.
         if (!((mm && fused(skv_linear_residual_mm_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
                                                       stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
-                                                      bias_of(down_proj_), h, y, split, s),
+                                                      bias_of(down_proj_), h, y, s),
                            "prefill_into: down_proj on the matrix cores")) ||
               fused(skv_linear_residual_rows_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
                                                  stride_k(down_proj_), stride_n(down_proj_), inter, hidden,

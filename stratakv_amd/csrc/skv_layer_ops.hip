@@ -738,49 +738,25 @@ int launch_fused_rows(const FusedGemv& f, bool bf16, int items, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Matrix-core projections of a block of tokens (long prompts).  The input
-// rows (fp32, normalised first when gamma is given, with rmsnorm_kernel's
-// arithmetic) are split once into two bf16 planes, hi = bf16(x) and
-// lo = bf16(x - hi), so that W x = W hi + W lo on v_mfma_f32_16x16x32_bf16
-// with fp32 accumulation: every product of a bf16 weight with a part is exact
-// and x is carried to ~16 significant bits, close to the fp32 dot products
-// of the one-token kernels (not bit-identical to them: the summation order
-// differs).
-//
-// split_rows_kernel: one workgroup per row; the planes go to the caller's
-// scratch of rows * K floats (hi plane, then lo plane, rows * K bf16 each).
+// Matrix-core projections of a block of tokens (long prompts).  Each input
+// value v (the rmsnorm_kernel output when gamma is given) is split into bf16
+// parts hi = bf16(v) and lo = bf16(v - hi), so that W v = W hi + W lo on
+// v_mfma_f32_16x16x32_bf16 with fp32 accumulation: every product of a bf16
+// weight with a part is exact and v keeps ~16 significant bits, close to the
+// fp32 dot products of the one-token kernels (not bit-identical to them: the
+// summation order differs).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ in,
-                                                         const float* __restrict__ gamma, int n, float eps,
-                                                         uint16_t* __restrict__ hi, uint16_t* __restrict__ lo) {
-    extern __shared__ float xg_s[];  // [2][n]: the row and gamma
-    __shared__ float red[4];
-    const int64_t row = blockIdx.x;
-    const float* x = in + row * n;
-    stage_to_lds(x, xg_s, n);
-    if (gamma != nullptr) stage_to_lds(gamma, xg_s + n, n);
-    __syncthreads();
-    float inv = 1.0f;
-    if (gamma != nullptr) inv = rms_inverse([&](int i) { return xg_s[i]; }, n, eps, red);
-    for (int i = threadIdx.x; i < n; i += 256) {
-        const float v = gamma != nullptr ? xg_s[i] * inv * xg_s[n + i] : xg_s[i];
-        const __bf16 h = static_cast<__bf16>(v);
-        const __bf16 l = static_cast<__bf16>(v - static_cast<float>(h));
-        hi[row * n + i] = __builtin_bit_cast(uint16_t, h);
-        lo[row * n + i] = __builtin_bit_cast(uint16_t, l);
-    }
-}
-
 typedef __bf16 mm_bf16x8_t __attribute__((ext_vector_type(8)));
 typedef uint32_t mm_u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kMmTokens = 64;   // tokens per workgroup (4 column tiles of 16)
-constexpr int kMmSplitK = 4;    // wavefronts per workgroup, each a quarter of K
+constexpr int kMmTokens = 64;                      // tokens per workgroup (4 column tiles of 16)
+constexpr int kMmWaves = 4;                        // wavefronts per workgroup, one feature group each
+constexpr int kMmStageK = 64;                      // k per LDS stage (two 32-wide MFMA steps)
+constexpr int kMmRowBytes = kMmStageK * 2 + 16;    // one token's stage in LDS (bf16, padded)
+constexpr int kMmRing = 2;                         // stages of operands in flight
 
 struct MmArgs {
     FusedGemv f;
-    const uint16_t* x_hi;       // [rows][K] bf16 planes of the input
-    const uint16_t* x_lo;
     int groups;                 // 32-feature groups
     int token_tiles;            // cdiv(rows, kMmTokens)
 };
@@ -818,107 +794,158 @@ __device__ __forceinline__ MmGroup mm_group(const FusedGemv& f, int g) {
     return q;
 }
 
-// One workgroup = one feature group x kMmTokens tokens.  Wavefront w computes
-// the 32 x 64 tile over k in [w K/4, (w + 1) K/4) with operands loaded
-// straight from global memory in the MFMA layouts (lane (t, j): A = weight
-// row t of a tile, k chunk 8j..8j+7; B = token t of a column tile, the same
-// chunk), RING k-steps ahead (RING divides the wavefront's step count, so
-// the loop has no branch around a load and never waits for all of them); the
-// four partial tiles are summed through LDS in a fixed order and wavefront 0
-// applies the epilogue.  Output lane layout: acc[a][c][i] = feature (tile a)
-// 4j + i, token 16c + t.
-template <int MODE, int RING>
-__global__ __launch_bounds__(64 * kMmSplitK) void proj_mm_kernel(MmArgs args) {
+// One workgroup = kMmWaves / KS feature groups x kMmTokens tokens, K split
+// into KS parts (KS = 2 when the grid would be too small to fill the chip):
+// wavefront w computes group w % (kMmWaves / KS) over part w / (kMmWaves / KS)
+// and the parts are summed through LDS in a fixed order.  The inputs go
+// through LDS in stages of kMmStageK per part: each thread loads 16
+// consecutive fp32 of one token per part, splits them into hi and lo parts
+// and stores them (two LDS buffers, one barrier per stage); a wavefront reads
+// them in the MFMA B layout (lane (t, j): token t of a column tile, k chunk
+// 8j..8j+7) and its weight rows straight from global memory in the A layout
+// (row t of a tile, the same chunk).  Inputs and weights are requested
+// kMmRing stages ahead, the inputs of a stage after its weights, so that each
+// wait in issue order covers exactly the stage it needs.  Output lane layout:
+// acc[a][c][i] = feature (tile a) 4j + i, token 16c + t.
+constexpr int kMmPartBytes = 2 * kMmTokens * kMmRowBytes;   // hi + lo of one part's stage
+
+template <int MODE, int KS>
+__global__ __launch_bounds__(64 * kMmWaves) void proj_mm_kernel(MmArgs args) {
+    constexpr int GPW = kMmWaves / KS;   // feature groups per workgroup
     const FusedGemv& f = args.f;
-    __shared__ f32x4_t part[kMmSplitK - 1][8][64];
-    const int lane = threadIdx.x & 63, t = lane & 15, j = lane >> 4;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    extern __shared__ __align__(16) unsigned char xs[];   // [buffer][part][hi, lo][token]
+    auto xs_at = [&](int buf, int part, int half) { return xs + ((buf * KS + part) * 2 + half) * (kMmPartBytes / 2); };
+    const int tid = threadIdx.x, lane = tid & 63, t = lane & 15, j = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int part = w / GPW;
     // Workgroups are dealt to the 8 XCDs round-robin: the token tiles of one
-    // feature group go to the same XCD, one after another, so its weight rows
+    // feature tile go to the same XCD, one after another, so its weight rows
     // are read from HBM once and then from that XCD's L2.
     const int id = blockIdx.x, xcd = id & 7, local = id >> 3;
-    const int g = (local / args.token_tiles) * 8 + xcd;
+    const int ftile = (local / args.token_tiles) * 8 + xcd;
     const int tile = local % args.token_tiles;
-    if (g >= args.groups) return;
-    const MmGroup grp = mm_group<MODE>(f, g);
-    const int K = f.K, rows = f.rows;
-    const int ksteps = K / 32 / kMmSplitK, kbase = w * ksteps * 32;
+    if (ftile * GPW >= args.groups) return;      // the whole workgroup, before any barrier
+    const int g = ftile * GPW + w % GPW;
+    const bool live = g < args.groups;           // a wave past the last group stores nothing
+    const MmGroup grp = mm_group<MODE>(f, min(g, args.groups - 1));
+    const int K = f.K, rows = f.rows, nst = K / kMmStageK / KS;   // stages per part
     const int tok0 = tile * kMmTokens;
 
+    // Staging: thread -> token tid / 4, k (tid % 4) * 16 .. + 15 of a stage.
+    const int st_tok = tid >> 2, st_k = (tid & 3) * 16;
+    const float* xrow = f.x + static_cast<int64_t>(min(tok0 + st_tok, rows - 1)) * K + st_k;
+    // Weight rows of this wavefront's two tiles.
     const int mb = MODE == FUSED_GATE_UP ? 1 : grp.m;
     const char* wa = static_cast<const char*>(f.w[grp.m]) + static_cast<int64_t>(grp.r0 + t) * f.row_bytes[grp.m];
     const char* wb = static_cast<const char*>(f.w[mb]) + static_cast<int64_t>(grp.r1 + t) * f.row_bytes[mb];
-    const uint16_t* xh[4];
-    const uint16_t* xl[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int64_t tok = min(tok0 + 16 * c + t, rows - 1);
-        xh[c] = args.x_hi + tok * K;
-        xl[c] = args.x_lo + tok * K;
-    }
 
-    struct Ops {
-        mm_u32x4_t a[2], h[4], l[4];
+    struct Stage {
+        mm_u32x4_t wop[2][2];   // [k-step][tile] weight operands of this wavefront's part
+        f32x4_t x[KS][4];       // this thread's 16 staged inputs of every part
     };
-    auto load = [&](int s, Ops& o) __attribute__((always_inline)) {
-        const int k = kbase + 32 * s + 8 * j;
-        o.a[0] = *reinterpret_cast<const mm_u32x4_t*>(wa + 2 * k);
-        o.a[1] = *reinterpret_cast<const mm_u32x4_t*>(wb + 2 * k);
+    auto load = [&](int s, Stage& o) __attribute__((always_inline)) {
+        s = min(s, nst - 1);    // past the end: the last stage again (in bounds, unused)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            o.h[c] = *reinterpret_cast<const mm_u32x4_t*>(xh[c] + k);
-            o.l[c] = *reinterpret_cast<const mm_u32x4_t*>(xl[c] + k);
+        for (int ks = 0; ks < 2; ++ks) {
+            const int k = (part * nst + s) * kMmStageK + ks * 32 + 8 * j;
+            o.wop[ks][0] = *reinterpret_cast<const mm_u32x4_t*>(wa + 2 * k);
+            o.wop[ks][1] = *reinterpret_cast<const mm_u32x4_t*>(wb + 2 * k);
+        }
+#pragma unroll
+        for (int q = 0; q < KS; ++q)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                o.x[q][r] = reinterpret_cast<const f32x4_t*>(xrow + (q * nst + s) * kMmStageK)[r];
+    };
+    auto stage_inputs = [&](int buf, const Stage& o) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < KS; ++q) {
+            uint32_t hw[8], lw[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v0 = o.x[q][e >> 1][2 * (e & 1)], v1 = o.x[q][e >> 1][2 * (e & 1) + 1];
+                const __bf16 h0 = static_cast<__bf16>(v0), h1 = static_cast<__bf16>(v1);
+                const __bf16 l0 = static_cast<__bf16>(v0 - static_cast<float>(h0));
+                const __bf16 l1 = static_cast<__bf16>(v1 - static_cast<float>(h1));
+                hw[e] = __builtin_bit_cast(uint16_t, h0) |
+                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+                lw[e] = __builtin_bit_cast(uint16_t, l0) |
+                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
+            }
+            unsigned char* dh = xs_at(buf, q, 0) + st_tok * kMmRowBytes + st_k * 2;
+            unsigned char* dl = xs_at(buf, q, 1) + st_tok * kMmRowBytes + st_k * 2;
+            reinterpret_cast<mm_u32x4_t*>(dh)[0] = mm_u32x4_t{hw[0], hw[1], hw[2], hw[3]};
+            reinterpret_cast<mm_u32x4_t*>(dh)[1] = mm_u32x4_t{hw[4], hw[5], hw[6], hw[7]};
+            reinterpret_cast<mm_u32x4_t*>(dl)[0] = mm_u32x4_t{lw[0], lw[1], lw[2], lw[3]};
+            reinterpret_cast<mm_u32x4_t*>(dl)[1] = mm_u32x4_t{lw[4], lw[5], lw[6], lw[7]};
         }
     };
+
     f32x4_t acc[2][4];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[a][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    auto mfma = [&](const Ops& o) __attribute__((always_inline)) {
+    auto compute = [&](int buf, const Stage& o) __attribute__((always_inline)) {
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int ks = 0; ks < 2; ++ks) {
+            mm_u32x4_t bh[4], bl[4];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const mm_bf16x8_t av = __builtin_bit_cast(mm_bf16x8_t, o.a[a]);
-                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(mm_bf16x8_t, o.h[c]),
-                                                                    acc[a][c], 0, 0, 0);
-                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(mm_bf16x8_t, o.l[c]),
-                                                                    acc[a][c], 0, 0, 0);
+                const int off = (16 * c + t) * kMmRowBytes + (ks * 32 + 8 * j) * 2;
+                bh[c] = *reinterpret_cast<const mm_u32x4_t*>(xs_at(buf, part, 0) + off);
+                bl[c] = *reinterpret_cast<const mm_u32x4_t*>(xs_at(buf, part, 1) + off);
             }
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const mm_bf16x8_t av = __builtin_bit_cast(mm_bf16x8_t, o.wop[ks][a]);
+                    acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(mm_bf16x8_t, bh[c]),
+                                                                        acc[a][c], 0, 0, 0);
+                    acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(mm_bf16x8_t, bl[c]),
+                                                                        acc[a][c], 0, 0, 0);
+                }
+        }
     };
-    // Steps 0 .. RING - 1 loaded up front; each later step's operands are
-    // loaded when its ring slot is consumed; the last RING steps load nothing.
-    Ops ring[RING];
+
+    // Ring: slot u holds stage s0 + u (weights for the compute of that stage,
+    // inputs for its staging one stage earlier).  Stage 0's inputs are staged
+    // before the loop; the loop computes stage s, then stages s + 1.
+    Stage ring[kMmRing];
 #pragma unroll
-    for (int u = 0; u < RING; ++u) load(u, ring[u]);
-    for (int s0 = 0; s0 < ksteps - RING; s0 += RING) {
+    for (int u = 0; u < kMmRing; ++u) load(u, ring[u]);
+    stage_inputs(0, ring[0]);
+    __syncthreads();
+    for (int s0 = 0; s0 < nst; s0 += kMmRing) {   // nst is a multiple of kMmRing
 #pragma unroll
-        for (int u = 0; u < RING; ++u) {
-            const Ops o = ring[u];
-            load(s0 + u + RING, ring[u]);
-            __builtin_amdgcn_sched_barrier(0);   // issue order kept: the loads stay RING steps ahead
-            mfma(o);
+        for (int u = 0; u < kMmRing; ++u) {
+            const int s = s0 + u;
+            compute(s & 1, ring[u]);
+            load(s + kMmRing, ring[u]);
+            __builtin_amdgcn_sched_barrier(0);   // issue order kept: the loads stay kMmRing stages ahead
+            stage_inputs((s + 1) & 1, ring[(u + 1) % kMmRing]);
+            __syncthreads();
         }
     }
+    if constexpr (KS == 2) {
+        // Part 1's sums into LDS (the staging buffers are idle after the
+        // last barrier), then part 0 adds them: part 0 + part 1.
+        f32x4_t* red = reinterpret_cast<f32x4_t*>(xs) + (w % GPW) * 8 * 64;
+        if (part == 1) {
 #pragma unroll
-    for (int u = 0; u < RING; ++u) mfma(ring[u]);
-
-    // Sum of the K quarters in the order 0 + 1 + 2 + 3.
-    if (w > 0) {
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) red[(4 * a + c) * 64 + lane] = acc[a][c];
+        }
+        __syncthreads();
+        if (part == 1) return;
 #pragma unroll
         for (int a = 0; a < 2; ++a)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) part[w - 1][4 * a + c][lane] = acc[a][c];
+            for (int c = 0; c < 4; ++c) acc[a][c] += red[(4 * a + c) * 64 + lane];
     }
-    __syncthreads();
-    if (w > 0) return;
-#pragma unroll
-    for (int q = 0; q < kMmSplitK - 1; ++q)
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) acc[a][c] += part[q][4 * a + c][lane];
+    if (!live) return;
 
     auto bias4 = [&](int m, int r) {
         const float* b = f.bias[m];
@@ -961,11 +988,11 @@ __global__ __launch_bounds__(64 * kMmSplitK) void proj_mm_kernel(MmArgs args) {
 }
 
 // Shapes the matrix-core projections take: bf16 weights in 16-byte aligned
-// output-major rows, K a multiple of 128 (32-wide k-steps split four ways),
-// every matrix's output count a multiple of 32 (16 for gate/up), and for
-// RoPE head_dim a multiple of 32.
+// output-major rows, K a multiple of 128 (stages of 64 in pairs), every
+// matrix's output count a multiple of 32 (16 for gate/up), a 16-byte aligned
+// input, and for RoPE head_dim a multiple of 32.
 bool mm_supported(const FusedGemv& f, int nmat, int esz, int64_t stride_k) {
-    if (esz != 2 || stride_k != 1 || f.K < 128 || f.K % 128 != 0) return false;
+    if (esz != 2 || stride_k != 1 || f.K < 128 || f.K % 128 != 0 || !aligned16(f.x)) return false;
     for (int m = 0; m < nmat; ++m)
         if (f.w[m] == nullptr || !aligned16(f.w[m]) || f.row_bytes[m] % 16 != 0 || f.row_bytes[m] < 2 * f.K ||
             f.n[m] % 16 != 0 || (nmat != 2 && f.n[m] % 32 != 0))
@@ -973,24 +1000,27 @@ bool mm_supported(const FusedGemv& f, int nmat, int esz, int64_t stride_k) {
     return true;
 }
 
-// Splits x (normalised when gamma != nullptr) into the scratch planes and
-// launches proj_mm_kernel over `groups` feature groups.
+// Launches proj_mm_kernel over `groups` feature groups (f.x already
+// normalised when the projection normalises).
+// K is split in two (twice the workgroups, half the stages each) when the
+// whole-K grid would give fewer than 256 workgroups and K is a multiple of 256.
 template <int MODE>
-int launch_mm(FusedGemv f, int groups, const float* gamma, float eps, float* scratch, hipStream_t s) {
-    const int64_t elems = static_cast<int64_t>(f.rows) * f.K;
-    uint16_t* hi = reinterpret_cast<uint16_t*>(scratch);
-    uint16_t* lo = hi + elems;
-    split_rows_kernel<<<f.rows, 256, 2 * sizeof(float) * f.K, s>>>(f.x, gamma, f.K, eps, hi, lo);
-    if (int rc = check_launch("split_rows_kernel")) return rc;
-    MmArgs a{f, hi, lo, groups, cdiv(f.rows, kMmTokens)};
-    const int64_t wgs = static_cast<int64_t>(cdiv(groups, 8)) * 8 * a.token_tiles;
-    SKV_REQUIRE(wgs <= INT32_MAX, "proj_mm_kernel: grid of %lld workgroups is too large", static_cast<long long>(wgs));
-    const int ksteps = f.K / 32 / kMmSplitK;
-    const dim3 grid(static_cast<unsigned>(wgs)), block(64 * kMmSplitK);
-    // Two k-steps in flight (a deeper ring runs out of registers).
-    if (ksteps % 2 == 0) proj_mm_kernel<MODE, 2><<<grid, block, 0, s>>>(a);
-    else proj_mm_kernel<MODE, 1><<<grid, block, 0, s>>>(a);
-    return check_launch("proj_mm_kernel");
+int launch_mm(const FusedGemv& f, int groups, hipStream_t s) {
+    MmArgs a{f, groups, cdiv(f.rows, kMmTokens)};
+    auto grid_of = [&](int gpw) { return static_cast<int64_t>(cdiv(cdiv(groups, gpw), 8)) * 8 * a.token_tiles; };
+    auto go = [&](auto kern, int ks) {
+        const int64_t wgs = grid_of(kMmWaves / ks);
+        SKV_REQUIRE(wgs <= INT32_MAX, "proj_mm_kernel: grid of %lld workgroups is too large",
+                    static_cast<long long>(wgs));
+        const size_t lds = 2 * static_cast<size_t>(ks) * kMmPartBytes;
+        const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (attr != hipSuccess) return set_error(SKV_ERR_HIP, "proj_mm_kernel: %s", hipGetErrorString(attr));
+        kern<<<static_cast<unsigned>(wgs), 64 * kMmWaves, lds, s>>>(a);
+        return check_launch("proj_mm_kernel");
+    };
+    if (grid_of(kMmWaves) < 256 && f.K % 256 == 0) return go(proj_mm_kernel<MODE, 2>, 2);
+    return go(proj_mm_kernel<MODE, 1>, 1);
 }
 
 }  // namespace skv
@@ -1142,15 +1172,18 @@ int fused_qkv(const char* fn, const float* hidden, int rows, const float* gamma,
     const int items = (ns[0] + ns[1] + ns[2]) / 2;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (mm) {
-        SKV_REQUIRE(normalized != nullptr && aligned16(normalized), "%s: 16-byte aligned scratch required", fn);
-        if (!mm_supported(f, 3, esz, stride_k) || (position >= 0 && head_dim % 32 != 0) || !aligned16(q) ||
+        if (gamma != nullptr) SKV_REQUIRE(normalized != nullptr, "%s: normalized scratch required with gamma", fn);
+        FusedGemv fx = f;
+        fx.x = gamma != nullptr ? normalized : hidden;
+        if (!mm_supported(fx, 3, esz, stride_k) || (position >= 0 && head_dim % 32 != 0) || !aligned16(q) ||
             !aligned16(k) || !aligned16(v))
             return set_error(SKV_ERR_UNSUPPORTED,
                              "%s: needs bf16 weights, hidden_dim a multiple of 128, outputs and head_dim multiples "
-                             "of 32 and 16-byte aligned outputs", fn);
+                             "of 32 and 16-byte aligned input and outputs", fn);
         if (position >= 0) f.rope = rope_inv_freq(head_dim);
+        if (int rc = normalize_rows(fn, f.x, rows, gamma, epsilon, hidden_dim, normalized, s)) return rc;
         f.gamma = nullptr;
-        return launch_mm<FUSED_QKV>(f, (ns[0] + ns[1] + ns[2]) / 32, gamma, epsilon, normalized, s);
+        return launch_mm<FUSED_QKV>(f, (ns[0] + ns[1] + ns[2]) / 32, s);
     }
     if (rows == 1) {
         if (position >= 0) f.rope = rope_table(head_dim, position);
@@ -1194,13 +1227,16 @@ int fused_gate_up(const char* fn, const float* x, int rows, const float* gamma, 
     f.y[0] = act;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (mm) {
-        SKV_REQUIRE(normalized != nullptr && aligned16(normalized), "%s: 16-byte aligned scratch required", fn);
-        if (!mm_supported(f, 2, esz, stride_k) || !aligned16(act))
+        if (gamma != nullptr) SKV_REQUIRE(normalized != nullptr, "%s: normalized scratch required with gamma", fn);
+        FusedGemv fx = f;
+        fx.x = gamma != nullptr ? normalized : x;
+        if (!mm_supported(fx, 2, esz, stride_k) || !aligned16(act))
             return set_error(SKV_ERR_UNSUPPORTED,
-                             "%s: needs bf16 weights, in_dim a multiple of 128, out_dim a multiple of 16 and a "
-                             "16-byte aligned output", fn);
+                             "%s: needs bf16 weights, in_dim a multiple of 128, out_dim a multiple of 16 and "
+                             "16-byte aligned input and output", fn);
+        if (int rc = normalize_rows(fn, f.x, rows, gamma, epsilon, in_dim, normalized, s)) return rc;
         f.gamma = nullptr;
-        return launch_mm<FUSED_GATE_UP>(f, out_dim / 16, gamma, epsilon, normalized, s);
+        return launch_mm<FUSED_GATE_UP>(f, out_dim / 16, s);
     }
     if (rows == 1) return launch_fused<FUSED_GATE_UP>(f, esz == 2, out_dim, s);
     if (!rows_supported(esz == 2, in_dim))
@@ -1212,7 +1248,7 @@ int fused_gate_up(const char* fn, const float* x, int rows, const float* gamma, 
 
 int linear_residual(const char* fn, const float* x, int rows, const void* weight, int weight_dtype,
                     int64_t stride_k, int64_t stride_n, int in_dim, int out_dim, const float* bias,
-                    const float* residual, float* y, void* stream, float* scratch = nullptr, bool mm = false) {
+                    const float* residual, float* y, void* stream, bool mm = false) {
     SKV_REQUIRE(x && residual && y && rows > 0 && in_dim > 0 && out_dim > 0, "%s: invalid pointers or sizes",
                 fn);
     SKV_REQUIRE(weight_dtype == SKV_DTYPE_BF16 || weight_dtype == SKV_DTYPE_FP32,
@@ -1235,12 +1271,11 @@ int linear_residual(const char* fn, const float* x, int rows, const void* weight
     f.residual = residual;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (mm) {
-        SKV_REQUIRE(scratch != nullptr && aligned16(scratch), "%s: 16-byte aligned scratch required", fn);
         if (!mm_supported(f, 1, esz, stride_k) || !aligned16(y) || !aligned16(residual))
             return set_error(SKV_ERR_UNSUPPORTED,
                              "%s: needs bf16 weights, in_dim a multiple of 128, out_dim a multiple of 32 and "
-                             "16-byte aligned residual and output", fn);
-        return launch_mm<FUSED_RESIDUAL>(f, out_dim / 32, nullptr, 0.0f, scratch, s);
+                             "16-byte aligned input, residual and output", fn);
+        return launch_mm<FUSED_RESIDUAL>(f, out_dim / 32, s);
     }
     if (rows == 1) return launch_fused<FUSED_RESIDUAL>(f, esz == 2, cdiv(out_dim, 2), s);
     return launch_fused_rows<FUSED_RESIDUAL>(f, esz == 2, cdiv(out_dim, 2), s);
@@ -1313,26 +1348,25 @@ extern "C" int skv_fused_qkv_mm_f32(const float* hidden, int rows, const float* 
                                     int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
                                     const float* bias_k, const float* bias_v, int hidden_dim, int num_heads,
                                     int num_kv_heads, int head_dim, int first_position, float* q, float* k,
-                                    float* v, float* scratch, void* stream) {
+                                    float* v, float* normalized, void* stream) {
     return fused_qkv("skv_fused_qkv_mm_f32", hidden, rows, gamma, epsilon, wq, wk, wv, weight_dtype, stride_k,
                      stride_n, bias_q, bias_k, bias_v, hidden_dim, num_heads, num_kv_heads, head_dim,
-                     first_position, q, k, v, scratch, stream, true);
+                     first_position, q, k, v, normalized, stream, true);
 }
 
 extern "C" int skv_fused_gate_up_swiglu_mm_f32(const float* x, int rows, const float* gamma, float epsilon,
                                                const void* w_gate, const void* w_up, int weight_dtype,
                                                int64_t stride_k, int64_t stride_n_gate, int64_t stride_n_up,
                                                const float* bias_gate, const float* bias_up, int in_dim,
-                                               int out_dim, float* act, float* scratch, void* stream) {
+                                               int out_dim, float* act, float* normalized, void* stream) {
     return fused_gate_up("skv_fused_gate_up_swiglu_mm_f32", x, rows, gamma, epsilon, w_gate, w_up, weight_dtype,
-                         stride_k, stride_n_gate, stride_n_up, bias_gate, bias_up, in_dim, out_dim, act, scratch,
+                         stride_k, stride_n_gate, stride_n_up, bias_gate, bias_up, in_dim, out_dim, act, normalized,
                          stream, true);
 }
 
 extern "C" int skv_linear_residual_mm_f32(const float* x, int rows, const void* weight, int weight_dtype,
                                           int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
-                                          const float* bias, const float* residual, float* y, float* scratch,
-                                          void* stream) {
+                                          const float* bias, const float* residual, float* y, void* stream) {
     return linear_residual("skv_linear_residual_mm_f32", x, rows, weight, weight_dtype, stride_k, stride_n,
-                           in_dim, out_dim, bias, residual, y, stream, scratch, true);
+                           in_dim, out_dim, bias, residual, y, stream, true);
 }

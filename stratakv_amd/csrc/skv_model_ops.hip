@@ -81,10 +81,12 @@ int launch_convert(const void* src, int src_dtype, size_t count, void* dst, int 
 // Embedding lookup: out[i] = table[ids[index] * hidden + i] widened to fp32.
 // An id outside [0, vocab) gives zeros and sets bit SKV_FLAG_BAD_TOKEN.
 // ---------------------------------------------------------------------------
+// Row blockIdx.y: out[y][i] = table[ids[index + y]][i].
 __global__ void embedding_kernel(const void* __restrict__ table, int dtype, int vocab, int hidden,
                                  const int32_t* __restrict__ ids, int index, float* __restrict__ out,
                                  int32_t* __restrict__ flags) {
-    const int id = ids[index];
+    const int id = ids[index + static_cast<int>(blockIdx.y)];
+    out += static_cast<size_t>(blockIdx.y) * static_cast<size_t>(hidden);
     const bool ok = id >= 0 && id < vocab;
     if (!ok && threadIdx.x == 0 && blockIdx.x == 0 && flags != nullptr) atomicOr(flags, SKV_FLAG_BAD_TOKEN);
     const size_t row = static_cast<size_t>(ok ? id : 0) * static_cast<size_t>(hidden);
@@ -581,17 +583,34 @@ extern "C" int skv_check_finite(const void* src, int src_dtype, size_t count, in
     return launch_convert(src, src_dtype, count, nullptr, 0, nonfinite, stream, "skv_check_finite");
 }
 
+namespace {
+int embedding_rows(const char* fn, const void* table, int table_dtype, int vocab, int hidden,
+                   const int32_t* token_ids, int first_index, int rows, float* out, int32_t* flags, void* stream) {
+    SKV_REQUIRE(table && token_ids && out, "%s: NULL pointer", fn);
+    SKV_REQUIRE(table_dtype == SKV_DTYPE_BF16 || table_dtype == SKV_DTYPE_FP32 || table_dtype == SKV_DTYPE_F16,
+                "%s: unknown table dtype %d", fn, table_dtype);
+    SKV_REQUIRE(vocab > 0 && hidden > 0 && first_index >= 0 && rows > 0 && rows <= 65535 &&
+                    first_index <= INT32_MAX - rows,
+                "%s: invalid dimensions", fn);
+    const dim3 grid(static_cast<unsigned>(std::min(cdiv(hidden, 256), 64)), static_cast<unsigned>(rows));
+    embedding_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(table, table_dtype, vocab, hidden,
+                                                                         token_ids, first_index, out, flags);
+    return check_launch(fn);
+}
+}  // namespace
+
 extern "C" int skv_embedding_f32(const void* table, int table_dtype, int vocab, int hidden,
                                  const int32_t* token_ids, int index, float* out, int32_t* flags,
                                  void* stream) {
-    SKV_REQUIRE(table && token_ids && out, "skv_embedding_f32: NULL pointer");
-    SKV_REQUIRE(table_dtype == SKV_DTYPE_BF16 || table_dtype == SKV_DTYPE_FP32 || table_dtype == SKV_DTYPE_F16,
-                "skv_embedding_f32: unknown table dtype %d", table_dtype);
-    SKV_REQUIRE(vocab > 0 && hidden > 0 && index >= 0, "skv_embedding_f32: invalid dimensions");
-    const unsigned blocks = static_cast<unsigned>(std::min(cdiv(hidden, 256), 64));
-    embedding_kernel<<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(table, table_dtype, vocab, hidden,
-                                                                           token_ids, index, out, flags);
-    return check_launch("skv_embedding_f32");
+    return embedding_rows("skv_embedding_f32", table, table_dtype, vocab, hidden, token_ids, index, 1, out, flags,
+                          stream);
+}
+
+extern "C" int skv_embedding_rows_f32(const void* table, int table_dtype, int vocab, int hidden,
+                                      const int32_t* token_ids, int first_index, int rows, float* out,
+                                      int32_t* flags, void* stream) {
+    return embedding_rows("skv_embedding_rows_f32", table, table_dtype, vocab, hidden, token_ids, first_index, rows,
+                          out, flags, stream);
 }
 
 namespace {

@@ -377,7 +377,7 @@ def test_mm_projections_match_float64(gpu, dims, with_bias):
         out = {k: D(4 * n * m) for k, m in sizes.items()}
         for buf in out.values():
             buf.upload(np.full(buf.nbytes // 4, np.nan, np.float32))
-        scratch = D(4 * n * max(H, inter, Hq * hd))
+        scratch = D(4 * n * H)
         gpu._check(lib.skv_fused_qkv_mm_f32(dx.ptr, n, dg.ptr, eps, dW["q"].ptr, dW["k"].ptr, dW["v"].ptr,
                                             gpu.DTYPE_BF16, 1, strides, bp("q"), bp("k"), bp("v"), H, Hq, Hkv,
                                             hd, position, out["q"].ptr, out["k"].ptr, out["v"].ptr, scratch.ptr,
@@ -386,9 +386,9 @@ def test_mm_projections_match_float64(gpu, dims, with_bias):
                                                        gpu.DTYPE_BF16, 1, H, H, bp("g"), bp("u"), H, inter,
                                                        out["act"].ptr, scratch.ptr, None))
         gpu._check(lib.skv_linear_residual_mm_f32(dctx.ptr, n, dW["o"].ptr, gpu.DTYPE_BF16, 1, Hq * hd, Hq * hd,
-                                                  H, bp("o"), dres.ptr, out["o"].ptr, scratch.ptr, None))
+                                                  H, bp("o"), dres.ptr, out["o"].ptr, None))
         gpu._check(lib.skv_linear_residual_mm_f32(dact.ptr, n, dW["d"].ptr, gpu.DTYPE_BF16, 1, inter, inter, H,
-                                                  bp("d"), dres.ptr, out["d"].ptr, scratch.ptr, None))
+                                                  bp("d"), dres.ptr, out["d"].ptr, None))
         gpu.synchronize()
         ref = _mm_reference(W, B, x, gamma, ctx, act_in, res, dims, position)
         for k, m in sizes.items():
@@ -408,9 +408,7 @@ def test_mm_projections_refuse_unsupported_shapes(gpu):
         esz = 2 if dt == gpu.DTYPE_BF16 else 4
         w = D(64 * K * esz)
         x = D.from_numpy(np.ones((3, K), np.float32))
-        scratch = D(4 * 3 * K)
-        rc = lib.skv_linear_residual_mm_f32(x.ptr, 3, w.ptr, dt, 1, K, K, out_dim, None, res.ptr, y.ptr,
-                                            scratch.ptr, None)
+        rc = lib.skv_linear_residual_mm_f32(x.ptr, 3, w.ptr, dt, 1, K, K, out_dim, None, res.ptr, y.ptr, None)
         assert rc == gpu.SKV_ERR_UNSUPPORTED, (K, out_dim, dt)
     gpu.synchronize()
     assert np.array_equal(y.download(np.float32, (3, 64)), np.full((3, 64), 7.0, np.float32))

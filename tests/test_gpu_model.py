@@ -94,6 +94,17 @@ def test_embedding_lookup(gpu, dt):
         else:
             assert not got.any()
     assert flags.download(np.int32, 1)[0] == skv.FLAG_BAD_TOKEN
+    # The rows variant (one launch for a prompt): ids 1.. of the same list.
+    rows = skv.DeviceBuffer(4 * hidden * 4)
+    flags2 = skv.DeviceBuffer.from_numpy(np.zeros(1, np.int32))
+    skv.embedding_rows(d_t, dt, vocab, hidden, d_ids, 1, 4, rows, flags2)
+    got = rows.download(np.float32, (4, hidden))
+    for r, tok in enumerate(ids[1:]):
+        if 0 <= tok < vocab:
+            np.testing.assert_array_equal(got[r].view(np.uint32), want_rows(tok).view(np.uint32))
+        else:
+            assert not got[r].any()
+    assert flags2.download(np.int32, 1)[0] == skv.FLAG_BAD_TOKEN
 
 
 def test_argmax_first_index(gpu):
