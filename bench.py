@@ -485,6 +485,20 @@ def run_cfg1(steps: int, warmup: int, with_cpu: bool):
                 "generate(1); weight_gbs = bf16 weight bytes read per decode token / decode time"))
         else:
             log(f"generate driver failed ({proc.returncode}): {proc.stderr.strip()[-300:]}")
+        # A long prompt: the prompt pass (prefill_into of 2,048 tokens in
+        # 256-token chunks, projections on the matrix cores) and the first token.
+        proc = subprocess.run([gen_driver, "--prompt", "2048", "--new", "1", "--repeat", "3"], stdout=subprocess.PIPE,
+                              stderr=subprocess.PIPE, text=True, timeout=600)
+        if proc.returncode == 0:
+            g = json.loads(proc.stdout.strip().splitlines()[-1])
+            ms = g["prefill_and_first_token_ms"]
+            line["prompt_2048"] = {
+                "ms": ms, "prompt_tokens_per_s": round(2048 / (ms / 1e3), 1),
+                "note": ("Generator::generate(prompt of 2,048 ids, 1 new token): embedding, prefill_into of 22 "
+                         "TinyLlama-shaped layers (q/k/v, o, gate/up, down on the matrix cores with inputs split "
+                         "into bf16 hi + lo, causal prefill attention), lm_head and the first greedy token")}
+        else:
+            log(f"long-prompt driver failed ({proc.returncode}): {proc.stderr.strip()[-300:]}")
     if with_cpu:
         import oracle
         # One layer's 144 single-sequence decodes with the oracle, scaled to 22 layers.
