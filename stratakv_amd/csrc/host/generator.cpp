@@ -286,9 +286,12 @@ void Generator::prompt_pass(std::size_t P, float* logits) {
     if (!prompt_rows_ || prompt_rows_->shape()[0] != P)
         prompt_rows_.emplace(std::vector<std::size_t>{P, config_.hidden_dim}, DataType::FP32, Device::GPU);
     auto* rows = static_cast<float*>(prompt_rows_->raw_data());
-    detail::check(skv_embedding_rows_f32(embeddings_->raw_data(), dtype, vocab, h, ids_, 0, static_cast<int>(P),
-                                         rows, flags_, stream_),
-                  "Generator: embedding");
+    constexpr std::size_t kEmbedRows = 65535;  // rows per embedding launch
+    for (std::size_t i = 0; i < P; i += kEmbedRows)
+        detail::check(skv_embedding_rows_f32(embeddings_->raw_data(), dtype, vocab, h, ids_, static_cast<int>(i),
+                                             static_cast<int>(std::min(kEmbedRows, P - i)),
+                                             rows + i * config_.hidden_dim, flags_, stream_),
+                      "Generator: embedding");
     for (std::size_t l = 0; l < blocks_.size(); ++l)
         blocks_[l].prefill_into(*prompt_rows_, *prompt_rows_, 0, pages_[l], pools_[l]);
     logits_of(rows + (P - 1) * config_.hidden_dim, logits);
