@@ -486,7 +486,7 @@ def run_cfg1(steps: int, warmup: int, with_cpu: bool):
         else:
             log(f"generate driver failed ({proc.returncode}): {proc.stderr.strip()[-300:]}")
         # A long prompt: the prompt pass (prefill_into of 2,048 tokens in
-        # 256-token chunks, projections on the matrix cores) and the first token.
+        # 1,024-token chunks, projections on the matrix cores) and the first token.
         proc = subprocess.run([gen_driver, "--prompt", "2048", "--new", "1", "--repeat", "3"], stdout=subprocess.PIPE,
                               stderr=subprocess.PIPE, text=True, timeout=600)
         if proc.returncode == 0:

@@ -62,8 +62,14 @@ public:
     // of the chunk runs the prefill kernel instead of the decode kernel.
     void prefill_into(const Tensor& hidden_states, Tensor& output, int seq_id,
                       memory::PageTable& page_table, memory::BlockPool& block_pool);
-    // Tokens per prefill_into pass (longer inputs run in chunks of this many).
-    static constexpr int kPrefillChunk = 256;
+    // Tokens per prefill_into pass: longer inputs run in chunks of
+    // prefill_chunk_rows() tokens, as many as kPrefillChunk and the scratch
+    // budget allow (never fewer than kPrefillMinChunk).  Long chunks give the
+    // projections and the attention large grids.
+    static constexpr int kPrefillChunk = 1024;
+    static constexpr int kPrefillMinChunk = 256;
+    static constexpr std::size_t kPrefillScratchBudget = std::size_t{96} << 20;  // bytes per block
+    int prefill_chunk_rows() const noexcept;
     // Chunk length from which the projections run on the matrix cores.
     static constexpr int kPrefillMmRows = 32;
     void forward_into(const Tensor& hidden_states, Tensor& output, int seq_id,
@@ -116,7 +122,8 @@ private:
     std::optional<Tensor> down_workspace_;
     std::optional<Tensor> decode_workspace_;  // skv_paged_attention_decode scratch
     // prefill_into scratch, [rows][dim] for up to prefill_rows_ tokens
-    // (allocated on first use, grown to kPrefillChunk at most).
+    // (allocated on first use, grown to prefill_chunk_rows() at most;
+    // pf_up_ and pf_down_ only when the separate-kernel fallback runs).
     void ensure_prefill_workspace(int rows);
     int prefill_rows_ = 0;
     std::optional<Tensor> pf_queries_, pf_keys_, pf_values_, pf_context_, pf_residual_, pf_act_;

@@ -260,6 +260,16 @@ void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output,
     }
 }
 
+int TransformerBlock::prefill_chunk_rows() const noexcept {
+    // fp32 scratch per token: q, k, v, context, residual, act, normalised input.
+    const std::size_t q_dim = attention_.num_heads() * attention_.head_dim();
+    const std::size_t kv_dim = attention_.num_kv_heads() * attention_.head_dim();
+    const std::size_t row_bytes = 4 * (2 * q_dim + 2 * kv_dim + 2 * hidden_dim_ + gate_proj_.output_dim());
+    const std::size_t fit = kPrefillScratchBudget / std::max<std::size_t>(row_bytes, 1);
+    const std::size_t rows = std::min<std::size_t>(kPrefillChunk, fit) / 64 * 64;
+    return static_cast<int>(std::max<std::size_t>(kPrefillMinChunk, rows));
+}
+
 void TransformerBlock::ensure_prefill_workspace(int rows) {
     if (rows <= prefill_rows_) return;
     const std::size_t r = static_cast<std::size_t>(rows);
@@ -276,8 +286,8 @@ void TransformerBlock::ensure_prefill_workspace(int rows) {
     make(pf_residual_, hidden_dim_);
     make(pf_act_, inter);
     make(pf_normalized_, hidden_dim_);
-    make(pf_up_, inter);
-    make(pf_down_, hidden_dim_);
+    pf_up_.reset();
+    pf_down_.reset();
     if (!pf_meta_) pf_meta_.emplace(std::vector<std::size_t>{4}, DataType::FP32, Device::GPU);
     prefill_rows_ = rows;
 }
@@ -317,7 +327,13 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
     const int hidden = static_cast<int>(hidden_dim_);
     const int inter = static_cast<int>(gate_proj_.output_dim());
     const int q_dim = num_heads * head_dim;
-    ensure_prefill_workspace(std::min(tokens, kPrefillChunk));
+    const int chunk = prefill_chunk_rows();
+    ensure_prefill_workspace(std::min(tokens, chunk));
+    const std::size_t ws_rows = static_cast<std::size_t>(prefill_rows_);
+    auto fallback_buffer = [&](std::optional<Tensor>& t, std::size_t dim) {
+        if (!t) t.emplace(std::vector<std::size_t>{ws_rows, dim}, DataType::FP32, Device::GPU);
+        return static_cast<float*>(t->raw_data());
+    };
     void* s = stream_;
 
     auto fp = [](Tensor& t) { return static_cast<float*>(t.raw_data()); };
@@ -355,8 +371,8 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
     float* act = fp(*pf_act_);
     auto* meta = static_cast<std::int32_t*>(pf_meta_->raw_data());
 
-    for (int c0 = 0; c0 < tokens; c0 += kPrefillChunk) {
-        const int n = std::min(kPrefillChunk, tokens - c0);
+    for (int c0 = 0; c0 < tokens; c0 += chunk) {
+        const int n = std::min(chunk, tokens - c0);
         const float* x = cfp(hidden_states) + static_cast<std::size_t>(c0) * hidden;
         float* y = fp(output) + static_cast<std::size_t>(c0) * hidden;
         const int p0 = page_table.get_state(seq_id).sequence_length;
@@ -424,7 +440,7 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                fused(gate_up(skv_fused_gate_up_swiglu_rows_f32, fp(*pf_normalized_)),
                      "prefill_into: fused rmsnorm + gate/up + swiglu")))) {
             float* hn = fp(*pf_normalized_);
-            float* up = fp(*pf_up_);
+            float* up = fallback_buffer(pf_up_, static_cast<std::size_t>(inter));
             detail::check(skv_rmsnorm_f32(h, hn, cfp(norm2_.gamma()), n, hidden, norm2_.epsilon(), s),
                           "prefill_into: post-attention rmsnorm");
             linear(gate_proj_, hn, n, act, "prefill_into: gate_proj");
@@ -440,7 +456,7 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                                                  stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
                                                  bias_of(down_proj_), h, y, s),
                     "prefill_into: fused down_proj + residual"))) {
-            float* d = fp(*pf_down_);
+            float* d = fallback_buffer(pf_down_, hidden_dim_);
             linear(down_proj_, act, n, d, "prefill_into: down_proj");
             detail::check(skv_add_f32(h, d, n * hidden, s), "prefill_into: residual");
             detail::check(skv_memcpy_d2d(y, h, static_cast<std::size_t>(n) * hidden * sizeof(float), s),
