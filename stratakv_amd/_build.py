@@ -32,6 +32,10 @@ ARCH = "gfx950"
 # forms v_pk_* from float2-shaped code); the host pass ignores the feature.
 NO_PACKED_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall"] + NO_PACKED_FP32
+# Per-file additions.  skv_layer_ops.hip: the matrix-core projections keep
+# their MFMA accumulators in ordinary VGPRs (in AGPRs the allocator rotates
+# them between unrolled stages with ~40 copies per loop iteration).
+FILE_FLAGS = {"skv_layer_ops.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def _run(cmd: list[str], cwd: str | None = None) -> None:
@@ -61,7 +65,8 @@ def build_library() -> str:
         objs.append(obj)
     for src in sorted(glob.glob(os.path.join(CSRC, "*.hip"))):
         obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-        _run([HIPCC, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj])
+        extra = FILE_FLAGS.get(os.path.basename(src), [])
+        _run([HIPCC, *HIP_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj])
         objs.append(obj)
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", *objs, "-o", LIB + ".tmp"])
     os.replace(LIB + ".tmp", LIB)

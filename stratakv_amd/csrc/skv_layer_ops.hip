@@ -860,17 +860,20 @@ __global__ __launch_bounds__(64 * kMmWaves) void proj_mm_kernel(MmArgs args) {
     auto stage_inputs = [&](int buf, const Stage& o) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < KS; ++q) {
+            // hi = bf16(v) for a pair in one conversion; its two values back as
+            // floats with a byte permute (low half to the top) and a mask; lo =
+            // bf16 of the exact remainder v - hi, one conversion per pair.
+            typedef __bf16 mm_bf16x2_t __attribute__((ext_vector_type(2)));
             uint32_t hw[8], lw[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float v0 = o.x[q][e >> 1][2 * (e & 1)], v1 = o.x[q][e >> 1][2 * (e & 1) + 1];
-                const __bf16 h0 = static_cast<__bf16>(v0), h1 = static_cast<__bf16>(v1);
-                const __bf16 l0 = static_cast<__bf16>(v0 - static_cast<float>(h0));
-                const __bf16 l1 = static_cast<__bf16>(v1 - static_cast<float>(h1));
-                hw[e] = __builtin_bit_cast(uint16_t, h0) |
-                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
-                lw[e] = __builtin_bit_cast(uint16_t, l0) |
-                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
+                const mm_bf16x2_t h = {static_cast<__bf16>(v0), static_cast<__bf16>(v1)};
+                hw[e] = __builtin_bit_cast(uint32_t, h);
+                const float h0 = __uint_as_float(__builtin_amdgcn_perm(hw[e], hw[e], 0x01000c0cu));
+                const float h1 = __uint_as_float(hw[e] & 0xFFFF0000u);
+                const mm_bf16x2_t l = {static_cast<__bf16>(v0 - h0), static_cast<__bf16>(v1 - h1)};
+                lw[e] = __builtin_bit_cast(uint32_t, l);
             }
             unsigned char* dh = xs_at(buf, q, 0) + st_tok * kMmRowBytes + st_k * 2;
             unsigned char* dl = xs_at(buf, q, 1) + st_tok * kMmRowBytes + st_k * 2;
@@ -896,16 +899,22 @@ __global__ __launch_bounds__(64 * kMmWaves) void proj_mm_kernel(MmArgs args) {
                 bh[c] = *reinterpret_cast<const mm_u32x4_t*>(xs_at(buf, part, 0) + off);
                 bl[c] = *reinterpret_cast<const mm_u32x4_t*>(xs_at(buf, part, 1) + off);
             }
+            // All hi products, then all lo products: no MFMA waits on the one
+            // issued just before it.
 #pragma unroll
             for (int a = 0; a < 2; ++a)
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const mm_bf16x8_t av = __builtin_bit_cast(mm_bf16x8_t, o.wop[ks][a]);
-                    acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(mm_bf16x8_t, bh[c]),
-                                                                        acc[a][c], 0, 0, 0);
-                    acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(mm_bf16x8_t, bl[c]),
-                                                                        acc[a][c], 0, 0, 0);
-                }
+                for (int c = 0; c < 4; ++c)
+                    acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(mm_bf16x8_t, o.wop[ks][a]), __builtin_bit_cast(mm_bf16x8_t, bh[c]),
+                        acc[a][c], 0, 0, 0);
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(mm_bf16x8_t, o.wop[ks][a]), __builtin_bit_cast(mm_bf16x8_t, bl[c]),
+                        acc[a][c], 0, 0, 0);
         }
     };
 
