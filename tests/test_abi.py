@@ -122,3 +122,37 @@ def test_multi_token_entry_points_reject_invalid_arguments():
     assert lib.skv_write_i32(FAKE, vals, 17, None) == skv.SKV_ERR_INVALID_ARGUMENT
     assert lib.skv_write_i32(None, vals, 2, None) == skv.SKV_ERR_INVALID_ARGUMENT
     assert lib.skv_write_i32(FAKE, vals, 0, None) == skv.SKV_OK             # nothing to write
+
+
+def test_matrix_core_projections_and_prompt_embedding_reject_invalid_arguments():
+    """The *_mm_f32 projections and skv_embedding_rows_f32 validate before any
+    device work: INVALID_ARGUMENT for bad sizes or a missing scratch,
+    UNSUPPORTED (nothing launched) for shapes the matrix-core kernel does not
+    take: fp32 weights, in_dim not a multiple of 128, an output count not a
+    multiple of 32 (16 for gate/up), a rotated head_dim not a multiple of 32."""
+    lib = skv.lib()
+    eps = ctypes.c_float(1e-5)
+    strides = (ctypes.c_int64 * 3)(2048, 2048, 2048)
+    qkv = lambda rows, gamma, dt, K, hd, position, normalized: lib.skv_fused_qkv_mm_f32(
+        FAKE, rows, gamma, eps, FAKE, FAKE, FAKE, dt, 1, strides, None, None, None, K, 32, 4, hd, position,
+        FAKE, FAKE, FAKE, normalized, None)
+    B = skv.DTYPE_BF16
+    assert qkv(0, FAKE, B, 2048, 64, 0, FAKE) == skv.SKV_ERR_INVALID_ARGUMENT       # no rows
+    assert qkv(4, FAKE, B, 2048, 64, 0, None) == skv.SKV_ERR_INVALID_ARGUMENT       # gamma without scratch
+    assert qkv(4, FAKE, skv.DTYPE_FP32, 2048, 64, 0, FAKE) == skv.SKV_ERR_UNSUPPORTED
+    assert qkv(4, FAKE, B, 2000, 64, 0, FAKE) == skv.SKV_ERR_UNSUPPORTED            # K not a multiple of 128
+    assert qkv(4, FAKE, B, 2048, 48, 0, FAKE) == skv.SKV_ERR_UNSUPPORTED            # rotated head_dim 48
+    gate_up = lambda rows, K, out: lib.skv_fused_gate_up_swiglu_mm_f32(
+        FAKE, rows, FAKE, eps, FAKE, FAKE, B, 1, K, K, None, None, K, out, FAKE, FAKE, None)
+    assert gate_up(0, 2048, 5632) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert gate_up(3, 2048, 5640) == skv.SKV_ERR_UNSUPPORTED                        # out_dim not a multiple of 16
+    res = lambda rows, K, out: lib.skv_linear_residual_mm_f32(FAKE, rows, FAKE, B, 1, K, K, out, None, FAKE, FAKE,
+                                                             None)
+    assert res(-1, 2048, 2048) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert res(2, 2048, 2050) == skv.SKV_ERR_UNSUPPORTED                            # out_dim not a multiple of 32
+    emb = lambda table, first, rows: lib.skv_embedding_rows_f32(table, B, 32000, 2048, FAKE, first, rows, FAKE,
+                                                                None, None)
+    assert emb(FAKE, 0, 0) == skv.SKV_ERR_INVALID_ARGUMENT                          # no rows
+    assert emb(FAKE, 0, 65536) == skv.SKV_ERR_INVALID_ARGUMENT                      # more than one launch takes
+    assert emb(FAKE, -1, 4) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert emb(None, 0, 4) == skv.SKV_ERR_INVALID_ARGUMENT
