@@ -224,17 +224,22 @@ def _checkpoint(name, ckpt_dir, golden):
     return path
 
 
-def _check_forced(path, golden):
+def _check_forced(path, golden, n_prompt=None):
     """Teacher-forced logits vs the reference's top-8 per step; returns the
-    greedy tokens of the forced run and the max logit error."""
+    greedy tokens of the forced run and the max logit error.  n_prompt (default:
+    the golden prompt) tokens go through the prompt pass at once; the logits
+    from its last row on are checked."""
     prompt, gen = golden["prompt"], golden["generated"]
     tokens = prompt + gen
+    n_prompt = len(prompt) if n_prompt is None else n_prompt
+    first = n_prompt - len(prompt)   # golden step of the first checked row
     out = os.path.join(os.path.dirname(path), "forced.bin")
-    res = tool("forced", path, len(prompt), out, "--", *tokens)
+    res = tool("forced", path, n_prompt, out, "--", *tokens)
     assert res["ok"], res
     logits = np.fromfile(out, np.float32).reshape(res["rows"], res["vocab"])
-    top_ids, top_vals = np.array(golden["top_ids"]), np.array(golden["top_vals"], np.float32)
-    assert logits.shape[0] == top_ids.shape[0] == len(gen) + 1
+    top_ids = np.array(golden["top_ids"])[first:]
+    top_vals = np.array(golden["top_vals"], np.float32)[first:]
+    assert logits.shape[0] == top_ids.shape[0] == len(tokens) - n_prompt + 1
     got = np.take_along_axis(logits, top_ids, axis=1)
     err = np.abs(got - top_vals)
     bound = LOGIT_ABS + LOGIT_REL * np.abs(top_vals)
@@ -317,3 +322,8 @@ def test_generate_tinyllama_matches_reference(gpu, ckpt_dir):
           "gen_ms", res["gen_ms"], "load_ms", res["load_ms"])
     _, err = _check_forced(path, golden)
     print(f"tinyllama max logit error {err:.3e}")
+    # A 100-token prompt (the projections of the prompt pass on the matrix
+    # cores, inputs split into hi + lo bf16 parts), then the 44 remaining
+    # tokens teacher-forced through the cache it wrote: the same bounds.
+    _, err = _check_forced(path, golden, n_prompt=100)
+    print(f"tinyllama max logit error after a 100-token prompt pass {err:.3e}")
