@@ -96,6 +96,14 @@ constexpr int kGemvRowsPerWave = 2;    // output rows per wavefront
 constexpr int kGemvUnroll = 4;         // 16-byte loads per row in flight
 constexpr int kGemvMaxLdsK = 8192;     // x staged in LDS up to this many inputs
 
+// Weight rows are read once per call (streamed): 16-byte loads with the
+// non-temporal hint, which keeps them from displacing reused lines in L2.
+__device__ __forceinline__ uint4 load_stream16(const char* p) {
+    typedef uint32_t u32x4s_t __attribute__((ext_vector_type(4)));
+    const u32x4s_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4s_t*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 // Dot products of x (K floats, LDS or global) with two output-major weight
 // rows (byte pointers, 16-byte aligned, K elements each; r1 may repeat r0), by
 // one wavefront: 16 bytes per lane per load, fp32 accumulation, then a wave
@@ -128,7 +136,7 @@ struct PairPrefetch {
             for (int u = 0; u < NU; ++u)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    q[j][u] = *reinterpret_cast<const uint4*>(rows[j] + (min(u, npre - 1) * STEP + lane * EPL) * ESZ);
+                    q[j][u] = load_stream16(rows[j] + (min(u, npre - 1) * STEP + lane * EPL) * ESZ);
         }
     }
 
@@ -167,14 +175,14 @@ struct PairPrefetch {
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int u = 0; u < NU; ++u)
-                    q[j][u] = *reinterpret_cast<const uint4*>(rows[j] + (k0 + u * STEP + lane * EPL) * ESZ);
+                    q[j][u] = load_stream16(rows[j] + (k0 + u * STEP + lane * EPL) * ESZ);
             accumulate(xr, k0, lane, NU, acc);
         }
         for (int k = k0 + lane * EPL; k + EPL <= K; k += STEP) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 float f[EPL];
-                widen16<BF16W>(*reinterpret_cast<const uint4*>(rows[j] + k * ESZ), f);
+                widen16<BF16W>(load_stream16(rows[j] + k * ESZ), f);
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) acc[j] = fmaf(xr[k + e], f[e], acc[j]);
             }
