@@ -464,7 +464,8 @@ def run_cfg1(steps: int, warmup: int, with_cpu: bool):
             line["layer_stack"] = dict(stack, note=(
                 "end-to-end forward_into of 22 TinyLlama-shaped layers per token (bf16 N(0,0.02) "
                 "weights, GEMVs, norms, RoPE, fused append + decode, SwiGLU, residuals); "
-                "embedding, lm_head and sampling are not part of this build"))
+                "embedding, lm_head and token choice are outside this measurement (the "
+                "generator entry times them)"))
         else:
             log(f"layer stack driver failed ({proc.returncode}): {proc.stderr.strip()[-300:]}")
     # The whole generation through Generator::generate (embedding, 22 layers,

@@ -221,6 +221,16 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
     const int kvh = SPLIT ? static_cast<int>(blockIdx.x % Hkv) : w % Hkv;
     const int range = w / Hkv;
 
+    // SPLIT: the workgroup names its sequence, so the sequence's whole table
+    // row (max_blocks <= 64 entries, one per lane) is loaded beside the
+    // lengths, before the split is known: the block addresses then wait on one
+    // dependent load (lengths and table together) instead of two.
+    int trow = 0;
+    if constexpr (SPLIT) {
+        const int64_t row = static_cast<int64_t>(blockIdx.x / Hkv) * p.max_blocks;
+        trow = p.tables[row + std::min(lane, p.max_blocks - 1)];
+    }
+
     const WorkSplit split = build_split(p, P_s);
     if (!SPLIT && range >= split.used) return;
     const int per = split.per;
@@ -259,7 +269,7 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
         int64_t new_dst = 0;
         u32x4_t knew = {0u, 0u, 0u, 0u}, vnew = {0u, 0u, 0u, 0u};
         if (p.k_new != nullptr && kb1 == nb && L >= 1 && L <= nb * BS) {
-            const int64_t e = table[nb - 1];
+            const int64_t e = SPLIT ? __shfl(trow, nb - 1, 64) : table[nb - 1];
             if (e >= 0 && e < p.total_blocks) {
                 const int slot = (L - 1) - (nb - 1) * BS;
                 kb_new = nb - 1;
@@ -325,7 +335,11 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
         // Table entries of the segment, 64 at a time: lane i holds entry tb + i
         // (tv) and tb + 64 + i (tvn, loaded one chunk ahead), so the block
         // addresses never wait on a dependent table load.
-        auto table_entry = [&](int k) -> int { return table[k < kb1 ? k : kb1 - 1]; };
+        auto table_entry = [&](int k) -> int {
+            const int kc = k < kb1 ? k : kb1 - 1;
+            if constexpr (SPLIT) return __shfl(trow, kc, 64);  // kc < nb <= max_blocks
+            return table[kc];
+        };
         int tb = k0;
         int tv = table_entry(tb + lane);
         int tvn = table_entry(tb + 64 + lane);
