@@ -221,8 +221,7 @@ def run_gpu(w, steps: int, warmup: int, fused: bool = True):
     lens = skv.DeviceBuffer.from_numpy(w["lens"])
     positions = skv.DeviceBuffer.from_numpy(w["lens"] - 1)
     out = skv.DeviceBuffer(B * Hq * hd * 4)
-    wsb = skv.decode_workspace_bytes(B, Hq, Hkv, hd)
-    ws = skv.DeviceBuffer(wsb)
+    ws, wsb = skv.decode_workspace(B, Hq, Hkv, hd, stream.handle)
     max_blocks = w["tables"].shape[1]
     scale = 1.0 / math.sqrt(hd)
     stream.synchronize()
@@ -400,9 +399,8 @@ def run_cfg1(steps: int, warmup: int, with_cpu: bool):
     # A fresh LIFO pool hands the one sequence blocks 0, 1, 2, ... in every layer.
     table = skv.DeviceBuffer.from_numpy(np.arange(-(-P // bs), dtype=np.int32))
     out = skv.DeviceBuffer(Hq * hd * 4)
-    wsb = int(skv.lib().skv_paged_attention_decode_workspace_bytes(Hq, Hkv, hd))
-    ws = skv.DeviceBuffer(wsb)
     stream = skv.Stream()
+    ws, wsb = skv.single_decode_workspace(Hq, Hkv, hd, stream.handle)
     scale = 1.0 / math.sqrt(hd)
     qrow, kvrow = Hq * hd * 4, Hkv * hd * 4
 

@@ -28,8 +28,8 @@
  *   skv_malloc / skv_free / skv_memcpy_*
  *                               <- the cudaMalloc/cudaFree/cudaMemcpy calls of
  *                                  BlockPool and PageTable,
- *                                  src/memory/block_pool.cpp:175-206,
- *                                  src/memory/page_table.cpp:289-347
+ *                                  src/memory/block_pool.cpp:85-105,118-145,
+ *                                  src/memory/page_table.cpp:180-238
  */
 #ifndef STRATAKV_AMD_H
 #define STRATAKV_AMD_H

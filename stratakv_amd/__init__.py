@@ -251,6 +251,20 @@ def decode_workspace_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int, h
     return int(lib().skv_paged_decode_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim))
 
 
+def decode_workspace(num_seqs: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                     stream=None) -> tuple["DeviceBuffer", int]:
+    """A decode workspace for these arguments; returns (buffer, size in bytes)."""
+    nbytes = decode_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim)
+    return DeviceBuffer(nbytes), nbytes
+
+
+def single_decode_workspace(num_q_heads: int, num_kv_heads: int, head_dim: int,
+                            stream=None) -> tuple["DeviceBuffer", int]:
+    """The same for the single-sequence entry points (skv_paged_attention_decode*)."""
+    nbytes = int(lib().skv_paged_attention_decode_workspace_bytes(num_q_heads, num_kv_heads, head_dim))
+    return DeviceBuffer(nbytes), nbytes
+
+
 def paged_decode(q, q_dtype: int, k_pool, v_pool, total_blocks: int, block_tables,
                  max_blocks_per_seq: int, context_lens, num_seqs: int, num_q_heads: int,
                  num_kv_heads: int, head_dim: int, block_size: int, scale: float, out,
@@ -397,7 +411,8 @@ class Stream:
 __all__ = [
     "LIB_PATH", "HEADER_PATH", "SkvError", "SkvInvalidArgument", "DTYPE_BF16", "DTYPE_FP32",
     "header_symbols", "lib", "device_count", "require_gpu", "synchronize", "DeviceBuffer",
-    "fill_normal_bf16", "kv_append", "decode_workspace_bytes", "paged_decode",
+    "fill_normal_bf16", "kv_append", "decode_workspace_bytes",
+    "decode_workspace", "single_decode_workspace", "paged_decode",
     "paged_attention_decode", "gather_blocks", "Event", "Stream", "convert_to_bf16", "convert_to_f32",
     "check_finite", "embedding", "embedding_rows", "argmax", "sample",
 ]

@@ -52,22 +52,38 @@ OBJ = os.path.join(ROOT, "build", "obj")
 CXX = os.environ.get("CXX", "g++")
 
 
+def _jobs() -> int:
+    """Parallel compile jobs: MAX_JOBS when set, else the CPU count, at most 16."""
+    try:
+        return max(1, min(16, int(os.environ.get("MAX_JOBS", "0")) or (os.cpu_count() or 1)))
+    except ValueError:
+        return max(1, min(16, os.cpu_count() or 1))
+
+
+def _run_all(cmds: list[list[str]]) -> None:
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=_jobs()) as pool:
+        for f in [pool.submit(_run, c) for c in cmds]:
+            f.result()
+
+
 def build_library() -> str:
     """Compile the HIP kernels and C ABI (hipcc, gfx950) and the C++ host
     layer (plain C++17; it reaches the GPU only through the C ABI) into one
     shared library."""
     os.makedirs(OBJ, exist_ok=True)
-    objs = []
+    objs, cmds = [], []
     for src in sorted(glob.glob(os.path.join(CSRC, "host", "*.cpp"))):
         obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-        _run([CXX, "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", f"-I{INCLUDE}", "-c", src,
-              "-o", obj])
+        cmds.append([CXX, "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", f"-I{INCLUDE}", "-c", src,
+                     "-o", obj])
         objs.append(obj)
     for src in sorted(glob.glob(os.path.join(CSRC, "*.hip"))):
         obj = os.path.join(OBJ, os.path.basename(src) + ".o")
         extra = FILE_FLAGS.get(os.path.basename(src), [])
-        _run([HIPCC, *HIP_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj])
+        cmds.append([HIPCC, *HIP_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj])
         objs.append(obj)
+    _run_all(cmds)
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", *objs, "-o", LIB + ".tmp"])
     os.replace(LIB + ".tmp", LIB)
     return LIB
@@ -76,14 +92,14 @@ def build_library() -> str:
 def build_cpp_tests() -> list[str]:
     """Compile tests/cpp/*.cpp against the library (and the oracle, for traces)."""
     os.makedirs(BIN, exist_ok=True)
-    outs = []
+    outs, cmds = [], []
     for src in sorted(glob.glob(os.path.join(ROOT, "tests", "cpp", "*.cpp"))):
         exe = os.path.join(BIN, os.path.splitext(os.path.basename(src))[0])
-        cmd = [HIPCC, "-O2", "-std=c++17", f"-I{INCLUDE}", f"-I{ORACLE}", "-x", "c++", src,
-               f"-L{PKG}", "-lstratakv_amd", f"-Wl,-rpath,{PKG}",
-               f"-L{ORACLE}", "-loracle", f"-Wl,-rpath,{ORACLE}", "-o", exe]
-        _run(cmd)
+        cmds.append([HIPCC, "-O2", "-std=c++17", f"-I{INCLUDE}", f"-I{ORACLE}", "-x", "c++", src,
+                     f"-L{PKG}", "-lstratakv_amd", f"-Wl,-rpath,{PKG}",
+                     f"-L{ORACLE}", "-loracle", f"-Wl,-rpath,{ORACLE}", "-o", exe])
         outs.append(exe)
+    _run_all(cmds)
     return outs
 
 
@@ -91,12 +107,13 @@ def build_bench() -> list[str]:
     """Compile the C++ benchmark drivers (stratakv_amd/csrc/bench/*.cpp) into
     build/bin/bench_<name>; they use only the library's public headers."""
     os.makedirs(BIN, exist_ok=True)
-    outs = []
+    outs, cmds = [], []
     for src in sorted(glob.glob(os.path.join(CSRC, "bench", "*.cpp"))):
         exe = os.path.join(BIN, "bench_" + os.path.splitext(os.path.basename(src))[0])
-        _run([CXX, "-O2", "-std=c++17", "-Wall", f"-I{INCLUDE}", src, f"-L{PKG}", "-lstratakv_amd",
-              f"-Wl,-rpath,{PKG}", "-o", exe])
+        cmds.append([CXX, "-O2", "-std=c++17", "-Wall", f"-I{INCLUDE}", src, f"-L{PKG}", "-lstratakv_amd",
+                     f"-Wl,-rpath,{PKG}", "-o", exe])
         outs.append(exe)
+    _run_all(cmds)
     return outs
 
 
@@ -104,7 +121,7 @@ def build_oracle() -> None:
     """Test infrastructure: the C oracle, plus the reference checker when present."""
     _run(["make", "-B", "-C", ORACLE, "all"])
     if os.path.isdir(os.path.join(REFERENCE, "src")):
-        _run(["make", "-B", "-C", ORACLE, "ref", f"REF={REFERENCE}"])
+        _run(["make", "-B", f"-j{_jobs()}", "-C", ORACLE, "ref", f"REF={REFERENCE}"])
 
 
 def build_all() -> None:

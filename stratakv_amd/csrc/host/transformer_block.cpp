@@ -63,7 +63,7 @@ void TransformerBlock::to(Device device) {
         const std::size_t ws = skv_paged_attention_decode_workspace_bytes(
             static_cast<int>(attention_.num_heads()), static_cast<int>(attention_.num_kv_heads()),
             static_cast<int>(attention_.head_dim()));
-        decode_workspace_.emplace(std::vector<std::size_t>{ws}, DataType::FP32, device);
+        decode_workspace_.emplace(std::vector<std::size_t>{(ws + 3) / 4}, DataType::FP32, device);
     } else {
         normalized_input_workspace_.reset();
         query_workspace_.reset();

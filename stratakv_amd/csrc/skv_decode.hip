@@ -27,9 +27,12 @@
 //   Each wavefront keeps a ring of NBUF blocks in registers: while one is
 //   computed the next NBUF - 1 are in flight, and the block addresses come
 //   from table entries preloaded 64 at a time (no dependent table load per
-//   block).  K/V are read once per step, so the loads carry the non-temporal
-//   hint (streamed through L2 without displacing reused lines), which on
-//   MI355X raises the achievable rate of this pattern by ~10 %.
+//   block).  The rows are read with buffer loads through a descriptor that
+//   spans exactly one block, so a ring position past the segment reads
+//   through a descriptor of size 0 (zeros, no memory traffic).  K/V are read
+//   once per step, so the loads carry the non-temporal hint (streamed through
+//   L2 without displacing reused lines), which on MI355X raises the
+//   achievable rate of this pattern by ~10 %.
 // * Online softmax in the exp2 domain with lazy rescaling: the running max is
 //   only raised (and acc, sum rescaled) when a block's max exceeds it by more
 //   than 2^8, which after the first blocks is rare; the result is exact since
@@ -82,6 +85,8 @@ constexpr int kMaxHeadDim = 512;
 constexpr int kMaxWaves = 8192;      // bound on persistent wavefronts (workspace sizing)
 constexpr int kMaxBatchPerLaunch = 4096;  // sequences per launch (LDS prefix table)
 constexpr float kLazyRescale = 8.0f;
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer descriptor: 32-bit data format, no swizzle
+constexpr int kLoadNonTemporal = 2;     // cache policy of the K/V loads: nt (read once per step)
 
 __device__ __forceinline__ int seq_len(const DecodeParams& p, int b) {
     return p.lens != nullptr ? p.lens[b] : p.single_len;
@@ -94,7 +99,7 @@ __device__ __forceinline__ int seq_blocks(const DecodeParams& p, int b) {
 }
 
 // ---------------------------------------------------------------------------
-// Work split ("stream-K" over blocks).  Every wavefront builds P[b] = blocks of
+// Work split ("stream-K" over blocks).  Every workgroup builds P[b] = blocks of
 // the sequences before b in LDS (a wave scan over the batch), so no planner
 // launch is needed.  The flattened (sequence, block) space [0, P[B]) is cut
 // into `used` ranges of `per` blocks; wavefront w serves range w / Hseg for
@@ -109,7 +114,7 @@ struct WorkSplit {
     int total, per, used;
 };
 
-__device__ WorkSplit build_split(const DecodeParams& p, int* P_s) {
+__device__ WorkSplit build_split(const DecodeParams& p, int* P_s, bool stream_k) {
     const int lane = threadIdx.x;
     if (lane < 64) {  // wavefront 0 of the workgroup scans
         int carry = 0;
@@ -138,8 +143,8 @@ __device__ WorkSplit build_split(const DecodeParams& p, int* P_s) {
         if (lane == 0) P_s[0] = 0;
     }
     __syncthreads();
-    WorkSplit ws;
-    ws.total = P_s[p.B];
+    WorkSplit ws{P_s[p.B], 0, 0};
+    if (!stream_k) return ws;  // one workgroup per segment: no ranges
     ws.per = std::max(p.min_per, ws.total > 0 ? cdiv(ws.total, p.ranges) : 1);
     ws.used = ws.total > 0 ? cdiv(ws.total, ws.per) : 0;
     if (blockIdx.x == 0 && lane < 64) {  // publish for the merge kernel
@@ -165,6 +170,21 @@ __device__ __forceinline__ int find_seq(const int* P, int B, int pos) {
 
 __device__ __forceinline__ int64_t partial_row(int range, bool tail, int Hseg, int group) {
     return (2 * static_cast<int64_t>(range) + (tail ? 1 : 0)) * Hseg + group;
+}
+
+// N values x (N = 8, 4, 2 or 1; o aligned to 4 N bytes) times sc.
+template <int N>
+__device__ __forceinline__ void store_scaled(float* o, const float* x, float sc) {
+    if constexpr (N == 8) {
+        reinterpret_cast<float4*>(o)[0] = make_float4(x[0] * sc, x[1] * sc, x[2] * sc, x[3] * sc);
+        reinterpret_cast<float4*>(o)[1] = make_float4(x[4] * sc, x[5] * sc, x[6] * sc, x[7] * sc);
+    } else if constexpr (N == 4) {
+        *reinterpret_cast<float4*>(o) = make_float4(x[0] * sc, x[1] * sc, x[2] * sc, x[3] * sc);
+    } else if constexpr (N == 2) {
+        *reinterpret_cast<float2*>(o) = make_float2(x[0] * sc, x[1] * sc);
+    } else {
+        o[0] = x[0] * sc;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -231,10 +251,11 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
         trow = p.tables[row + std::min(lane, p.max_blocks - 1)];
     }
 
-    const WorkSplit split = build_split(p, P_s);
+    const WorkSplit split = build_split(p, P_s, !SPLIT);
     if (!SPLIT && range >= split.used) return;
     const int per = split.per;
     const int64_t row_stride = static_cast<int64_t>(Hkv) * HD;
+    const int block_bytes = static_cast<int>(BS * row_stride * 2);
     int range_lo = range * per;
     int range_hi = range_lo + per;
     int b = 0;
@@ -330,7 +351,7 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
 
-        const int64_t lane_off = static_cast<int64_t>(r) * row_stride + static_cast<int64_t>(kvh) * HD + c * 8;
+        const int lane_off_b = static_cast<int>((r * row_stride + static_cast<int64_t>(kvh) * HD + c * 8) * 2);
 
         // Table entries of the segment, 64 at a time: lane i holds entry tb + i
         // (tv) and tb + 64 + i (tvn, loaded one chunk ahead), so the block
@@ -345,9 +366,10 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
         int tvn = table_entry(tb + 64 + lane);
 
         // Loads of block kb into one register buffer.  Every call issues the
-        // same loads (a position past the segment reloads its last block, an
-        // entry outside the pool reads block 0), so the compiler's wait counts
-        // stay exact; the return value says whether the block is real.
+        // same loads, so the compiler's wait counts stay exact: a position
+        // past the segment, or a table entry outside the pool, reads through
+        // a buffer descriptor of size 0, whose loads return zeros without
+        // touching memory.  The return value says whether the block is real.
         auto issue = [&](int kb, u32x4_t (&kk)[TPL], u32x4_t (&vv)[TPL]) -> bool {
             const bool in_seg = kb < kb1;
             kb = in_seg ? kb : kb1 - 1;
@@ -358,13 +380,16 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
             }
             const int64_t e = __builtin_amdgcn_readlane(tv, kb - tb);
             const bool valid = in_seg && e >= 0 && e < p.total_blocks;
-            const int64_t pb = e >= 0 && e < p.total_blocks ? e : 0;
-            const int64_t base = pb * BS * row_stride + lane_off;
+            const int64_t base = (valid ? e : 0) * BS * row_stride;
+            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t*>(p.k + base), 0, valid ? block_bytes : 0, kRsrcWord3);
+            const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t*>(p.v + base), 0, valid ? block_bytes : 0, kRsrcWord3);
 #pragma unroll
             for (int i = 0; i < TPL; ++i) {
-                const int64_t off = base + static_cast<int64_t>(i) * RPI * row_stride;
-                kk[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p.k + off));
-                vv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p.v + off));
+                const int soff = static_cast<int>(i * RPI * row_stride * 2);
+                kk[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, lane_off_b, soff, kLoadNonTemporal));
+                vv[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, lane_off_b, soff, kLoadNonTemporal));
             }
             return valid;
         };
@@ -494,63 +519,33 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
         wave_lds_sync();
         const bool final_out = !SPLIT && seg_lo >= range_lo && seg_hi <= range_hi;
         const int64_t prow = partial_row(range, seg_lo > range_lo, Hkv, kvh);
-        const int v0 = NF * r;
-        // Partial of head g: ws (merge kernel) or, SPLIT, this wave's LDS slot.
-        auto partial_acc = [&](int g) -> float* {
-            if constexpr (SPLIT) return &part_acc[wv][g * HD];
-            return p.ws_acc + (prow * G + g) * HD;
-        };
-        auto partial_ml = [&](int g, float mg, float lg) {
-            if constexpr (SPLIT) {
-                part_ml[wv][0][g] = mg;
-                part_ml[wv][1][g] = lg;
-            } else {
-                p.ws_ml[(prow * G + g) * 2 + 0] = mg;
-                p.ws_ml[(prow * G + g) * 2 + 1] = lg;
-            }
-        };
-        if constexpr (NF >= 8) {
+        // Lane (r, c) stores VPH values of each of its NHL heads at dims d0...
+        constexpr int NHL = NF >= 8 ? NF / 8 : 1;
+        constexpr int VPH = NF >= 8 ? 8 : NF;
+        const int g0 = NF * r / 8;
+        const int d0 = 8 * c + (NF >= 8 ? 0 : NF * r % 8);
+        const bool owns_ml = c == 0 && d0 == 0;  // one lane per head stores (max, sum)
 #pragma unroll
-            for (int gg = 0; gg < NF / 8; ++gg) {
-                const int g = v0 / 8 + gg;
-                const float lsum = h_s[0][g];
-                const float* x = v + 8 * gg;
-                float4* o;
-                float sc = 1.0f;
-                if (final_out) {
-                    sc = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-                    o = reinterpret_cast<float4*>(p.out + (static_cast<int64_t>(b) * p.Hq + h0 + g) * HD + 8 * c);
-                } else {
-                    o = reinterpret_cast<float4*>(partial_acc(g) + 8 * c);
-                    if (c == 0) partial_ml(g, h_s[1][g], lsum);
-                }
-                if (final_out) {
-                    o[0] = make_float4(x[0] * sc, x[1] * sc, x[2] * sc, x[3] * sc);
-                    o[1] = make_float4(x[4] * sc, x[5] * sc, x[6] * sc, x[7] * sc);
-                } else {
-                    o[0] = make_float4(x[0], x[1], x[2], x[3]);
-                    o[1] = make_float4(x[4], x[5], x[6], x[7]);
-                }
-            }
-        } else {
-            const int g = v0 / 8, e0 = v0 % 8;
+        for (int hh = 0; hh < NHL; ++hh) {
+            const int g = g0 + hh;
             const float lsum = h_s[0][g];
-            float* o;
-            float sc = 1.0f;
+            const float* x = v + VPH * hh;
             if (final_out) {
-                sc = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-                o = p.out + (static_cast<int64_t>(b) * p.Hq + h0 + g) * HD + 8 * c + e0;
-            } else {
-                o = partial_acc(g) + 8 * c + e0;
-                if (c == 0 && e0 == 0) partial_ml(g, h_s[1][g], lsum);
+                store_scaled<VPH>(p.out + (static_cast<int64_t>(b) * p.Hq + h0 + g) * HD + d0, x,
+                                  lsum > 0.0f ? 1.0f / lsum : 0.0f);
+            } else if constexpr (SPLIT) {  // this wavefront's LDS slot
+                store_scaled<VPH>(&part_acc[wv][g * HD + d0], x, 1.0f);
+                if (owns_ml) {
+                    part_ml[wv][0][g] = h_s[1][g];
+                    part_ml[wv][1][g] = lsum;
+                }
+            } else {  // workspace slot, merged by decode_merge_kernel
+                store_scaled<VPH>(p.ws_acc + (prow * G + g) * HD + d0, x, 1.0f);
+                if (owns_ml)
+                    *reinterpret_cast<float2*>(p.ws_ml + (prow * G + g) * 2) = make_float2(h_s[1][g], lsum);
             }
-            float x[NF];
-#pragma unroll
-            for (int i = 0; i < NF; ++i) x[i] = final_out ? v[i] * sc : v[i];
-            if constexpr (NF == 4) *reinterpret_cast<float4*>(o) = make_float4(x[0], x[1], x[2], x[3]);
-            else if constexpr (NF == 2) *reinterpret_cast<float2*>(o) = make_float2(x[0], x[1]);
-            else o[0] = x[0];
         }
+
         wave_lds_sync();
 
         pos = stop;
@@ -603,7 +598,7 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
     const int w = blockIdx.x;
     const int h = w % Hq;
     const int range = w / Hq;
-    const WorkSplit split = build_split(p, P_s);
+    const WorkSplit split = build_split(p, P_s, true);
     if (range >= split.used) return;
     const int per = split.per;
     const int64_t row_elems = static_cast<int64_t>(p.Hkv) * HD;
@@ -928,7 +923,7 @@ int resident_waves(K kernel, int wpw, size_t lds, int max_per_simd) {
 // `wpw` of them, wpw dividing Hseg), then the merge.
 template <typename K>
 int launch_pair(K kern, int wpw, int max_per_simd, DecodeParams p, hipStream_t s, const char* name) {
-    const size_t lds = sizeof(int) * (static_cast<size_t>(p.B) + 1);
+    const size_t lds = sizeof(int) * (static_cast<size_t>(p.B) + 1);  // the block prefix
     const int waves = resident_waves(kern, wpw, lds, max_per_simd);
     // No more ranges than the largest possible work needs (small batches and
     // short contexts launch a small grid).

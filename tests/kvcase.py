@@ -104,13 +104,11 @@ def gpu_decode(skv, case, single: bool = False, poison: bool = True):
     qd = skv.DTYPE_BF16 if c["q_dtype"] == "bf16" else skv.DTYPE_FP32
     if single:
         assert c["B"] == 1 and c["q_dtype"] == "fp32"
-        wsb = int(skv.lib().skv_paged_attention_decode_workspace_bytes(c["Hq"], c["Hkv"], c["hd"]))
-        ws = skv.DeviceBuffer(wsb)
+        ws, wsb = skv.single_decode_workspace(c["Hq"], c["Hkv"], c["hd"])
         skv.paged_attention_decode(dq, dk, dv, c["total_blocks"], dt, dout, int(c["lens"][0]),
                                    c["bs"], c["Hq"], c["Hkv"], c["hd"], c["scale"], ws, wsb)
     else:
-        wsb = skv.decode_workspace_bytes(c["B"], c["Hq"], c["Hkv"], c["hd"])
-        ws = skv.DeviceBuffer(wsb)
+        ws, wsb = skv.decode_workspace(c["B"], c["Hq"], c["Hkv"], c["hd"])
         skv.paged_decode(dq, qd, dk, dv, c["total_blocks"], dt, c["tables"].shape[1], dl, c["B"],
                          c["Hq"], c["Hkv"], c["hd"], c["bs"], c["scale"], dout, ws, wsb)
     skv.synchronize()

@@ -46,8 +46,7 @@ def _step(skv, w, seed):
     d["t"] = skv.DeviceBuffer.from_numpy(w["tables"])
     d["l"] = skv.DeviceBuffer.from_numpy(w["lens"])
     d["p"] = skv.DeviceBuffer.from_numpy(w["lens"] - 1)
-    wsb = skv.decode_workspace_bytes(B, Hq, Hkv, hd)
-    d["ws"] = skv.DeviceBuffer(wsb)
+    d["ws"], wsb = skv.decode_workspace(B, Hq, Hkv, hd)
     mb = w["tables"].shape[1]
 
     def decode(fused=False):

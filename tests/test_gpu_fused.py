@@ -66,8 +66,7 @@ def _run(skv, c, fused, misalign=False):
     out_shape = (B, c["Hq"], c["hd"])
     dout = skv.DeviceBuffer(4 * int(np.prod(out_shape)))
     dout.upload(np.full(out_shape, np.nan, np.float32))
-    wsb = skv.decode_workspace_bytes(B, c["Hq"], c["Hkv"], c["hd"])
-    ws = skv.DeviceBuffer(wsb)
+    ws, wsb = skv.decode_workspace(B, c["Hq"], c["Hkv"], c["hd"])
     mb = c["tables"].shape[1]
     if fused:
         skv.paged_decode_append(dq, qd, kn_ptr, vn_ptr, kvd, dk, dv, c["total"], dt, mb, dl, B,
@@ -169,7 +168,6 @@ def test_single_sequence_fused_entry(gpu, L):
     v_row = rng.standard_normal((Hkv, hd), dtype=np.float32)
     q = rng.standard_normal((Hq, hd), dtype=np.float32)
     scale = 1.0 / math.sqrt(hd)
-    wsb = int(gpu.lib().skv_paged_attention_decode_workspace_bytes(Hq, Hkv, hd))
     results = []
     for fused in (True, False):
         dk, dv = gpu.DeviceBuffer.from_numpy(k_pool), gpu.DeviceBuffer.from_numpy(v_pool)
@@ -177,7 +175,7 @@ def test_single_sequence_fused_entry(gpu, L):
         dq = gpu.DeviceBuffer.from_numpy(q)
         dkr, dvr = gpu.DeviceBuffer.from_numpy(k_row), gpu.DeviceBuffer.from_numpy(v_row)
         dout = gpu.DeviceBuffer(4 * Hq * hd)
-        ws = gpu.DeviceBuffer(wsb)
+        ws, wsb = gpu.single_decode_workspace(Hq, Hkv, hd)
         if fused:
             gpu.paged_attention_decode_append(dq, dkr, dvr, gpu.DTYPE_FP32, dk, dv, total, dt, dout,
                                               L, bs, Hq, Hkv, hd, scale, ws, wsb)

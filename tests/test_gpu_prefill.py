@@ -97,8 +97,7 @@ def test_prefill_last_token_matches_decode(gpu):
     dq, dk, dv = (gpu.DeviceBuffer.from_numpy(a) for a in (q_last, c["kp"], c["vp"]))
     dt, dl = gpu.DeviceBuffer.from_numpy(c["tables"]), gpu.DeviceBuffer.from_numpy(c["lens"])
     dout = gpu.DeviceBuffer(4 * B * 32 * 128)
-    wsb = gpu.decode_workspace_bytes(B, 32, 8, 128)
-    ws = gpu.DeviceBuffer(wsb)
+    ws, wsb = gpu.decode_workspace(B, 32, 8, 128)
     gpu.paged_decode(dq, gpu.DTYPE_BF16, dk, dv, c["total"], dt, c["tables"].shape[1], dl, B, 32, 8,
                      128, 16, c["scale"], dout, ws, wsb)
     gpu.synchronize()
