@@ -195,6 +195,25 @@ int skv_paged_decode_append(const void* q, int q_dtype,
                             int block_size, float scale, float* out,
                             void* workspace, size_t workspace_bytes, void* stream);
 
+/* skv_paged_decode_append without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The partial results live in a library-owned device array of 24 MiB per GPU
+ * (held from the first use until the process ends); the grid uses as many
+ * ranges as fit in it (every benchmark shape fits its full persistent grid),
+ * and a shape with more query heads x head_dim than one range per head needs
+ * is refused with SKV_ERR_UNSUPPORTED.  Calls no allocation routine.  All
+ * calls on one GPU share that array: calls that overlap in time on one GPU
+ * (different streams, no ordering between them) race and must not be made. */
+int skv_paged_decode_append_noalloc(const void* q, int q_dtype,
+                                    const void* k_new, const void* v_new, int kv_dtype,
+                                    uint16_t* k_pool, uint16_t* v_pool,
+                                    int64_t total_blocks,
+                                    const int32_t* block_tables, int max_blocks_per_seq,
+                                    const int32_t* context_lens, int num_seqs,
+                                    int num_q_heads, int num_kv_heads, int head_dim,
+                                    int block_size, float scale, float* out, void* stream);
+
 /* Chunked prefill attention over the paged cache.  The query rows
  * seq_offsets[b] .. seq_offsets[b+1]-1 of q ([num_tokens][num_q_heads][head_dim],
  * q_dtype) are sequence b's chunk: the last n_b positions of its

@@ -79,6 +79,7 @@ struct DecodeParams {
     uint16_t* k_pool_w;    // the pools again, writable (the new rows are stored)
     uint16_t* v_pool_w;
     int merge_cw;          // output columns per merge workgroup (a multiple of 64)
+    int max_slots;         // (range, head group) pairs the workspace holds partials for
 };
 
 constexpr int kMaxHeadDim = 512;
@@ -879,12 +880,14 @@ struct WorkspaceLayout {
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Partial slots: 2 per (range, head group) with ranges * Hseg <= kMaxWaves,
-// each holding NH heads (NH = G for the MFMA kernel, 1 for the generic one).
-WorkspaceLayout workspace_layout(int B, int Hq, int Hkv, int HD) {
+// Partial slots: 2 per (range, head group), for at most `slots` (range, head
+// group) pairs (ranges * Hseg <= slots), each holding NH heads (NH = G for the
+// MFMA kernel, 1 for the generic one).  The public size query assumes the
+// largest persistent grid (kMaxWaves pairs).
+WorkspaceLayout workspace_layout(int B, int Hq, int Hkv, int HD, int slots = kMaxWaves) {
     WorkspaceLayout w{};
     const int G = Hq / std::max(Hkv, 1);
-    const size_t head_slots = 2 * static_cast<size_t>(kMaxWaves) * std::max(G, 1);
+    const size_t head_slots = 2 * static_cast<size_t>(slots) * std::max(G, 1);
     const size_t plan_ints = 3 + static_cast<size_t>(std::min(B, kMaxBatchPerLaunch)) + 1;
     w.plan_off = 0;
     w.ml_off = align256(sizeof(int32_t) * plan_ints);
@@ -928,7 +931,8 @@ int launch_pair(K kern, int wpw, int max_per_simd, DecodeParams p, hipStream_t s
     // No more ranges than the largest possible work needs (small batches and
     // short contexts launch a small grid).
     const int64_t max_work = static_cast<int64_t>(p.B) * p.max_blocks;
-    p.ranges = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(waves / p.Hseg, cdiv<int64_t>(max_work, p.min_per))));
+    p.ranges = static_cast<int>(std::max<int64_t>(
+        1, std::min<int64_t>({waves / p.Hseg, cdiv<int64_t>(max_work, p.min_per), p.max_slots / p.Hseg})));
     const unsigned groups = static_cast<unsigned>(p.ranges) * (p.Hseg / wpw);
     kern<<<groups, 64 * wpw, lds, s>>>(p);
     if (int rc = check_launch(name)) return rc;
@@ -1027,8 +1031,9 @@ int run_decode_chunk(DecodeParams p, int q_dtype, char* ws, const WorkspaceLayou
 // Batches larger than kMaxBatchPerLaunch run as consecutive launches on the
 // same stream (sequences are independent), reusing the workspace.
 int run_decode(DecodeParams p, int q_dtype, void* workspace, size_t workspace_bytes,
-               hipStream_t s) {
-    const WorkspaceLayout w = workspace_layout(p.B, p.Hq, p.Hkv, p.HD);
+               hipStream_t s, int slots = kMaxWaves) {
+    const WorkspaceLayout w = workspace_layout(p.B, p.Hq, p.Hkv, p.HD, slots);
+    p.max_slots = slots;
     if (workspace == nullptr || workspace_bytes < w.total)
         return set_error(SKV_ERR_WORKSPACE,
                          "decode workspace of %zu bytes is smaller than the %zu required",
@@ -1066,6 +1071,86 @@ int validate_geometry(const char* fn, int B, int Hq, int Hkv, int HD, int bs, fl
     SKV_REQUIRE(scale > 0.0f && std::isfinite(scale), "%s: scale must be positive and finite", fn);
     if (HD > kMaxHeadDim)
         return set_error(SKV_ERR_UNSUPPORTED, "%s: head_dim %d exceeds %d", fn, HD, kMaxHeadDim);
+    return SKV_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point (skv_paged_decode_append_noalloc):
+// the partial results live in this file-scope device array instead of a
+// caller workspace.  Each device holds its own copy from module load until the
+// process ends.  In host code `scratch` names a host-side stand-in, never a
+// device address: its device address comes from hipGetSymbolAddress, once per
+// device with that device current, and only that pointer is passed on.
+// Nothing in it must start at zero (every partial and the plan are written by
+// the attention kernel before the merge kernel reads them).
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = size_t(24) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int scratch_for_current_device(void** ptr) {
+    int dev = 0;
+    SKV_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return set_error(SKV_ERR_UNSUPPORTED, "skv_paged_decode_append_noalloc: device %d beyond %d", dev,
+                         kMaxScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* addr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || addr == nullptr)
+            return set_error(SKV_ERR_HIP, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = addr;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return SKV_OK;
+}
+
+// (range, head group) pairs whose partials fit in the scratch for this shape.
+int scratch_slots(int B, int Hq, int Hkv, int HD) {
+    int slots = kMaxWaves;
+    while (slots > 0 && workspace_layout(B, Hq, Hkv, HD, slots).total > kScratchBytes) slots -= 64;
+    return slots;
+}
+
+int fill_decode_append(DecodeParams& p, const char* fn, const void* q, int q_dtype, const void* k_new,
+                       const void* v_new, int kv_dtype, uint16_t* k_pool, uint16_t* v_pool,
+                       int64_t total_blocks, const int32_t* block_tables, int max_blocks_per_seq,
+                       const int32_t* context_lens, int num_seqs, int num_q_heads, int num_kv_heads,
+                       int head_dim, int block_size, float scale, float* out) {
+    SKV_REQUIRE(q && k_new && v_new && k_pool && v_pool && block_tables && context_lens && out,
+                "%s: invalid device pointers or attention dimensions", fn);
+    SKV_REQUIRE(q_dtype == SKV_DTYPE_BF16 || q_dtype == SKV_DTYPE_FP32, "%s: unknown query dtype %d", fn,
+                q_dtype);
+    SKV_REQUIRE(kv_dtype == SKV_DTYPE_BF16 || kv_dtype == SKV_DTYPE_FP32, "%s: unknown K/V dtype %d", fn,
+                kv_dtype);
+    SKV_REQUIRE(total_blocks > 0 && max_blocks_per_seq > 0, "%s: pool and table sizes must be positive", fn);
+    if (int rc = validate_geometry(fn, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, scale))
+        return rc;
+    p = DecodeParams{};
+    p.q = q;
+    p.k = k_pool;
+    p.v = v_pool;
+    p.total_blocks = total_blocks;
+    p.tables = block_tables;
+    p.max_blocks = max_blocks_per_seq;
+    p.lens = context_lens;
+    p.single_len = 0;
+    p.B = num_seqs;
+    p.Hq = num_q_heads;
+    p.Hkv = num_kv_heads;
+    p.HD = head_dim;
+    p.bs = block_size;
+    p.qscale = scale * 1.4426950408889634f;
+    p.out = out;
+    p.k_new = k_new;
+    p.v_new = v_new;
+    p.kv_new_fp32 = kv_dtype == SKV_DTYPE_FP32 ? 1 : 0;
+    p.k_pool_w = k_pool;
+    p.v_pool_w = v_pool;
     return SKV_OK;
 }
 
@@ -1122,39 +1207,38 @@ extern "C" int skv_paged_decode_append(const void* q, int q_dtype, const void* k
                                        int num_kv_heads, int head_dim, int block_size, float scale,
                                        float* out, void* workspace, size_t workspace_bytes,
                                        void* stream) {
-    SKV_REQUIRE(q && k_new && v_new && k_pool && v_pool && block_tables && context_lens && out,
-                "skv_paged_decode_append: invalid device pointers or attention dimensions");
-    SKV_REQUIRE(q_dtype == SKV_DTYPE_BF16 || q_dtype == SKV_DTYPE_FP32,
-                "skv_paged_decode_append: unknown query dtype %d", q_dtype);
-    SKV_REQUIRE(kv_dtype == SKV_DTYPE_BF16 || kv_dtype == SKV_DTYPE_FP32,
-                "skv_paged_decode_append: unknown K/V dtype %d", kv_dtype);
-    SKV_REQUIRE(total_blocks > 0 && max_blocks_per_seq > 0,
-                "skv_paged_decode_append: pool and table sizes must be positive");
-    if (int rc = validate_geometry("skv_paged_decode_append", num_seqs, num_q_heads, num_kv_heads,
-                                   head_dim, block_size, scale))
+    DecodeParams p;
+    if (int rc = fill_decode_append(p, "skv_paged_decode_append", q, q_dtype, k_new, v_new, kv_dtype, k_pool,
+                                    v_pool, total_blocks, block_tables, max_blocks_per_seq, context_lens,
+                                    num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, scale, out))
         return rc;
-    DecodeParams p{};
-    p.q = q;
-    p.k = k_pool;
-    p.v = v_pool;
-    p.total_blocks = total_blocks;
-    p.tables = block_tables;
-    p.max_blocks = max_blocks_per_seq;
-    p.lens = context_lens;
-    p.single_len = 0;
-    p.B = num_seqs;
-    p.Hq = num_q_heads;
-    p.Hkv = num_kv_heads;
-    p.HD = head_dim;
-    p.bs = block_size;
-    p.qscale = scale * 1.4426950408889634f;
-    p.out = out;
-    p.k_new = k_new;
-    p.v_new = v_new;
-    p.kv_new_fp32 = kv_dtype == SKV_DTYPE_FP32 ? 1 : 0;
-    p.k_pool_w = k_pool;
-    p.v_pool_w = v_pool;
     return run_decode(p, q_dtype, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int skv_paged_decode_append_noalloc(const void* q, int q_dtype, const void* k_new,
+                                               const void* v_new, int kv_dtype, uint16_t* k_pool,
+                                               uint16_t* v_pool, int64_t total_blocks,
+                                               const int32_t* block_tables, int max_blocks_per_seq,
+                                               const int32_t* context_lens, int num_seqs,
+                                               int num_q_heads, int num_kv_heads, int head_dim,
+                                               int block_size, float scale, float* out, void* stream) {
+    DecodeParams p;
+    if (int rc = fill_decode_append(p, "skv_paged_decode_append_noalloc", q, q_dtype, k_new, v_new, kv_dtype,
+                                    k_pool, v_pool, total_blocks, block_tables, max_blocks_per_seq,
+                                    context_lens, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
+                                    scale, out))
+        return rc;
+    // At least one range per head group (kv heads for the MFMA kernel, query
+    // heads for the generic one) must fit; more ranges are used up to the
+    // persistent grid as the scratch allows.
+    const int slots = scratch_slots(num_seqs, num_q_heads, num_kv_heads, head_dim);
+    if (slots < num_q_heads)
+        return set_error(SKV_ERR_UNSUPPORTED,
+                         "skv_paged_decode_append_noalloc: %d query heads x head_dim %d need more than the "
+                         "%zu-byte scratch", num_q_heads, head_dim, kScratchBytes);
+    void* ws = nullptr;
+    if (int rc = scratch_for_current_device(&ws)) return rc;
+    return run_decode(p, q_dtype, ws, kScratchBytes, static_cast<hipStream_t>(stream), slots);
 }
 
 extern "C" size_t skv_paged_attention_decode_workspace_bytes(int num_q_heads, int num_kv_heads,
