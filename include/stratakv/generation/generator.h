@@ -82,6 +82,15 @@ public:
     // Extensions (no counterpart in the reference).
     // Stream for all device work (a hipStream_t; nullptr = default stream).
     void set_stream(void* stream);
+    // The block table of sequence 0 in `layer` during the last generate /
+    // forced_logits call (the ids it used, in table order; empty when that
+    // call returned without running the model).
+    std::vector<int> last_block_table(std::size_t layer) const {
+        return layer < last_tables_.size() ? last_tables_[layer] : std::vector<int>{};
+    }
+    // Reseed the sampler's uniform stream (the reference seeds it from
+    // std::random_device, as the constructor here does).
+    void seed_sampler(std::uint32_t seed) { sampler_ = Sampler(config_.sampler, seed); }
     // Teacher forcing: tokens[0..n_prompt) are the prompt, then every later
     // token is fed in turn.  Returns the logits after each of the positions
     // n_prompt-1 .. tokens.size()-1, row-major [(tokens.size() - n_prompt + 1) x vocab].
@@ -92,11 +101,11 @@ private:
     void begin_sequence(std::size_t tokens);
     void end_sequence() noexcept;
     // One decode step: embedding of ids_[in_index], all layers, final norm,
-    // lm_head into `logits` (device [vocab]).
-    void step(int in_index, float* logits);
+    // lm_head into `logits` (device [vocab]); data errors go to *flags.
+    void step(int in_index, float* logits, std::int32_t* flags);
     // The prompt ids_[0 .. P): all P embeddings, every layer over the P rows
     // at once (TransformerBlock::prefill_into), then the logits of the last row.
-    void prompt_pass(std::size_t P, float* logits);
+    void prompt_pass(std::size_t P, float* logits, std::int32_t* flags);
     // Final norm + lm_head of one hidden row into `logits`.
     void logits_of(const float* x, float* logits);
     void raise_flags(std::int32_t flags) const;
@@ -116,9 +125,15 @@ private:
     std::optional<Tensor> logits_;           // [1, vocab] FP32
     std::int32_t* ids_ = nullptr;            // device token ids, capacity ids_capacity_
     std::size_t ids_capacity_ = 0;
-    std::int32_t* flags_ = nullptr;          // device SKV_FLAG_* bits
+    std::int32_t* flags_ = nullptr;          // device SKV_FLAG_* words: prompt, then sample / step pairs
+    std::size_t flags_capacity_ = 0;
     std::int32_t* host_ids_ = nullptr;       // page-locked copies of the chosen ids
     std::vector<void*> step_events_;         // ring of kLookahead + 1 events
+    // Free lists saved by begin_sequence and put back by end_sequence (the
+    // reference's SequenceGuard restores whole pool copies), and the tables
+    // of the last sequence.
+    std::vector<std::vector<int>> saved_free_lists_;
+    std::vector<std::vector<int>> last_tables_;
     double last_generation_ms_ = 0.0;
     double initialization_ms_ = 0.0;
 };

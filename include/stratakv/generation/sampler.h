@@ -48,6 +48,13 @@ public:
 
     const SamplerConfig& config() const noexcept { return config_; }
 
+    // Extension: the host uniform stream (one draw per sampled step).  The
+    // Generator saves it before each queued draw and puts it back to the state
+    // after the EOS step's draw, so the stream advances exactly as the
+    // reference's one-draw-per-step loop.
+    std::mt19937 rng_state() const { return rng_; }
+    void set_rng_state(const std::mt19937& state) const { rng_ = state; }
+
 private:
     SamplerConfig config_;
     mutable std::mt19937 rng_;

@@ -42,6 +42,14 @@ public:
     void free_block(int block_id);
 
     std::size_t free_count() const noexcept { return free_list_.size(); }
+    // Extension: the free stack (back() is handed out next), and putting a
+    // saved one back.  Generator uses them as the reference's SequenceGuard
+    // uses a pool copy (src/generation/generator.cpp:347-371), without
+    // copying the KV storage: after a generation the free list, and so the
+    // block ids of the next one, are what they were before it.  restore
+    // throws std::invalid_argument for an id out of range or listed twice.
+    const std::vector<int>& free_list() const noexcept { return free_list_; }
+    void restore_free_list(const std::vector<int>& ids);
     int block_size() const noexcept { return block_size_; }
     int total_blocks() const noexcept { return total_blocks_; }
     int num_kv_heads() const noexcept { return num_kv_heads_; }

@@ -32,6 +32,10 @@ namespace memory {
 struct SequenceState {
     int sequence_length = 0;         // tokens appended so far
     std::vector<int> physical_blocks;  // ordered block ids
+    // Extension: unique per allocate_sequence in the process, so a holder of
+    // uploaded block ids (DeviceBatch) notices a seq_id that was freed and
+    // allocated again.
+    std::uint64_t generation = 0;
 };
 
 class PageTable {
@@ -85,8 +89,10 @@ public:
     // Bind the batch to `seq_ids` (in this order) and upload their tables.
     void bind(const PageTable& pages, const std::vector<int>& seq_ids, void* stream = nullptr);
     // Upload what changed since the last bind/sync: block ids appended to the
-    // bound sequences, their context lengths and append positions.  Throws
-    // if a bound sequence was freed or shrank (rebind instead).
+    // bound sequences, their context lengths and append positions.  A bound
+    // seq_id that was freed and allocated again since (a new generation) has
+    // its whole row and length uploaded again.  Throws if a bound sequence is
+    // unknown or lost blocks without being re-allocated (rebind instead).
     void sync(const PageTable& pages, void* stream = nullptr);
 
     int num_seqs() const noexcept { return static_cast<int>(seq_ids_.size()); }
@@ -116,6 +122,7 @@ private:
     std::vector<int> seq_ids_;
     std::vector<int> uploaded_blocks_;
     std::vector<int> uploaded_len_;
+    std::vector<std::uint64_t> uploaded_gen_;  // SequenceState::generation of the uploaded row
 };
 
 }  // namespace memory

@@ -41,6 +41,12 @@ public:
     ~TransformerBlock() = default;
 
     void to(Device device);
+    // The reference's parity diagnostic: on sequence 0's first token,
+    // forward_into compares the paged attention output with a host
+    // double-precision restatement over the K/V read back from the pool and
+    // prints "[PARITY L0] paged_attention: max_diff = ..." to stderr (the
+    // reference also reports its other ops against its CPU path, which this
+    // build does not have).
     void set_parity_diagnostic(bool enabled) noexcept { parity_diagnostic_ = enabled; }
     // Stream for the device work of forward_into (a hipStream_t; nullptr =
     // the default stream).
@@ -108,6 +114,8 @@ private:
     layers::Linear up_proj_;
     layers::Linear down_proj_;
     bool parity_diagnostic_ = false;
+    void parity_check_attention(const Tensor& queries, const Tensor& context, const memory::SequenceState& state,
+                                const memory::BlockPool& pool) const;
     void* stream_ = nullptr;
     // Persistent GPU scratchpads, allocated by to(Device::GPU) and reused by
     // every forward_into; a block serves one request at a time.

@@ -149,3 +149,21 @@ void BlockPool::free_block(int block_id) {
 
 }  // namespace memory
 }  // namespace stratakv
+
+namespace stratakv {
+namespace memory {
+
+void BlockPool::restore_free_list(const std::vector<int>& ids) {
+    std::vector<unsigned char> seen(static_cast<std::size_t>(total_blocks_), 0);
+    for (int id : ids) {
+        if (id < 0 || id >= total_blocks_ || seen[static_cast<std::size_t>(id)])
+            throw std::invalid_argument("BlockPool::restore_free_list: invalid or repeated block id " +
+                                        std::to_string(id));
+        seen[static_cast<std::size_t>(id)] = 1;
+    }
+    free_list_ = ids;
+    is_free_ = std::move(seen);
+}
+
+}  // namespace memory
+}  // namespace stratakv

@@ -12,10 +12,14 @@
 #include <chrono>
 #include <climits>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <initializer_list>
 #include <limits>
 #include <stdexcept>
 #include <string>
+#include <random>
 #include <utility>
 
 #include "abi_check.h"
@@ -184,12 +188,17 @@ Generator::Generator(GeneratorConfig config, io::WeightMap weights)
     (void)kv_dim;
 
     for (auto& b : blocks_) b.to(Device::GPU);
+    // STRATAKV_PARITY=1 (src/generation/generator.cpp:33-36): the reference
+    // compares every layer with its CPU copy; this build has no CPU layers and
+    // runs each block's attention check instead.
+    if (const char* v = std::getenv("STRATAKV_PARITY"); v != nullptr && std::strcmp(v, "1") == 0) {
+        std::fprintf(stderr, "[PARITY] per-layer CPU comparison is not available in this build; "
+                             "checking each layer's paged attention on the first token\n");
+        for (auto& b : blocks_) b.set_parity_diagnostic(true);
+    }
     hidden_.emplace(std::vector<std::size_t>{1, h}, DataType::FP32, Device::GPU);
     normed_.emplace(std::vector<std::size_t>{1, h}, DataType::FP32, Device::GPU);
     logits_.emplace(std::vector<std::size_t>{1, config_.vocab_size}, DataType::FP32, Device::GPU);
-    void* p = nullptr;
-    detail::check(skv_malloc(&p, sizeof(std::int32_t)), "Generator: workspace");
-    flags_ = static_cast<std::int32_t*>(p);
     step_events_.assign(kLookahead + 2, nullptr);
     for (auto& e : step_events_) detail::check(skv_event_create(&e), "Generator: workspace");
     if (!weights.empty()) throw std::invalid_argument("Unexpected weight: " + weights.begin()->first);
@@ -233,9 +242,12 @@ void Generator::begin_sequence(std::size_t tokens) {
         (void)skv_device_synchronize();
         if (ids_) (void)skv_free(ids_);
         if (host_ids_) (void)skv_host_free(host_ids_);
+        if (flags_) (void)skv_free(flags_);
         ids_ = nullptr;
         host_ids_ = nullptr;
+        flags_ = nullptr;
         ids_capacity_ = 0;
+        flags_capacity_ = 0;
         void* d = nullptr;
         void* hp = nullptr;
         detail::check(skv_malloc(&d, tokens * sizeof(std::int32_t)), "Generator: token buffer");
@@ -243,7 +255,13 @@ void Generator::begin_sequence(std::size_t tokens) {
         detail::check(skv_host_alloc(&hp, tokens * sizeof(std::int32_t)), "Generator: token buffer");
         host_ids_ = static_cast<std::int32_t*>(hp);
         ids_capacity_ = tokens;
+        // One flag word for the prompt pass, then one per sample and per step.
+        detail::check(skv_malloc(&d, (2 * tokens + 2) * sizeof(std::int32_t)), "Generator: flags");
+        flags_ = static_cast<std::int32_t*>(d);
+        flags_capacity_ = 2 * tokens + 2;
     }
+    saved_free_lists_.resize(pools_.size());
+    for (std::size_t l = 0; l < pools_.size(); ++l) saved_free_lists_[l] = pools_[l].free_list();
     std::size_t done = 0;
     try {
         for (; done < pages_.size(); ++done) {
@@ -257,29 +275,38 @@ void Generator::begin_sequence(std::size_t tokens) {
     }
 }
 
+// Frees sequence 0 in every layer and puts each pool's free list back as it
+// was before begin_sequence, so consecutive generations use the same block
+// ids in the same order, as after the reference's SequenceGuard restore
+// (src/generation/generator.cpp:347-371, 639).
 void Generator::end_sequence() noexcept {
     (void)skv_stream_synchronize(stream_);
+    last_tables_.assign(pages_.size(), {});
     for (std::size_t l = 0; l < pages_.size(); ++l) {
         try {
-            if (pages_[l].has_sequence(0)) pages_[l].free_sequence(0, pools_[l]);
+            if (pages_[l].has_sequence(0)) {
+                last_tables_[l] = pages_[l].get_state(0).physical_blocks;
+                pages_[l].free_sequence(0, pools_[l]);
+            }
+            if (l < saved_free_lists_.size()) pools_[l].restore_free_list(saved_free_lists_[l]);
         } catch (...) {
         }
     }
 }
 
-void Generator::step(int in_index, float* logits) {
+void Generator::step(int in_index, float* logits, std::int32_t* flags) {
     const int dtype = embeddings_->dtype() == DataType::BF16 ? SKV_DTYPE_BF16 : SKV_DTYPE_FP32;
     const int h = static_cast<int>(config_.hidden_dim);
     const int vocab = static_cast<int>(config_.vocab_size);
     auto* x = static_cast<float*>(hidden_->raw_data());
-    detail::check(skv_embedding_f32(embeddings_->raw_data(), dtype, vocab, h, ids_, in_index, x, flags_, stream_),
+    detail::check(skv_embedding_f32(embeddings_->raw_data(), dtype, vocab, h, ids_, in_index, x, flags, stream_),
                   "Generator: embedding");
     for (std::size_t l = 0; l < blocks_.size(); ++l)
         blocks_[l].forward_into(*hidden_, *hidden_, 0, pages_[l], pools_[l], true);
     if (logits != nullptr) logits_of(x, logits);
 }
 
-void Generator::prompt_pass(std::size_t P, float* logits) {
+void Generator::prompt_pass(std::size_t P, float* logits, std::int32_t* flags) {
     const int dtype = embeddings_->dtype() == DataType::BF16 ? SKV_DTYPE_BF16 : SKV_DTYPE_FP32;
     const int h = static_cast<int>(config_.hidden_dim);
     const int vocab = static_cast<int>(config_.vocab_size);
@@ -290,7 +317,7 @@ void Generator::prompt_pass(std::size_t P, float* logits) {
     for (std::size_t i = 0; i < P; i += kEmbedRows)
         detail::check(skv_embedding_rows_f32(embeddings_->raw_data(), dtype, vocab, h, ids_, static_cast<int>(i),
                                              static_cast<int>(std::min(kEmbedRows, P - i)),
-                                             rows + i * config_.hidden_dim, flags_, stream_),
+                                             rows + i * config_.hidden_dim, flags, stream_),
                       "Generator: embedding");
     for (std::size_t l = 0; l < blocks_.size(); ++l)
         blocks_[l].prefill_into(*prompt_rows_, *prompt_rows_, 0, pages_[l], pools_[l]);
@@ -325,7 +352,10 @@ std::vector<int> Generator::generate(const std::vector<int>& prompt, int max_new
     if (prompt.empty() || max_new_tokens < 0)
         throw std::invalid_argument("Generator: nonempty prompt and nonnegative max required");
     validate_prompt(prompt, static_cast<std::size_t>(max_new_tokens));
-    if (max_new_tokens == 0 || prompt.back() == config_.eos_token_id) return prompt;
+    if (max_new_tokens == 0 || prompt.back() == config_.eos_token_id) {
+        last_tables_.clear();
+        return prompt;
+    }
     const std::size_t P = prompt.size();
     const std::size_t required = P + static_cast<std::size_t>(max_new_tokens);
     const auto bs = static_cast<std::size_t>(config_.block_size);
@@ -339,13 +369,22 @@ std::vector<int> Generator::generate(const std::vector<int>& prompt, int max_new
     try {
         for (std::size_t i = 0; i < P; ++i) host_ids_[i] = prompt[i];
         detail::check(skv_memcpy_h2d_async(ids_, host_ids_, P * sizeof(std::int32_t), stream_), "Generator: prompt");
-        detail::check(skv_memset_d8(flags_, 0, sizeof(std::int32_t), stream_), "Generator: flags");
+        // Flag words: [0] the prompt pass; for generated step s, [1 + 2s] its
+        // token choice and [2 + 2s] the step that embeds that token and makes
+        // the next logits.  Only the words of steps up to an EOS count: steps
+        // queued past it never ran in the reference.
+        const std::size_t words = 2 * static_cast<std::size_t>(max_new_tokens) + 1;
+        detail::check(skv_memset_d8(flags_, 0, words * sizeof(std::int32_t), stream_), "Generator: flags");
         auto* logits = static_cast<float*>(logits_->raw_data());
         const int vocab = static_cast<int>(config_.vocab_size);
-        if (P >= 2) prompt_pass(P, logits);
-        else step(0, logits);
+        if (P >= 2) prompt_pass(P, logits, flags_);
+        else step(0, logits, flags_);
 
         const int R = static_cast<int>(step_events_.size());
+        // The sampler's stream before each queued draw (a ring as deep as the
+        // lookahead), to put it back to the state after the EOS step's draw.
+        const bool draws = sampler_.config().temperature != 0.0f && vocab >= 2;
+        std::vector<std::mt19937> rng_before(draws ? static_cast<std::size_t>(R) : 0);
         int checked = 0;      // generated tokens the host has read
         bool stop = false;    // EOS seen at generated index `checked - 1`
         int queued = 0;       // generated tokens queued
@@ -365,7 +404,8 @@ std::vector<int> Generator::generate(const std::vector<int>& prompt, int max_new
         };
         for (int s = 0; s < max_new_tokens && !stop; ++s) {
             const int pos = static_cast<int>(P) + s;
-            sampler_.sample_into(logits, vocab, ids_, pos, flags_, stream_);
+            if (draws) rng_before[s % R] = sampler_.rng_state();
+            sampler_.sample_into(logits, vocab, ids_, pos, flags_ + 1 + 2 * s, stream_);
             detail::check(skv_memcpy_d2h_async(host_ids_ + pos, ids_ + pos, sizeof(std::int32_t), stream_),
                           "Generator: token copy");
             detail::check(skv_event_record(step_events_[s % R], stream_), "Generator: token copy");
@@ -373,12 +413,17 @@ std::vector<int> Generator::generate(const std::vector<int>& prompt, int max_new
             while (!stop && checked < queued && read_one(queued - checked > kLookahead)) {
             }
             if (stop || s + 1 == max_new_tokens) break;
-            step(pos, logits);  // embeds the token just chosen
+            step(pos, logits, flags_ + 2 + 2 * s);  // embeds the token just chosen
         }
         while (!stop && checked < queued) read_one(true);
+        // Draws made for steps queued past the EOS step are taken back.
+        if (draws && queued > checked) sampler_.set_rng_state(rng_before[checked % R]);
         detail::check(skv_stream_synchronize(stream_), "Generator: generate");
+        std::vector<std::int32_t> flag_words(2 * static_cast<std::size_t>(checked));
+        detail::check(skv_memcpy_d2h(flag_words.data(), flags_, flag_words.size() * sizeof(std::int32_t), stream_),
+                      "Generator: flags");
         std::int32_t flags = 0;
-        detail::check(skv_memcpy_d2h(&flags, flags_, sizeof(flags), stream_), "Generator: flags");
+        for (std::int32_t f : flag_words) flags |= f;
         raise_flags(flags);
         for (int s = 0; s < checked; ++s) result.push_back(host_ids_[P + s]);
     } catch (...) {
@@ -406,9 +451,9 @@ std::vector<float> Generator::forced_logits(const std::vector<int>& tokens, std:
         for (std::size_t i = 0; i < N; ++i) host_ids_[i] = tokens[i];
         detail::check(skv_memcpy_h2d_async(ids_, host_ids_, N * sizeof(std::int32_t), stream_), "Generator: tokens");
         detail::check(skv_memset_d8(flags_, 0, sizeof(std::int32_t), stream_), "Generator: flags");
-        if (n_prompt >= 2) prompt_pass(n_prompt, base);
-        else step(0, base);
-        for (std::size_t r = 1; r < rows; ++r) step(static_cast<int>(n_prompt - 1 + r), base + r * vocab);
+        if (n_prompt >= 2) prompt_pass(n_prompt, base, flags_);
+        else step(0, base, flags_);
+        for (std::size_t r = 1; r < rows; ++r) step(static_cast<int>(n_prompt - 1 + r), base + r * vocab, flags_);
         detail::check(skv_stream_synchronize(stream_), "Generator: forced_logits");
         detail::check(skv_memcpy_d2h(out.data(), base, out.size() * sizeof(float), stream_), "Generator: logits");
         std::int32_t flags = 0;

@@ -3,6 +3,7 @@
 #include "stratakv/memory/page_table.h"
 
 #include <algorithm>
+#include <atomic>
 #include <limits>
 #include <string>
 #include <utility>
@@ -12,6 +13,11 @@
 namespace stratakv {
 namespace memory {
 namespace {
+
+std::uint64_t next_generation() noexcept {
+    static std::atomic<std::uint64_t> counter{0};
+    return ++counter;
+}
 
 SequenceState& checked_lookup(std::unordered_map<int, SequenceState>& table, int seq_id,
                               const char* caller) {
@@ -83,6 +89,7 @@ void PageTable::allocate_sequence(int seq_id, BlockPool& pool) {
                                  " already exists");
     SequenceState state;
     state.physical_blocks.push_back(pool.allocate_block());  // the first block, eagerly
+    state.generation = next_generation();
     table_.emplace(seq_id, std::move(state));
     device_table_dirty_ = true;
 }
@@ -220,6 +227,7 @@ void DeviceBatch::bind(const PageTable& pages, const std::vector<int>& seq_ids, 
     seq_ids_ = seq_ids;
     uploaded_blocks_.assign(seq_ids.size(), 0);
     uploaded_len_.assign(seq_ids.size(), -1);
+    uploaded_gen_.assign(seq_ids.size(), 0);
     sync(pages, stream);
 }
 
@@ -234,13 +242,18 @@ void DeviceBatch::sync(const PageTable& pages, void* stream) {
     };
     for (std::size_t i = 0; i < seq_ids_.size(); ++i) {
         const SequenceState& st = pages.get_state(seq_ids_[i]);
+        if (st.generation != uploaded_gen_[i]) {  // bound anew, or freed and allocated again
+            uploaded_blocks_[i] = 0;
+            uploaded_len_[i] = -1;
+            uploaded_gen_[i] = st.generation;
+        }
         const int nb = static_cast<int>(st.physical_blocks.size());
         if (nb > max_blocks_)
             throw std::length_error("DeviceBatch::sync: sequence " + std::to_string(seq_ids_[i]) +
                                     " has more blocks than max_blocks_per_seq");
         if (nb < uploaded_blocks_[i])
             throw std::logic_error("DeviceBatch::sync: sequence " + std::to_string(seq_ids_[i]) +
-                                   " lost blocks; rebind the batch");
+                                   " lost blocks without being re-allocated; rebind the batch");
         for (int k = uploaded_blocks_[i]; k < nb; ++k)
             add(i * static_cast<std::size_t>(max_blocks_) + static_cast<std::size_t>(k), st.physical_blocks[k]);
         uploaded_blocks_[i] = nb;

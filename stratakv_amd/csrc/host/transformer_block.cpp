@@ -7,6 +7,10 @@
 // output-major rows, else as the separate kernels of skv_layer_ops.hip.
 #include "stratakv/models/transformer_block.h"
 
+#include <cstring>
+
+#include <cstdio>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -90,6 +94,66 @@ Tensor TransformerBlock::forward(const Tensor& hidden_states, int seq_id, memory
     throw std::runtime_error(
         "TransformerBlock::forward: the CPU path is not part of this build; move the block and "
         "the hidden states to Device::GPU");
+}
+
+// The reference's STRATAKV parity diagnostic (src/models/transformer_block.cpp:
+// 63-80, 405-526) compares every op of sequence 0's first token with its CPU
+// path.  This build has no CPU forward, so it checks the op it replaces: the
+// paged attention output against a double-precision two-pass softmax over
+// the K/V read back from the pool, printed in the reference's report format.
+void TransformerBlock::parity_check_attention(const Tensor& queries, const Tensor& context,
+                                              const memory::SequenceState& state,
+                                              const memory::BlockPool& pool) const {
+    detail::check(skv_stream_synchronize(stream_), "parity diagnostic");
+    const int Hq = static_cast<int>(attention_.num_heads()), Hkv = static_cast<int>(attention_.num_kv_heads());
+    const int hd = static_cast<int>(attention_.head_dim()), bs = pool.block_size();
+    const int L = state.sequence_length;
+    std::vector<float> q(static_cast<std::size_t>(Hq) * hd), gpu(q.size());
+    detail::check(skv_memcpy_d2h(q.data(), queries.raw_data(), q.size() * sizeof(float), nullptr), "parity diagnostic");
+    detail::check(skv_memcpy_d2h(gpu.data(), context.raw_data(), gpu.size() * sizeof(float), nullptr),
+                  "parity diagnostic");
+    const std::size_t blk = pool.block_elements();
+    const std::size_t nb = static_cast<std::size_t>((L + bs - 1) / bs);
+    std::vector<std::uint16_t> k(nb * blk), v(nb * blk);
+    for (std::size_t i = 0; i < nb; ++i) {
+        const std::size_t off = static_cast<std::size_t>(state.physical_blocks[i]) * blk;
+        detail::check(skv_memcpy_d2h(k.data() + i * blk, pool.key_cache() + off, blk * 2, nullptr), "parity diagnostic");
+        detail::check(skv_memcpy_d2h(v.data() + i * blk, pool.value_cache() + off, blk * 2, nullptr), "parity diagnostic");
+    }
+    auto widen = [](std::uint16_t b) {
+        const std::uint32_t bits = static_cast<std::uint32_t>(b) << 16;
+        float f;
+        std::memcpy(&f, &bits, sizeof f);
+        return static_cast<double>(f);
+    };
+    auto row = [&](int t, int kvh) { return (static_cast<std::size_t>(t) * Hkv + kvh) * hd; };  // within the gathered blocks
+    const double scale = 1.0 / std::sqrt(static_cast<double>(hd));
+    std::vector<float> cpu(gpu.size());
+    std::vector<double> sc(static_cast<std::size_t>(L));
+    for (int h = 0; h < Hq; ++h) {
+        const int kvh = h / (Hq / Hkv);
+        double mx = -INFINITY;
+        for (int t = 0; t < L; ++t) {
+            double d = 0.0;
+            for (int e = 0; e < hd; ++e) d += q[static_cast<std::size_t>(h) * hd + e] * widen(k[row(t, kvh) + e]);
+            sc[t] = d * scale;
+            mx = std::max(mx, sc[t]);
+        }
+        double den = 0.0;
+        for (int t = 0; t < L; ++t) den += (sc[t] = std::exp(sc[t] - mx));
+        for (int e = 0; e < hd; ++e) {
+            double o = 0.0;
+            for (int t = 0; t < L; ++t) o += sc[t] / den * widen(v[row(t, kvh) + e]);
+            cpu[static_cast<std::size_t>(h) * hd + e] = static_cast<float>(o);
+        }
+    }
+    float max_diff = 0.0f;
+    for (std::size_t i = 0; i < gpu.size(); ++i) max_diff = std::max(max_diff, std::fabs(gpu[i] - cpu[i]));
+    std::fprintf(stderr,
+                 "[PARITY L0] paged_attention: max_diff = %.9g, gpu_sample[0..2] = [%.9g, %.9g, %.9g], "
+                 "cpu_sample[0..2] = [%.9g, %.9g, %.9g]\n",
+                 max_diff, gpu[0], gpu.size() > 1 ? gpu[1] : 0.0f, gpu.size() > 2 ? gpu[2] : 0.0f, cpu[0],
+                 cpu.size() > 1 ? cpu[1] : 0.0f, cpu.size() > 2 ? cpu[2] : 0.0f);
 }
 
 void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output, int seq_id,
@@ -221,6 +285,8 @@ void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output,
                       1.0f / std::sqrt(static_cast<float>(head_dim)), ws.raw_data(),
                       ws.num_elements() * ws.element_size(), s),
                   "forward_into: KV append + paged attention");
+    if (parity_diagnostic_ && seq_id == 0 && append_tokens && logical_position == 0)
+        parity_check_attention(queries, context, state, block_pool);
 
     // o_proj + residual: reads hidden_states before output is written
     // (aliasing-safe).  down holds h = hidden + attention output.

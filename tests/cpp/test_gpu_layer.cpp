@@ -91,6 +91,30 @@ void device_tables() {
             check(same, "DeviceBatch row " + std::to_string(i) + " step " + std::to_string(step));
         }
     }
+    // A bound seq_id freed and allocated again between syncs, with at least as
+    // many blocks as were uploaded: its block went to another sequence, so the
+    // row must be re-uploaded whole (stale ids would send the fused append
+    // into a block the other sequence owns).
+    {
+        BlockPool p2(16, 4, 2, 64, Device::GPU);
+        PageTable t2;
+        t2.allocate_sequence(7, p2);  // block 0
+        DeviceBatch b2(2, 8);
+        b2.bind(t2, {7});
+        const int old_first = t2.get_state(7).physical_blocks[0];
+        t2.free_sequence(7, p2);      // block 0 back on top of the free stack
+        t2.allocate_sequence(8, p2);  // takes block 0
+        t2.allocate_sequence(7, p2);  // a different block
+        for (int k = 0; k < 4; ++k) t2.append_token(7, p2);
+        const auto& st = t2.get_state(7);
+        check(st.physical_blocks[0] != old_first, "re-allocated sequence got a different block");
+        b2.sync(t2);
+        ok_or_die(skv_device_synchronize(), "sync");
+        const auto row = download<int32_t>(b2.tables(), st.physical_blocks.size());
+        const auto len = download<int32_t>(b2.context_lens(), 1);
+        check(std::vector<int>(row.begin(), row.end()) == st.physical_blocks && len[0] == st.sequence_length,
+              "DeviceBatch re-uploads the row of a re-allocated seq_id");
+    }
 }
 
 void pool_copy() {

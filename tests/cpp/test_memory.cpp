@@ -181,6 +181,26 @@ void random_traces_match_oracle() {
     }
 }
 
+// SequenceState::generation: unique per allocate_sequence, unchanged by
+// append_token, new after free + allocate of the same seq_id (DeviceBatch
+// relies on it to re-upload a re-allocated sequence's row).
+void sequence_generations() {
+    BlockPool pool(8, 4);
+    PageTable pt;
+    pt.allocate_sequence(3, pool);
+    pt.allocate_sequence(4, pool);
+    const auto g3 = pt.get_state(3).generation, g4 = pt.get_state(4).generation;
+    check(g3 != 0 && g4 != 0 && g3 != g4, "generations are nonzero and distinct");
+    for (int i = 0; i < 9; ++i) pt.append_token(3, pool);
+    check(pt.get_state(3).generation == g3, "append_token keeps the generation");
+    pt.free_sequence(3, pool);
+    pt.allocate_sequence(3, pool);
+    check(pt.get_state(3).generation != g3 && pt.get_state(3).generation != g4,
+          "a re-allocated seq_id gets a new generation");
+    PageTable copy(pt);
+    check(copy.get_state(3).generation == pt.get_state(3).generation, "a copy keeps the generations");
+}
+
 void tensor_rules() {
     using stratakv::DataType;
     using stratakv::Tensor;
@@ -228,6 +248,7 @@ int main() {
         phase4_pages();
         errors_and_lifo();
         random_traces_match_oracle();
+        sequence_generations();
         tensor_rules();
     } catch (const std::exception& e) {
         std::fprintf(stderr, "FAIL: unexpected exception %s\n", e.what());

@@ -9,7 +9,8 @@
 //       and reports its dtype.
 //   tool_model transpose IN OUT_F IN_F OUT
 //       io::load_linear_bf16_transposed of an FP32 [OUT_F, IN_F] file.
-//   tool_model generate <ckpt> MAX_NEW EOS [--host-loader] [--temp T]
+//   tool_model generate <ckpt> MAX_NEW EOS [--host-loader] [--temp T] [--top-k K] [--top-p P]
+//       [--repeat N] [--seed S] [--first-max M] -- PROMPT...
 //       [--top-k K] [--top-p P] [--repeat N] -- PROMPT...
 //       Generator::generate; prints tokens and timings.
 //   tool_model forced <ckpt> N_PROMPT OUT [--host-loader] -- TOKENS...
@@ -160,6 +161,8 @@ struct GenArgs {
     bool host_loader = false;
     generation::SamplerConfig sampler{0.0f, 0, 1.0f};
     int repeat = 1;
+    long long seed = -1;  // >= 0: Generator::seed_sampler
+    int first_max = -1;   // >= 0: max_new of the first call (later calls use MAX_NEW)
     std::vector<int> tokens;
 };
 
@@ -177,6 +180,8 @@ GenArgs parse_gen(int first, int argc, char** argv) {
         else if (s == "--top-k") a.sampler.top_k = std::stoi(argv[++i]);
         else if (s == "--top-p") a.sampler.top_p = std::stof(argv[++i]);
         else if (s == "--repeat") a.repeat = std::stoi(argv[++i]);
+        else if (s == "--seed") a.seed = std::stoll(argv[++i]);
+        else if (s == "--first-max") a.first_max = std::stoi(argv[++i]);
     }
     for (; i < argc; ++i) a.tokens.push_back(std::stoi(argv[i]));
     return a;
@@ -209,13 +214,29 @@ int cmd_generate(int argc, char** argv) {
         auto cfg = config_for(l.dims, eos);
         cfg.sampler = a.sampler;
         generation::Generator gen(cfg, std::move(l.weights));
+        if (a.seed >= 0) gen.seed_sampler(static_cast<std::uint32_t>(a.seed));
         std::vector<int> out;
+        std::vector<std::vector<int>> runs, tables;
         std::vector<double> gen_ms;
         for (int r = 0; r < a.repeat; ++r) {
-            out = gen.generate(a.tokens, max_new);
+            out = gen.generate(a.tokens, r == 0 && a.first_max >= 0 ? a.first_max : max_new);
+            runs.push_back(out);
+            tables.push_back(gen.last_block_table(0));
             gen_ms.push_back(gen.last_generation_ms());
         }
-        std::printf("{\"ok\": true, \"tokens\": [");
+        std::printf("{\"ok\": true, \"runs\": [");
+        for (std::size_t r = 0; r < runs.size(); ++r) {
+            std::printf("%s[", r ? ", " : "");
+            for (std::size_t i = 0; i < runs[r].size(); ++i) std::printf("%s%d", i ? ", " : "", runs[r][i]);
+            std::printf("]");
+        }
+        std::printf("], \"tables\": [");
+        for (std::size_t r = 0; r < tables.size(); ++r) {
+            std::printf("%s[", r ? ", " : "");
+            for (std::size_t i = 0; i < tables[r].size(); ++i) std::printf("%s%d", i ? ", " : "", tables[r][i]);
+            std::printf("]");
+        }
+        std::printf("], \"tokens\": [");
         for (std::size_t i = 0; i < out.size(); ++i) std::printf("%s%d", i ? ", " : "", out[i]);
         std::printf("], \"load_ms\": %.3f, \"payload_bytes\": %zu, \"decode_ms\": %.3f, \"init_ms\": %.3f, "
                     "\"gen_ms\": [",

@@ -25,6 +25,7 @@ import numpy as np
 import pytest
 
 import stratakv_amd as skv
+import oracle
 from oracle import sampler as osamp
 
 pytestmark = pytest.mark.gpu
@@ -310,6 +311,67 @@ def test_generate_repeatable_and_errors(gpu, ckpt_dir):
     # a prompt ending in EOS is returned as is
     res = tool("generate", path, 40, gen[0], "--", 3, gen[0])
     assert res["tokens"] == [3, gen[0]]
+
+
+def test_parity_diagnostic_reports_attention(gpu, ckpt_dir):
+    """STRATAKV_PARITY=1: every layer's paged attention on the first token is
+    compared with a host double-precision restatement and reported on stderr
+    (src/models/transformer_block.cpp:63-80 prints the same line format)."""
+    golden = _golden("mini")
+    path = _checkpoint("mini", ckpt_dir, golden)
+    env = dict(os.environ, STRATAKV_PARITY="1")
+    p = subprocess.run([TOOL, "generate", path, "4", "-1", "--", "5"], stdout=subprocess.PIPE,
+                       stderr=subprocess.PIPE, text=True, timeout=600, env=env)
+    assert p.returncode == 0 and json.loads(p.stdout.strip().splitlines()[-1])["ok"], p.stderr
+    diffs = [float(line.split("max_diff = ")[1].split(",")[0]) for line in p.stderr.splitlines()
+             if line.startswith("[PARITY L0] paged_attention: max_diff = ")]
+    assert len(diffs) == golden["checkpoint"]["layers"], p.stderr
+    assert max(diffs) < 1e-5, diffs
+
+
+def test_consecutive_generations_use_the_same_blocks(gpu, ckpt_dir):
+    """The reference restores every layer's pool after generate (SequenceGuard,
+    src/generation/generator.cpp:347-371), so each generation on a fresh
+    Generator allocates exactly as a fresh pool would: the table of
+    allocate_sequence + one append_token per position that is processed (the
+    prompt and every generated token but the last), on the oracle's
+    restatement of BlockPool / PageTable, twice in a row."""
+    from oracle import OP_ALLOC_SEQ, OP_APPEND
+    golden = _golden("mini")
+    path = _checkpoint("mini", ckpt_dir, golden)
+    prompt = golden["prompt"]
+    res = tool("generate", path, 40, -1, "--repeat", 3, "--", *prompt)
+    assert res["ok"], res
+    n_appends = len(res["tokens"]) - 1
+    ops = [(OP_ALLOC_SEQ, 0)] + [(OP_APPEND, 0)] * n_appends
+    _, lens, blocks, _ = oracle.pool_trace(1024, 16, ops, 1, 64)
+    want = blocks[0, : -(-int(lens[0]) // 16)].tolist()
+    assert res["tables"] == [want, want, want], (res["tables"], want)
+    assert res["free_blocks"] == 1024 * golden["checkpoint"]["layers"]
+
+
+def test_sampled_generate_stops_the_stream_at_eos(gpu, ckpt_dir):
+    """Sampling draws once per generated step, up to and including the EOS
+    step, as the reference's loop does (src/generation/generator.cpp:717-788):
+    the host queues steps ahead of the device, and the draws it made for steps
+    past the EOS are taken back.  A generator that stops at EOS after e + 1
+    tokens and one whose first call asks for exactly e + 1 tokens (no EOS) must
+    then produce the same second generation from the same seed."""
+    golden = _golden("mini")
+    path = _checkpoint("mini", ckpt_dir, golden)
+    prompt = golden["prompt"]
+    base = tool("generate", path, 40, -1, "--temp", 1.0, "--seed", 7, "--", *prompt)
+    assert base["ok"], base
+    gen = base["tokens"][len(prompt):]
+    for pick in (2, 11):
+        eos = gen[pick]
+        e = gen.index(eos)  # first occurrence: the EOS step
+        stopped = tool("generate", path, 40, eos, "--temp", 1.0, "--seed", 7, "--repeat", 2, "--", *prompt)
+        exact = tool("generate", path, 40, eos, "--temp", 1.0, "--seed", 7, "--repeat", 2, "--first-max", e + 1,
+                     "--", *prompt)
+        assert stopped["ok"] and exact["ok"]
+        assert stopped["runs"][0] == exact["runs"][0] == prompt + gen[: e + 1], (pick, e)
+        assert stopped["runs"][1] == exact["runs"][1], (pick, e, stopped["runs"][1], exact["runs"][1])
 
 
 @pytest.mark.timeout(400)  # writes a 2.2 GB checkpoint first (~30 s on 8 cores)
