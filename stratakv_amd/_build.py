@@ -9,6 +9,10 @@ Everything is compiled in-tree so the built files travel with the source tree:
   ``build/bin/bench_*`` -- the C++ benchmark drivers under ``stratakv_amd/csrc/bench``.
 * ``oracle/liboracle.so`` and, when the StrataKV sources are present,
   ``oracle/_ref/libstratakv_ref.so`` -- test infrastructure (``oracle/Makefile``).
+* ``build/asan/`` -- test infrastructure: the C++ host layer and the host-side
+  test programs built with AddressSanitizer and UndefinedBehaviorSanitizer
+  (g++, no GPU code), linked against ``tests/cpp/abi_host_stand_in.cpp``
+  instead of the library (``python -m stratakv_amd._build asan``).
 """
 from __future__ import annotations
 
@@ -93,7 +97,9 @@ def build_cpp_tests() -> list[str]:
     """Compile tests/cpp/*.cpp against the library (and the oracle, for traces)."""
     os.makedirs(BIN, exist_ok=True)
     outs, cmds = [], []
-    for src in sorted(glob.glob(os.path.join(ROOT, "tests", "cpp", "*.cpp"))):
+    srcs = glob.glob(os.path.join(ROOT, "tests", "cpp", "test_*.cpp")) + \
+        glob.glob(os.path.join(ROOT, "tests", "cpp", "tool_*.cpp"))
+    for src in sorted(srcs):
         exe = os.path.join(BIN, os.path.splitext(os.path.basename(src))[0])
         cmds.append([HIPCC, "-O2", "-std=c++17", f"-I{INCLUDE}", f"-I{ORACLE}", "-x", "c++", src,
                      f"-L{PKG}", "-lstratakv_amd", f"-Wl,-rpath,{PKG}",
@@ -124,13 +130,59 @@ def build_oracle() -> None:
         _run(["make", "-B", f"-j{_jobs()}", "-C", ORACLE, "ref", f"REF={REFERENCE}"])
 
 
+ASAN = os.path.join(ROOT, "build", "asan")
+# Programs of tests/cpp whose code paths are host-only (or run over the host
+# stand-in of the C ABI); test_gpu_layer needs the kernels and is left out.
+ASAN_PROGRAMS = ("test_memory", "test_host_layer", "tool_model")
+SANITIZE = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer"]
+
+
+def build_sanitized() -> list[str]:
+    """Test infrastructure: the host layer (BlockPool, PageTable, DeviceBatch,
+    the safetensors loader, Sampler, Generator, Tensor) and the host test
+    programs under AddressSanitizer + UndefinedBehaviorSanitizer.  Built with
+    g++ alone; the C ABI comes from tests/cpp/abi_host_stand_in.cpp (host
+    memory, copies and events; every kernel entry point reports
+    SKV_ERR_UNSUPPORTED), so nothing here touches a GPU."""
+    obj_dir = os.path.join(ASAN, "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    flags = ["-O1", "-g", "-std=c++17", "-Wall", *SANITIZE, f"-I{INCLUDE}", f"-I{ORACLE}"]
+    objs, cmds = [], []
+    for src in sorted(glob.glob(os.path.join(CSRC, "host", "*.cpp"))) + \
+            [os.path.join(ROOT, "tests", "cpp", "abi_host_stand_in.cpp")]:
+        obj = os.path.join(obj_dir, os.path.basename(src) + ".o")
+        cmds.append([CXX, *flags, "-c", src, "-o", obj])
+        objs.append(obj)
+    oracle_obj = os.path.join(obj_dir, "oracle.c.o")
+    cmds.append([os.environ.get("CC", "gcc"), "-O1", "-g", "-std=c11", *SANITIZE, "-c",
+                 os.path.join(ORACLE, "oracle.c"), "-o", oracle_obj])
+    tests = []
+    for name in ASAN_PROGRAMS:
+        obj = os.path.join(obj_dir, name + ".cpp.o")
+        cmds.append([CXX, *flags, "-c", os.path.join(ROOT, "tests", "cpp", name + ".cpp"), "-o", obj])
+        tests.append((name, obj))
+    _run_all(cmds)
+    outs = []
+    link = []
+    for name, obj in tests:
+        exe = os.path.join(ASAN, name)
+        link.append([CXX, *SANITIZE, obj, *objs, oracle_obj, "-lm", "-o", exe])
+        outs.append(exe)
+    _run_all(link)
+    return outs
+
+
 def build_all() -> None:
     build_library()
     build_bench()
     build_oracle()
     build_cpp_tests()
+    build_sanitized()
 
 
 if __name__ == "__main__":
-    build_all()
-    print("built", LIB)
+    if sys.argv[1:] == ["asan"]:
+        print("built", *build_sanitized())
+    else:
+        build_all()
+        print("built", LIB)

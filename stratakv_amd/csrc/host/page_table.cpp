@@ -234,6 +234,20 @@ void DeviceBatch::bind(const PageTable& pages, const std::vector<int>& seq_ids, 
 void DeviceBatch::sync(const PageTable& pages, void* stream) {
     // The previous flush's host staging must have been consumed.
     detail::check(skv_event_synchronize(copy_done_), "DeviceBatch::sync");
+    // Every bound sequence is checked before anything is staged, so a throw
+    // leaves the uploaded_* bookkeeping matching what the device holds.
+    std::vector<const SequenceState*> states(seq_ids_.size());
+    for (std::size_t i = 0; i < seq_ids_.size(); ++i) {
+        const SequenceState& st = pages.get_state(seq_ids_[i]);
+        const int nb = static_cast<int>(st.physical_blocks.size());
+        if (nb > max_blocks_)
+            throw std::length_error("DeviceBatch::sync: sequence " + std::to_string(seq_ids_[i]) +
+                                    " has more blocks than max_blocks_per_seq");
+        if (st.generation == uploaded_gen_[i] && nb < uploaded_blocks_[i])
+            throw std::logic_error("DeviceBatch::sync: sequence " + std::to_string(seq_ids_[i]) +
+                                   " lost blocks without being re-allocated; rebind the batch");
+        states[i] = &st;
+    }
     n_patches_ = 0;
     auto add = [&](std::size_t index, int value) {
         patch_host_[2 * n_patches_] = static_cast<std::int32_t>(index);
@@ -241,19 +255,13 @@ void DeviceBatch::sync(const PageTable& pages, void* stream) {
         ++n_patches_;
     };
     for (std::size_t i = 0; i < seq_ids_.size(); ++i) {
-        const SequenceState& st = pages.get_state(seq_ids_[i]);
+        const SequenceState& st = *states[i];
         if (st.generation != uploaded_gen_[i]) {  // bound anew, or freed and allocated again
             uploaded_blocks_[i] = 0;
             uploaded_len_[i] = -1;
             uploaded_gen_[i] = st.generation;
         }
         const int nb = static_cast<int>(st.physical_blocks.size());
-        if (nb > max_blocks_)
-            throw std::length_error("DeviceBatch::sync: sequence " + std::to_string(seq_ids_[i]) +
-                                    " has more blocks than max_blocks_per_seq");
-        if (nb < uploaded_blocks_[i])
-            throw std::logic_error("DeviceBatch::sync: sequence " + std::to_string(seq_ids_[i]) +
-                                   " lost blocks without being re-allocated; rebind the batch");
         for (int k = uploaded_blocks_[i]; k < nb; ++k)
             add(i * static_cast<std::size_t>(max_blocks_) + static_cast<std::size_t>(k), st.physical_blocks[k]);
         uploaded_blocks_[i] = nb;

@@ -2,7 +2,11 @@
 
 test_memory: Tensor bf16 rules, BlockPool / PageTable known answers of the
 reference (src/main.cpp Phase 3/4, tests/phase7_smoke.cpp) and random
-alloc/append/free traces compared op for op with the oracle.  CPU only.
+alloc/append/free traces compared op for op with the oracle.
+test_host_layer: Sampler configuration and RNG rules; its device sections
+(DeviceBatch, device block tables, device pool copies) report themselves
+skipped here and run in tests/test_gpu_host_cpp.py and, over host memory, in
+tests/test_host_sanitizers.py.  CPU only.
 """
 import os
 import subprocess
@@ -24,4 +28,9 @@ def _run(name, timeout=120):
 
 def test_cpp_memory_and_tensor():
     rc, out = _run("test_memory")
+    assert rc == 0, out
+
+
+def test_cpp_host_layer_host_sections():
+    rc, out = _run("test_host_layer")
     assert rc == 0, out

@@ -7,7 +7,9 @@
   payloads and -0) are bit-exact against numpy's own conversions and against
   the reference loader.
 * load_linear_bf16_transposed matches the reference bit for bit.
-The tool under test is build/bin/tool_model (tests/cpp/tool_model.cpp).
+The tool under test is build/bin/tool_model (tests/cpp/tool_model.cpp), or
+the binary SKV_TOOL_MODEL names (tests/test_host_sanitizers.py runs this
+module against the AddressSanitizer/UBSan build).
 """
 import ctypes
 import json
@@ -19,7 +21,7 @@ import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-TOOL = os.path.join(ROOT, "build", "bin", "tool_model")
+TOOL = os.environ.get("SKV_TOOL_MODEL") or os.path.join(ROOT, "build", "bin", "tool_model")
 REF = os.path.join(ROOT, "oracle", "_ref", "libstratakv_ref.so")
 
 
