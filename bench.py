@@ -194,37 +194,50 @@ def algorithmic_bytes(w):
 # ---------------------------------------------------------------------------
 # GPU run
 # ---------------------------------------------------------------------------
-def run_gpu(w, steps: int, warmup: int, fused: bool = True):
-    """Times `steps` decode steps.  A step is [pre] + [main]: with fused=True,
-    pre = the cfg5 churn work (table patch + prefill-chunk append; nothing for
-    the other configs) and main = one skv_paged_decode_append call (decode-token
-    append + attention); with fused=False, pre also holds the decode-token
-    skv_kv_append and main is skv_paged_decode alone."""
+def setup_gpu(w):
+    """The step's device inputs, resident in HBM: seeded N(0,1) bf16 pools,
+    queries and new rows, the tables and lengths, the output and workspace."""
     import stratakv_amd as skv
 
     skv.require_gpu()
     B, Hq, Hkv, hd, bs, total = w["B"], w["Hq"], w["Hkv"], w["hd"], w["bs"], w["total"]
     pool_elems = total * bs * Hkv * hd
     log(f"allocating pools: 2 x {pool_elems * 2 / 2**30:.2f} GiB")
-    stream = skv.Stream()
-    k_pool = skv.DeviceBuffer(pool_elems * 2)
-    v_pool = skv.DeviceBuffer(pool_elems * 2)
-    skv.fill_normal_bf16(k_pool, pool_elems, w["seed"], 0, stream.handle)
-    skv.fill_normal_bf16(v_pool, pool_elems, w["seed"] + 1, 0, stream.handle)
-    q = skv.DeviceBuffer(B * Hq * hd * 2)
-    skv.fill_normal_bf16(q, B * Hq * hd, w["seed"] + 2, 0, stream.handle)
-    k_new = skv.DeviceBuffer(B * Hkv * hd * 2)
-    v_new = skv.DeviceBuffer(B * Hkv * hd * 2)
-    skv.fill_normal_bf16(k_new, B * Hkv * hd, w["seed"] + 3, 0, stream.handle)
-    skv.fill_normal_bf16(v_new, B * Hkv * hd, w["seed"] + 4, 0, stream.handle)
-    tables = skv.DeviceBuffer.from_numpy(w["tables"])
-    lens = skv.DeviceBuffer.from_numpy(w["lens"])
-    positions = skv.DeviceBuffer.from_numpy(w["lens"] - 1)
-    out = skv.DeviceBuffer(B * Hq * hd * 4)
-    ws, wsb = skv.decode_workspace(B, Hq, Hkv, hd, stream.handle)
-    max_blocks = w["tables"].shape[1]
-    scale = 1.0 / math.sqrt(hd)
-    stream.synchronize()
+    d = dict(skv=skv, stream=skv.Stream())
+    h = d["stream"].handle
+    d["k_pool"] = skv.DeviceBuffer(pool_elems * 2)
+    d["v_pool"] = skv.DeviceBuffer(pool_elems * 2)
+    skv.fill_normal_bf16(d["k_pool"], pool_elems, w["seed"], 0, h)
+    skv.fill_normal_bf16(d["v_pool"], pool_elems, w["seed"] + 1, 0, h)
+    d["q"] = skv.DeviceBuffer(B * Hq * hd * 2)
+    skv.fill_normal_bf16(d["q"], B * Hq * hd, w["seed"] + 2, 0, h)
+    d["k_new"] = skv.DeviceBuffer(B * Hkv * hd * 2)
+    d["v_new"] = skv.DeviceBuffer(B * Hkv * hd * 2)
+    skv.fill_normal_bf16(d["k_new"], B * Hkv * hd, w["seed"] + 3, 0, h)
+    skv.fill_normal_bf16(d["v_new"], B * Hkv * hd, w["seed"] + 4, 0, h)
+    d["tables"] = skv.DeviceBuffer.from_numpy(w["tables"])
+    d["lens"] = skv.DeviceBuffer.from_numpy(w["lens"])
+    d["positions"] = skv.DeviceBuffer.from_numpy(w["lens"] - 1)
+    d["out"] = skv.DeviceBuffer(B * Hq * hd * 4)
+    d["ws"], d["wsb"] = skv.decode_workspace(B, Hq, Hkv, hd, h)
+    d["max_blocks"] = w["tables"].shape[1]
+    d["scale"] = 1.0 / math.sqrt(hd)
+    d["stream"].synchronize()
+    return d
+
+
+def run_gpu(w, steps: int, warmup: int, fused: bool = True):
+    """Times `steps` decode steps.  A step is [pre] + [main]: with fused=True,
+    pre = the cfg5 churn work (table patch + prefill-chunk append; nothing for
+    the other configs) and main = one skv_paged_decode_append call (decode-token
+    append + attention); with fused=False, pre also holds the decode-token
+    skv_kv_append and main is skv_paged_decode alone."""
+    d = setup_gpu(w)
+    skv, stream = d["skv"], d["stream"]
+    B, Hq, Hkv, hd, bs, total = w["B"], w["Hq"], w["Hkv"], w["hd"], w["bs"], w["total"]
+    k_pool, v_pool, q, k_new, v_new = d["k_pool"], d["v_pool"], d["q"], d["k_new"], d["v_new"]
+    tables, lens, positions, out = d["tables"], d["lens"], d["positions"], d["out"]
+    ws, wsb, max_blocks, scale = d["ws"], d["wsb"], d["max_blocks"], d["scale"]
     log("inputs resident; warming up")
 
     churn = w.get("churn")
@@ -296,6 +309,72 @@ def run_gpu(w, steps: int, warmup: int, fused: bool = True):
     return dict(ms_per_step=total_ms / steps, pre_ms=float(np.mean(pre_ms)),
                 main_ms=float(np.mean(main_ms)), main_ms_median=float(np.median(main_ms)),
                 main_ms_min=float(np.min(main_ms)), wall_ms_per_step=wall * 1e3 / steps)
+
+
+def block_bytes(w):
+    """K/V bytes of every block the decode reads (whole 16-row blocks)."""
+    nb = np.minimum(-(-w["lens"].astype(np.int64) // w["bs"]), w["tables"].shape[1])
+    return int(nb.sum()) * w["bs"] * w["Hkv"] * w["hd"] * 2 * 2
+
+
+def run_load_calibration(w, steps: int, warmup: int, rounds: int = 5):
+    """The decode's load pattern alone (skv_paged_block_checksum: the MFMA
+    decode kernel's grid, block order and buffer loads, the math replaced by a
+    checksum) timed beside the bench's decode call on the same inputs, in
+    `rounds` interleaved rounds of `steps` launches each."""
+    d = setup_gpu(w)
+    skv, stream = d["skv"], d["stream"]
+    h = stream.handle
+    B, Hq, Hkv, hd, bs, total = w["B"], w["Hq"], w["Hkv"], w["hd"], w["bs"], w["total"]
+    sums = skv.DeviceBuffer(B * Hkv * 4)
+
+    def checksum():
+        skv.paged_block_checksum(d["k_pool"], d["v_pool"], total, d["tables"], d["max_blocks"], d["lens"],
+                                 B, Hq, Hkv, hd, bs, sums, stream=h)
+
+    def decode():
+        skv.paged_decode_append(d["q"], skv.DTYPE_BF16, d["k_new"], d["v_new"], skv.DTYPE_BF16,
+                                d["k_pool"], d["v_pool"], total, d["tables"], d["max_blocks"], d["lens"],
+                                B, Hq, Hkv, hd, bs, d["scale"], d["out"], d["ws"], d["wsb"], stream=h)
+
+    def timed(fn):
+        ev = [skv.Event() for _ in range(steps + 1)]
+        ev[0].record(h)
+        for i in range(steps):
+            fn()
+            ev[i + 1].record(h)
+        skv.synchronize()
+        return [ev[i].elapsed_ms(ev[i + 1]) for i in range(steps)]
+
+    for _ in range(warmup):
+        checksum()
+        decode()
+    skv.synchronize()
+    t_sum, t_dec = [], []
+    for r in range(rounds):
+        t_sum += timed(checksum)
+        t_dec += timed(decode)
+        log(f"round {r}: checksum {np.mean(t_sum[-steps:]) * 1e3:.1f} us, "
+            f"decode call {np.mean(t_dec[-steps:]) * 1e3:.1f} us")
+    got = sums.download(np.uint32, (B * Hkv,))
+    kvb = block_bytes(w)
+    dec_bytes, tok_bytes, _, _ = algorithmic_bytes(w)
+    cs_ms, dec_ms = float(np.mean(t_sum)), float(np.mean(t_dec))
+    print(json.dumps({
+        "load_calibration": w["desc"],
+        "block_bytes": kvb,
+        "checksum_us": round(cs_ms * 1e3, 2),
+        "checksum_us_min": round(float(np.min(t_sum)) * 1e3, 2),
+        "checksum_gbs": round(kvb / (cs_ms / 1e3) / 1e9, 1),
+        "decode_call_us": round(dec_ms * 1e3, 2),
+        "decode_call_us_min": round(float(np.min(t_dec)) * 1e3, 2),
+        "decode_call_gbs_on_block_bytes": round(kvb / (dec_ms / 1e3) / 1e9, 1),
+        "decode_call_gbs_algorithmic": round((dec_bytes + tok_bytes) / (dec_ms / 1e3) / 1e9, 1),
+        "decode_frac_of_load_ceiling": round(cs_ms / dec_ms, 4),
+        "launches_each": steps * rounds,
+        "checksum_xor": int(np.bitwise_xor.reduce(got)),
+    }), flush=True)
+    return 0
 
 
 # ---------------------------------------------------------------------------
@@ -447,7 +526,9 @@ def run_cfg1(steps: int, warmup: int, with_cpu: bool):
         "roofline": {"bound": "hbm", "note": "launch-bound: each call moves 20-90 KB",
                      "kernel": "skv_paged_attention_decode_append (fused append + attention, merge)",
                      "achieved": round(gbs, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 6), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 6),
+                     "traffic": profile_traffic("cfg1"),
+                     "traffic_per": "generation (the sum over its 3,168 decode launches)",
                      "algorithmic_bytes": nbytes},
     }
     # The whole layer stack through the C++ API (TransformerBlock::forward_into
@@ -582,7 +663,8 @@ def run_prefill(steps: int, warmup: int):
                                 "0..2,047 (LIFO-reused blocks), 64 Q / 8 KV heads, head_dim 128, "
                                 "causal"), "chunk_tokens": chunk, "sequences": nn},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0,
-                     "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
+                     "traffic": profile_traffic("cfg5", "prefill"),
                      "algorithmic_flops": flops,
                      "note": ("P.V runs as two bf16 MFMAs (P split into hi + lo parts), so the "
                               "matrix cores execute 1.5x the algorithmic flops")},
@@ -591,10 +673,57 @@ def run_prefill(steps: int, warmup: int):
     return 0
 
 
-def profile_traffic(workload_key: str):
-    """HBM bytes per launch of the decode kernel from the committed rocprof
-    counter summary, if one exists for this workload."""
-    path = os.path.join(ROOT, "profiles", f"decode_traffic_{workload_key}.md")
+def cpu_compare(reps: int = 5):
+    """The CPU baseline's two candidates, 1 thread each, at cfg2 geometry (one
+    sequence, 32 Q / 4 KV heads, head_dim 64, context 4,097): the oracle's
+    decode loops (the restatement of src/layers/attention.cpp:263-337, on an
+    fp32 pool like the reference's cache and on a bf16 pool like this
+    build's) against the reference's own single-token PagedAttention::forward
+    (oracle/_ref), whose attention time is its time at context 4,097 minus its
+    time at context 1 (the four identity projections, RoPE and the cache write
+    are the same in both)."""
+    import oracle
+
+    Hq, Hkv, hd, bs, L = 32, 4, 64, 16, 4097
+    rng = np.random.default_rng(0x5EED0002)
+    nb = -(-L // bs)
+    tables = rng.permutation(nb + 8)[:nb].astype(np.int32).reshape(1, nb)
+    k32 = rng.standard_normal((nb + 8, bs, Hkv, hd), dtype=np.float32)
+    v32 = rng.standard_normal((nb + 8, bs, Hkv, hd), dtype=np.float32)
+    k16, v16 = oracle.f32_to_bf16(k32), oracle.f32_to_bf16(v32)
+    q = rng.standard_normal((1, Hq, hd), dtype=np.float32)
+    lens = np.array([L], np.int32)
+
+    def median_ms(fn):
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append((time.perf_counter() - t0) * 1e3)
+        return float(np.median(ts))
+
+    scale = 1.0 / math.sqrt(hd)
+    o32 = median_ms(lambda: oracle.paged_decode(q, k32, v32, tables, lens, Hkv, bs, scale))
+    o16 = median_ms(lambda: oracle.paged_decode(q, k16, v16, tables, lens, Hkv, bs, scale, threads=1))
+    line = {"cpu_compare": "cfg2 geometry: 1 sequence, 32 Q / 4 KV heads, head_dim 64, context 4,097, "
+                           "1 thread, median of %d" % reps,
+            "oracle_fp32_pool_ms": round(o32, 4), "oracle_bf16_pool_ms": round(o16, 4)}
+    try:
+        full, one = oracle.ref_decode_timing(Hq * hd, Hq, Hkv, bs, L, reps)
+        line.update(reference_forward_ctx4097_ms=round(full, 4), reference_forward_ctx1_ms=round(one, 4),
+                    reference_attention_ms=round(full - one, 4),
+                    reference_over_oracle_fp32=round((full - one) / o32, 3))
+    except (OSError, RuntimeError) as e:
+        line["reference"] = f"unavailable: {e}"
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def profile_traffic(workload_key: str, kind: str = "decode"):
+    """HBM bytes per launch of the measured kernel(s) from the committed
+    rocprof counter summary profiles/<kind>_traffic_<workload_key>.md, if one
+    exists for this workload."""
+    path = os.path.join(ROOT, "profiles", f"{kind}_traffic_{workload_key}.md")
     if not os.path.exists(path):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
@@ -636,9 +765,23 @@ def main() -> int:
                          "(skv_kv_append + skv_paged_decode) instead of the fused call")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                     help="only run a plain copy of MIB MiB (counter calibration) and exit")
+    ap.add_argument("--load-calibration", action="store_true",
+                    help="time the decode's load pattern alone (skv_paged_block_checksum) beside the "
+                         "decode call on the --config 2-5 inputs, and exit")
+    ap.add_argument("--cpu-compare", action="store_true",
+                    help="time the oracle's decode loops against the reference's own attention "
+                         "(oracle/_ref), 1 thread, at cfg2 geometry, and exit (CPU only)")
     args = ap.parse_args()
+    if args.cpu_compare:
+        return cpu_compare()
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.load_calibration:
+        if args.config not in (2, 3, 4, 5):
+            raise SystemExit("bench.py: --load-calibration runs on --config 2, 3, 4 or 5")
+        w = workload(args.config)
+        log(w["desc"])
+        return run_load_calibration(w, args.steps, args.warmup)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}). The paged "
               f"decode path shards by sequence or KV head with no exchange inside attention; that "

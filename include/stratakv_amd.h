@@ -467,6 +467,27 @@ int skv_gather_blocks(const uint16_t* pool, int64_t total_blocks,
                       const int32_t* table, int num_blocks,
                       int64_t block_elems, uint16_t* dst, void* stream);
 
+/* ---- measurement ----------------------------------------------------------
+ * Load-pattern calibration of skv_paged_decode: the MFMA decode kernel's K/V
+ * reads (the same grid for this geometry, the same block order per
+ * wavefront, the same buffer loads and cache hints) with the attention math
+ * replaced by a checksum.  checksums[b * num_kv_heads + h] (device,
+ * [num_seqs][num_kv_heads] uint32) receives the wrapping 32-bit sum of the
+ * 32-bit words of the head-h slice of all block_size rows of K and of V in the
+ * first min(ceil(context_lens[b] / block_size), max_blocks_per_seq) blocks of
+ * sequence b's table (an entry outside [0, total_blocks) adds 0).  Its
+ * duration is the rate the decode's loads alone reach: the ceiling the decode
+ * kernel is measured against.  The geometry of the MFMA decode path only
+ * (block_size 16, head_dim 64 or 128, num_q_heads / num_kv_heads in
+ * {1, 2, 4, 8, 16}, 16-byte aligned pools), at most 4096 sequences; other
+ * shapes give SKV_ERR_UNSUPPORTED.  No counterpart in the reference. */
+int skv_paged_block_checksum(const uint16_t* k_pool, const uint16_t* v_pool,
+                             int64_t total_blocks, const int32_t* block_tables,
+                             int max_blocks_per_seq, const int32_t* context_lens,
+                             int num_seqs, int num_q_heads, int num_kv_heads,
+                             int head_dim, int block_size, uint32_t* checksums,
+                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -237,6 +237,17 @@ def ref_attention_trace(hidden: int, heads: int, kv_heads: int, total_blocks: in
     return out, q, k, v, table[: nb.value].copy()
 
 
+def ref_decode_timing(hidden: int, heads: int, kv_heads: int, block_size: int, context: int, reps: int = 5):
+    """Median ms of the reference's single-token PagedAttention::forward at a
+    context of `context` tokens and at a context of 1 (identity projections)."""
+    a, b = ctypes.c_double(0.0), ctypes.c_double(0.0)
+    rc = ref().ref_decode_timing(hidden, heads, kv_heads, block_size, context, reps, ctypes.byref(a),
+                                 ctypes.byref(b))
+    if rc != 0:
+        raise RuntimeError("reference decode timing failed")
+    return a.value, b.value
+
+
 def ref_bf16_rne(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty(x.shape, np.uint16)

@@ -15,6 +15,7 @@
 #include "stratakv/tensor.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -180,6 +181,69 @@ int ref_attention_trace(int hidden, int heads, int kv_heads, int total_blocks, i
         const auto& pbs = pages.get_state(0).physical_blocks;
         *n_blocks = static_cast<int>(pbs.size());
         for (std::size_t k = 0; k < pbs.size(); ++k) table[k] = pbs[k];
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// Time the reference's single-token PagedAttention::forward (identity
+// projections as in ref_attention_trace) at a context of `context` tokens --
+// the first context - 1 written by one multi-token forward -- and, on a fresh
+// sequence, at a context of 1.  Each is the median of `reps` calls in ms (the
+// timed calls append their token, so the long context grows by one per call).
+// The difference is the attention over the context; the rest of forward (the
+// four projections, RoPE, the cache write) is the same in both.
+int ref_decode_timing(int hidden, int heads, int kv_heads, int block_size, int context, int reps,
+                      double* ms_context, double* ms_one) {
+    using stratakv::Tensor;
+    using clock = std::chrono::steady_clock;
+    try {
+        const int total_blocks = (context + reps) / block_size + reps + 4;
+        stratakv::layers::PagedAttention attn(hidden, heads, kv_heads, total_blocks, block_size);
+        const int hd = hidden / heads;
+        const int kv_dim = kv_heads * hd;
+        auto& wq = attn.query_projection().weight();
+        auto& wk = attn.key_projection().weight();
+        auto& wv = attn.value_projection().weight();
+        auto& wo = attn.output_projection().weight();
+        for (int i = 0; i < hidden; ++i) {
+            for (int j = 0; j < hidden; ++j) {
+                wq[static_cast<std::size_t>(i) * hidden + j] = i == j ? 1.0f : 0.0f;
+                wo[static_cast<std::size_t>(i) * hidden + j] = i == j ? 1.0f : 0.0f;
+            }
+            for (int j = 0; j < kv_dim; ++j) {
+                wk[static_cast<std::size_t>(i) * kv_dim + j] = i == j ? 1.0f : 0.0f;
+                wv[static_cast<std::size_t>(i) * kv_dim + j] = i == j + hidden - kv_dim ? 1.0f : 0.0f;
+            }
+        }
+        std::mt19937 rng(1234);
+        std::normal_distribution<float> nd(0.0f, 1.0f);
+        stratakv::memory::BlockPool pool(total_blocks, block_size);
+        stratakv::memory::PageTable pages;
+        pages.allocate_sequence(0, pool);
+        Tensor prefix({static_cast<std::size_t>(context - 1), static_cast<std::size_t>(hidden)});
+        for (std::size_t i = 0; i < prefix.num_elements(); ++i) prefix[i] = nd(rng);
+        (void)attn.forward(prefix, 0, pages, pool);
+        auto time_one = [&](int seq_id) {
+            Tensor xt({1, static_cast<std::size_t>(hidden)});
+            for (int i = 0; i < hidden; ++i) xt[i] = nd(rng);
+            const auto t0 = clock::now();
+            Tensor o = attn.forward(xt, seq_id, pages, pool);
+            const double ms = std::chrono::duration<double, std::milli>(clock::now() - t0).count();
+            if (!std::isfinite(o[0])) throw std::runtime_error("non-finite output");
+            return ms;
+        };
+        std::vector<double> t_ctx, t_one;
+        for (int r = 0; r < reps; ++r) t_ctx.push_back(time_one(0));
+        for (int r = 0; r < reps; ++r) {
+            pages.allocate_sequence(1 + r, pool);
+            t_one.push_back(time_one(1 + r));
+        }
+        std::sort(t_ctx.begin(), t_ctx.end());
+        std::sort(t_one.begin(), t_one.end());
+        *ms_context = t_ctx[t_ctx.size() / 2];
+        *ms_one = t_one[t_one.size() / 2];
         return 0;
     } catch (const std::exception&) {
         return -1;

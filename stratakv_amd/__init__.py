@@ -98,6 +98,8 @@ _PROTOS = {
     "skv_paged_attention_decode": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32,
                                           _i32, _f32, _vp, _sz, _vp]),
     "skv_gather_blocks": (_i32, [_vp, _i64, _vp, _i32, _i64, _vp, _vp]),
+    "skv_paged_block_checksum": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32,
+                                        _vp, _vp]),
     "skv_rmsnorm_f32": (_i32, [_vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "skv_linear_f32": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp]),
     "skv_rope_f32": (_i32, [_vp, _i32, _i32, _i32, _vp]),
@@ -330,6 +332,14 @@ def gather_blocks(pool, total_blocks: int, table, num_blocks: int, block_elems: 
                                    _ptr(dst), stream))
 
 
+def paged_block_checksum(k_pool, v_pool, total_blocks: int, block_tables, max_blocks_per_seq: int,
+                         context_lens, num_seqs: int, num_q_heads: int, num_kv_heads: int,
+                         head_dim: int, block_size: int, checksums, stream=None) -> None:
+    _check(lib().skv_paged_block_checksum(_ptr(k_pool), _ptr(v_pool), total_blocks, _ptr(block_tables),
+                                          max_blocks_per_seq, _ptr(context_lens), num_seqs, num_q_heads,
+                                          num_kv_heads, head_dim, block_size, _ptr(checksums), stream))
+
+
 def convert_to_bf16(src, src_dtype: int, count: int, dst, nonfinite=None, stream=None) -> None:
     _check(lib().skv_convert_to_bf16(_ptr(src), src_dtype, count, _ptr(dst), _ptr(nonfinite), stream))
 
@@ -415,6 +425,6 @@ __all__ = [
     "header_symbols", "lib", "device_count", "require_gpu", "synchronize", "DeviceBuffer",
     "fill_normal_bf16", "kv_append", "decode_workspace_bytes",
     "decode_workspace", "single_decode_workspace", "paged_decode",
-    "paged_attention_decode", "gather_blocks", "Event", "Stream", "convert_to_bf16", "convert_to_f32",
+    "paged_attention_decode", "gather_blocks", "paged_block_checksum", "Event", "Stream", "convert_to_bf16", "convert_to_f32",
     "check_finite", "embedding", "embedding_rows", "argmax", "sample",
 ]

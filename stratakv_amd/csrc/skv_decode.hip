@@ -122,7 +122,7 @@ __device__ WorkSplit build_split(const DecodeParams& p, int* P_s, bool stream_k)
         for (int b0 = 0; b0 < p.B; b0 += 64) {
             const int b = b0 + lane;
             int v = b < p.B ? seq_blocks(p, b) : 0;
-            if (blockIdx.x == 0) {
+            if (blockIdx.x == 0 && p.out != nullptr) {
                 // Sequences without context produce zeros (workgroup 0 writes them).
                 uint64_t empty = __ballot(b < p.B && v == 0);
                 const int64_t row = static_cast<int64_t>(p.Hq) * p.HD;
@@ -148,7 +148,7 @@ __device__ WorkSplit build_split(const DecodeParams& p, int* P_s, bool stream_k)
     if (!stream_k) return ws;  // one workgroup per segment: no ranges
     ws.per = std::max(p.min_per, ws.total > 0 ? cdiv(ws.total, p.ranges) : 1);
     ws.used = ws.total > 0 ? cdiv(ws.total, ws.per) : 0;
-    if (blockIdx.x == 0 && lane < 64) {  // publish for the merge kernel
+    if (blockIdx.x == 0 && lane < 64 && p.plan != nullptr) {  // publish for the merge kernel
         for (int i = lane; i <= p.B; i += 64) p.plan[3 + i] = P_s[i];
         if (lane == 0) {
             p.plan[0] = ws.total;
@@ -581,6 +581,107 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
 }
 
 // ---------------------------------------------------------------------------
+// Load-pattern calibration: the MFMA decode kernel's K/V reads with the
+// attention math replaced by a checksum.  Same work split (stream-K ranges
+// over the flattened (sequence, block) space, WPW neighbouring kv heads per
+// workgroup), same table preloading, same ring of NBUF blocks per wavefront
+// and the same non-temporal buffer loads, issued in the same order; each
+// consumed block is folded into a wrapping 32-bit sum of its K and V words.
+// sums[b * Hkv + h] receives the sum over the sequence's seq_blocks(b) blocks
+// (all 16 rows of each, the head-h slice of K and of V; a table entry outside
+// the pool contributes 0), so the result checks that every block was read
+// exactly once, whatever the split.  Its time is the rate the decode's
+// loads alone reach on this device: the ceiling the decode kernel is measured
+// against.
+// ---------------------------------------------------------------------------
+template <int HD, int WPW, int NBUF>
+__global__ __launch_bounds__(64 * WPW) void block_stream_checksum_kernel(DecodeParams p, uint32_t* sums) {
+    constexpr int BS = 16;
+    constexpr int CH = HD / 8;
+    constexpr int RPI = 64 / CH;
+    constexpr int TPL = BS / RPI;
+    extern __shared__ int P_s[];
+
+    const int wv = WPW == 1 ? 0 : __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int r = lane / CH, c = lane % CH;
+    const int Hkv = p.Hkv;
+    const int w = blockIdx.x * WPW + wv;
+    const int kvh = w % Hkv;
+    const int range = w / Hkv;
+    const WorkSplit split = build_split(p, P_s, true);
+    if (range >= split.used) return;
+    const int64_t row_stride = static_cast<int64_t>(Hkv) * HD;
+    const int block_bytes = static_cast<int>(BS * row_stride * 2);
+    const int range_lo = range * split.per;
+    const int end = std::min(range_lo + split.per, split.total);
+    int pos = range_lo;
+    int b = find_seq(P_s, p.B, pos);
+    const int lane_off_b = static_cast<int>((r * row_stride + static_cast<int64_t>(kvh) * HD + c * 8) * 2);
+
+    while (true) {
+        const int seg_lo = P_s[b], seg_hi = P_s[b + 1];
+        const int k0 = pos - seg_lo;
+        const int stop = std::min(end, seg_hi);
+        const int kb1 = stop - seg_lo;
+        const int32_t* table = p.tables + static_cast<int64_t>(b) * p.max_blocks;
+        auto table_entry = [&](int k) -> int { return table[k < kb1 ? k : kb1 - 1]; };
+        int tb = k0;
+        int tv = table_entry(tb + lane);
+        int tvn = table_entry(tb + 64 + lane);
+        auto issue = [&](int kb, u32x4_t (&kk)[TPL], u32x4_t (&vv)[TPL]) -> bool {
+            const bool in_seg = kb < kb1;
+            kb = in_seg ? kb : kb1 - 1;
+            if (kb - tb >= 64) {
+                tb += 64;
+                tv = tvn;
+                tvn = table_entry(tb + 64 + lane);
+            }
+            const int64_t e = __builtin_amdgcn_readlane(tv, kb - tb);
+            const bool valid = in_seg && e >= 0 && e < p.total_blocks;
+            const int64_t base = (valid ? e : 0) * BS * row_stride;
+            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t*>(p.k + base), 0, valid ? block_bytes : 0, kRsrcWord3);
+            const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t*>(p.v + base), 0, valid ? block_bytes : 0, kRsrcWord3);
+#pragma unroll
+            for (int i = 0; i < TPL; ++i) {
+                const int soff = static_cast<int>(i * RPI * row_stride * 2);
+                kk[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, lane_off_b, soff, kLoadNonTemporal));
+                vv[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, lane_off_b, soff, kLoadNonTemporal));
+            }
+            return valid;
+        };
+        uint32_t acc = 0;
+        auto consume = [&](u32x4_t (&kk)[TPL], u32x4_t (&vv)[TPL]) {
+#pragma unroll
+            for (int i = 0; i < TPL; ++i)
+                acc += (kk[i].x + kk[i].y) + (kk[i].z + kk[i].w) + (vv[i].x + vv[i].y) + (vv[i].z + vv[i].w);
+        };
+        u32x4_t kbuf[NBUF][TPL], vbuf[NBUF][TPL];
+        bool okb[NBUF];
+#pragma unroll
+        for (int u = 0; u < NBUF; ++u) okb[u] = issue(k0 + u, kbuf[u], vbuf[u]);
+        for (int kb = k0; kb < kb1; kb += NBUF) {
+#pragma unroll
+            for (int u = 0; u < NBUF; ++u) {
+                if (okb[u]) consume(kbuf[u], vbuf[u]);
+                okb[u] = issue(kb + u + NBUF, kbuf[u], vbuf[u]);
+            }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) acc += static_cast<uint32_t>(__shfl_xor(static_cast<int>(acc), o, 64));
+        if (lane == 0) atomicAdd(sums + static_cast<int64_t>(b) * Hkv + kvh, acc);
+
+        pos = stop;
+        if (pos >= end) break;
+        do {
+            ++b;
+        } while (P_s[b + 1] == P_s[b]);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Generic path: any block size, head_dim <= 512, any group size.  Segments are
 // (sequence, query head); lanes own tokens for q.k (q staged in LDS) and head
 // dimensions for P.V.  Correct for every shape the reference accepts; the
@@ -922,17 +1023,22 @@ int resident_waves(K kernel, int wpw, size_t lds, int max_per_simd) {
     return waves;
 }
 
+// Block ranges of the persistent grid: as many as `waves` resident wavefronts
+// hold (Hseg per range), no more than the largest possible work needs (small
+// batches and short contexts launch a small grid) and no more than the
+// workspace has partial slots for.
+int decode_ranges(const DecodeParams& p, int waves) {
+    const int64_t max_work = static_cast<int64_t>(p.B) * p.max_blocks;
+    return static_cast<int>(std::max<int64_t>(
+        1, std::min<int64_t>({waves / p.Hseg, cdiv<int64_t>(max_work, p.min_per), p.max_slots / p.Hseg})));
+}
+
 // Attention kernel over `ranges * Hseg` persistent wavefronts (workgroups of
 // `wpw` of them, wpw dividing Hseg), then the merge.
 template <typename K>
 int launch_pair(K kern, int wpw, int max_per_simd, DecodeParams p, hipStream_t s, const char* name) {
     const size_t lds = sizeof(int) * (static_cast<size_t>(p.B) + 1);  // the block prefix
-    const int waves = resident_waves(kern, wpw, lds, max_per_simd);
-    // No more ranges than the largest possible work needs (small batches and
-    // short contexts launch a small grid).
-    const int64_t max_work = static_cast<int64_t>(p.B) * p.max_blocks;
-    p.ranges = static_cast<int>(std::max<int64_t>(
-        1, std::min<int64_t>({waves / p.Hseg, cdiv<int64_t>(max_work, p.min_per), p.max_slots / p.Hseg})));
+    p.ranges = decode_ranges(p, resident_waves(kern, wpw, lds, max_per_simd));
     const unsigned groups = static_cast<unsigned>(p.ranges) * (p.Hseg / wpw);
     kern<<<groups, 64 * wpw, lds, s>>>(p);
     if (int rc = check_launch(name)) return rc;
@@ -987,6 +1093,37 @@ int launch_mfma(const DecodeParams& p, hipStream_t s) {
     SKV_MFMA(128, 1) SKV_MFMA(128, 2) SKV_MFMA(128, 4) SKV_MFMA(128, 8) SKV_MFMA(128, 16)
 #undef SKV_MFMA
     return set_error(SKV_ERR_UNSUPPORTED, "no MFMA decode kernel for head_dim %d, group %d", p.HD, G);
+}
+
+// The load-pattern calibration on the grid the MFMA decode kernel (bf16
+// queries, stream-K mode) would be launched with for the same geometry.
+template <int HD, int G>
+int launch_checksum_shape(DecodeParams p, uint32_t* sums, hipStream_t s) {
+    constexpr int NB = HD == 64 ? 3 : 2;
+    constexpr int PER_SIMD = mfma_waves_per_simd(HD, G);
+    const size_t lds = sizeof(int) * (static_cast<size_t>(p.B) + 1);
+    auto go = [&](auto decode_kern, auto sum_kern, int wpw) {
+        p.ranges = decode_ranges(p, resident_waves(decode_kern, wpw, lds, PER_SIMD));
+        const unsigned groups = static_cast<unsigned>(p.ranges) * (p.Hseg / wpw);
+        sum_kern<<<groups, 64 * wpw, lds, s>>>(p, sums);
+        return check_launch("block_stream_checksum_kernel");
+    };
+    if (p.Hkv % 4 == 0)
+        return go(decode_mfma_kernel<HD, G, false, 4, NB>, block_stream_checksum_kernel<HD, 4, NB>, 4);
+    if (p.Hkv % 2 == 0)
+        return go(decode_mfma_kernel<HD, G, false, 2, NB>, block_stream_checksum_kernel<HD, 2, NB>, 2);
+    return go(decode_mfma_kernel<HD, G, false, 1, NB>, block_stream_checksum_kernel<HD, 1, NB>, 1);
+}
+
+int launch_checksum(const DecodeParams& p, uint32_t* sums, hipStream_t s) {
+    const int G = p.Hq / p.Hkv;
+#define SKV_SUM(HD_, G_) \
+    if (p.HD == HD_ && G == G_) return launch_checksum_shape<HD_, G_>(p, sums, s);
+    SKV_SUM(64, 1) SKV_SUM(64, 2) SKV_SUM(64, 4) SKV_SUM(64, 8) SKV_SUM(64, 16)
+    SKV_SUM(128, 1) SKV_SUM(128, 2) SKV_SUM(128, 4) SKV_SUM(128, 8) SKV_SUM(128, 16)
+#undef SKV_SUM
+    return set_error(SKV_ERR_UNSUPPORTED, "skv_paged_block_checksum: head_dim %d, group %d has no MFMA decode shape",
+                     p.HD, G);
 }
 
 bool mfma_path_ok(const DecodeParams& p, int q_dtype) {
@@ -1318,4 +1455,45 @@ extern "C" int skv_paged_attention_decode_append(const float* query, const void*
     p.v_pool_w = value_cache;
     return run_decode(p, SKV_DTYPE_FP32, workspace, workspace_bytes,
                       static_cast<hipStream_t>(stream));
+}
+
+extern "C" int skv_paged_block_checksum(const uint16_t* k_pool, const uint16_t* v_pool, int64_t total_blocks,
+                                        const int32_t* block_tables, int max_blocks_per_seq,
+                                        const int32_t* context_lens, int num_seqs, int num_q_heads,
+                                        int num_kv_heads, int head_dim, int block_size, uint32_t* checksums,
+                                        void* stream) {
+    SKV_REQUIRE(k_pool && v_pool && block_tables && context_lens && checksums,
+                "skv_paged_block_checksum: invalid device pointers");
+    SKV_REQUIRE(total_blocks > 0 && max_blocks_per_seq > 0,
+                "skv_paged_block_checksum: pool and table sizes must be positive");
+    if (int rc = validate_geometry("skv_paged_block_checksum", num_seqs, num_q_heads, num_kv_heads, head_dim,
+                                   block_size, 1.0f))
+        return rc;
+    DecodeParams p{};
+    p.k = k_pool;
+    p.v = v_pool;
+    p.total_blocks = total_blocks;
+    p.tables = block_tables;
+    p.max_blocks = max_blocks_per_seq;
+    p.lens = context_lens;
+    p.B = num_seqs;
+    p.Hq = num_q_heads;
+    p.Hkv = num_kv_heads;
+    p.HD = head_dim;
+    p.bs = block_size;
+    p.Hseg = num_kv_heads;
+    p.NH = num_q_heads / num_kv_heads;
+    p.min_per = 4;
+    p.max_slots = kMaxWaves;
+    if (!mfma_path_ok(p, SKV_DTYPE_BF16) || !aligned16(k_pool) || !aligned16(v_pool))
+        return set_error(SKV_ERR_UNSUPPORTED,
+                         "skv_paged_block_checksum: needs the MFMA decode geometry (block_size 16, head_dim "
+                         "64 or 128, group 1-16, 16-byte aligned pools)");
+    if (num_seqs > kMaxBatchPerLaunch ||
+        static_cast<long long>(num_seqs) * max_blocks_per_seq >= (1ll << 30))
+        return set_error(SKV_ERR_UNSUPPORTED, "skv_paged_block_checksum: at most %d sequences of under 2^30 blocks",
+                         kMaxBatchPerLaunch);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    SKV_HIP_TRY(hipMemsetAsync(checksums, 0, sizeof(uint32_t) * static_cast<size_t>(num_seqs) * num_kv_heads, s));
+    return launch_checksum(p, checksums, s);
 }
