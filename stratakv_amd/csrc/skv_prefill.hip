@@ -19,6 +19,15 @@
 //   buffer; one barrier per step.  Rows are padded (K by 16 bytes, V by 32) so
 //   the operand reads below hit distinct banks.  The heaviest tiles (the
 //   latest tokens of each sequence) are scheduled first.
+// * The step loop keeps its K/V loads in flight through the compute: they are
+//   unconditional buffer loads through a per-(wavefront, block) descriptor that
+//   spans exactly the block's existing rows (rows past the context and absent
+//   blocks read as zeros without a memory access), the block ids come from
+//   table entries held 64 per VGPR and read with v_readlane (no scalar load,
+//   whose out-of-order return would turn every LDS wait into lgkmcnt(0)), and
+//   the query operands are complete before the loop.  With per-lane branches
+//   around the loads and a scalar table read per block, the compiler had
+//   waited for all of them (vmcnt(0)) before the step's first MFMA.
 // * S^T = K Q^T on the matrix cores (v_mfma_f32_16x16x32_bf16: keys as rows,
 //   query rows as columns), so each lane holds the scores of ONE query row:
 //   the causal/validity mask, the row max (2 shuffles) and the rescale of that
@@ -228,26 +237,49 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
             qop[0][c][cc] = __builtin_bit_cast(bf16x8_t, hi);
             if constexpr (QF32) qop[QP - 1][c][cc] = __builtin_bit_cast(bf16x8_t, lo);
         }
+    // The query operands are complete here (the empty asm reads them), so no
+    // wait for these loads is left for the step loop to merge with its own.
+#pragma unroll
+    for (int qp = 0; qp < QP; ++qp)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int cc = 0; cc < NKC; ++cc) {
+                const u32x4_t w = __builtin_bit_cast(u32x4_t, qop[qp][c][cc]);
+                asm volatile("" ::"v"(w.x), "v"(w.y), "v"(w.z), "v"(w.w));
+            }
 
-    // Block ids of a step's four 16-key blocks (-1: absent or outside the
-    // pool), read two steps ahead with uniform (scalar) loads so the K/V
-    // loads of a step never wait on a table read.
-    auto step_blocks = [&](int k0, int (&blk)[KS / 16]) {
+    // Table entries 64 per VGPR (lane i holds entry tb + i), the next 64
+    // loaded one chunk ahead; a step's four block ids are read with
+    // v_readlane, so the loop issues no scalar load (whose out-of-order
+    // return would make every LDS wait a full lgkmcnt(0)) and no K/V load
+    // waits on a table read.  -1: absent or outside the pool.
+    const int nb_tab = max(nb_seq, 1);
+    auto tab_load = [&](int first) -> int { return table[min(first + lane, nb_tab - 1)]; };
+    int tb = 0;
+    int tv = tab_load(0);
+    int tvn = tab_load(64);
+    auto step_blocks = [&](int k0s, int (&blk)[KS / 16]) {   // keys k0s .. k0s + KS - 1
+        const int b0 = k0s >> 4;
+        if (b0 - tb >= 64) {   // steps are visited in order: advance one chunk
+            tb += 64;
+            tv = tvn;
+            tvn = tab_load(tb + 64);
+        }
 #pragma unroll
         for (int hb = 0; hb < KS / 16; ++hb) {
-            const int kb = k0 + 16 * hb;
-            int pb = -1;
-            if (kb < keys_end) {
-                const int64_t e = table[kb >> 4];
-                if (e >= 0 && e < p.total_blocks) pb = static_cast<int>(e);
-            }
-            blk[hb] = pb;
+            const int kb = (b0 + hb) * 16;
+            const int e = __builtin_amdgcn_readlane(tv, b0 + hb - tb);
+            blk[hb] = kb < keys_end && e >= 0 && e < p.total_blocks ? e : -1;
         }
     };
-    // Loader mapping: thread -> (key row lr, chunk lc) for each of LOADS
-    // passes; CH consecutive threads read one row slice.  `valid` (the same in
-    // every thread) has bit k set when key k0 + k exists: below keys_end and in
-    // a block whose table entry is inside the pool.
+    // Loads of a step: thread -> (key row lr, chunk lc) for each of LOADS
+    // passes, CH consecutive threads per row slice; a wavefront's rows of one
+    // pass lie in one block, read through a buffer descriptor that spans
+    // exactly the block's existing rows (0 for an absent block), so rows that
+    // do not exist load as zeros and every load is issued unconditionally.
+    // `valid` (the same in every thread) has bit k set when key k0 + k exists.
+    const int64_t row_bytes = row_stride * 2;
     auto load_step = [&](int k0, const int (&blk)[KS / 16], u32x4_t (&kr)[LOADS], u32x4_t (&vr)[LOADS],
                          uint64_t& valid) {
         valid = 0;
@@ -263,17 +295,20 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
         for (int u = 0; u < LOADS; ++u) {
             const int idx = tid + NT * u;
             const int lr = idx / CH, lc = idx % CH;
-            kr[u] = u32x4_t{0u, 0u, 0u, 0u};
-            vr[u] = u32x4_t{0u, 0u, 0u, 0u};
-            if ((valid >> lr) & 1u) {
-                int pb = blk[0];
+            const int hb = __builtin_amdgcn_readfirstlane((wv * 64 + NT * u) / CH) >> 4;
+            int pb = blk[0];
 #pragma unroll
-                for (int hb = 1; hb < KS / 16; ++hb) pb = (lr >> 4) == hb ? blk[hb] : pb;
-                const int64_t off = (static_cast<int64_t>(pb) * 16 + (lr & 15)) * row_stride +
-                                    static_cast<int64_t>(kvh) * HD + lc * 8;
-                kr[u] = *reinterpret_cast<const u32x4_t*>(p.k + off);
-                vr[u] = *reinterpret_cast<const u32x4_t*>(p.v + off);
-            }
+            for (int h2 = 1; h2 < KS / 16; ++h2) pb = hb == h2 ? blk[h2] : pb;
+            const int cnt = pb >= 0 ? min(16, keys_end - (k0 + 16 * hb)) : 0;
+            const int64_t base = static_cast<int64_t>(pb >= 0 ? pb : 0) * 16 * row_stride + static_cast<int64_t>(kvh) * HD;
+            const int nrec = static_cast<int>(cnt * row_bytes);
+            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t*>(p.k + base), 0, nrec, 0x00020000);
+            const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t*>(p.v + base), 0, nrec, 0x00020000);
+            const int voff = static_cast<int>((lr & 15) * row_bytes + lc * 16);
+            kr[u] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, voff, 0, 0));
+            vr[u] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0));
         }
     };
     // Rows of keys that do not exist are stored as zeros (V must not carry
@@ -312,8 +347,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
     __syncthreads();
     for (int st = 0; st < nsteps; ++st) {
         const int cur = st & 1;
-        if (st + 1 < nsteps) load_step((st + 1) * KS, blk1, kr, vr, valid_next);  // in flight during compute
         step_blocks((st + 2) * KS, blk2);
+        if (st + 1 < nsteps) load_step((st + 1) * KS, blk1, kr, vr, valid_next);  // in flight during compute
         const unsigned char* kb = lds + cur * Lds::BUF;
         const unsigned char* vb = kb + Lds::KB;
         const int k0 = st * KS;
