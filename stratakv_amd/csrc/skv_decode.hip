@@ -251,6 +251,31 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
         const int64_t row = static_cast<int64_t>(blockIdx.x / Hkv) * p.max_blocks;
         trow = p.tables[row + std::min(lane, p.max_blocks - 1)];
     }
+    // Query chunks of head kvh * G + t (lanes t < G; zero for padded heads),
+    // as loaded.  SPLIT knows its sequence here, so its queries are requested
+    // with the table row and arrive by the split's barrier (one dependent
+    // round trip less before the first K/V loads); stream-K loads them per
+    // segment.
+    float4 qa[NMF][2];
+    u32x4_t qh[NMF];
+    auto load_q_raw = [&](int bq) {
+#pragma unroll
+        for (int cc = 0; cc < NMF; ++cc) {
+            qa[cc][0] = qa[cc][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            qh[cc] = u32x4_t{0u, 0u, 0u, 0u};
+            if (t < G) {
+                const int64_t qoff = (static_cast<int64_t>(bq) * p.Hq + kvh * G + t) * HD + (4 * cc + j) * 8;
+                if constexpr (QF32) {
+                    const float4* qp = reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + qoff);
+                    qa[cc][0] = qp[0];
+                    qa[cc][1] = qp[1];
+                } else {
+                    qh[cc] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.q) + qoff);
+                }
+            }
+        }
+    };
+    if constexpr (SPLIT) load_q_raw(static_cast<int>(blockIdx.x / Hkv));
 
     const WorkSplit split = build_split(p, P_s, !SPLIT);
     if (!SPLIT && range >= split.used) return;
@@ -317,28 +342,22 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
         }
 
         // q operand(s): head h0 + t, chunk 4*cc + j; zero for padded heads.
+        if constexpr (!SPLIT) load_q_raw(b);
         bf16x8_t qop[QP][NMF];
 #pragma unroll
         for (int cc = 0; cc < NMF; ++cc) {
-            u32x4_t hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
-            if (t < G) {
-                const int64_t qoff =
-                    (static_cast<int64_t>(b) * p.Hq + h0 + t) * HD + (4 * cc + j) * 8;
-                if constexpr (QF32) {
-                    const float4* qp = reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + qoff);
-                    const float4 a0 = qp[0], a1 = qp[1];
-                    const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-                    uint32_t hb[8], lb[8];
+            u32x4_t hi = qh[cc], lo = {0u, 0u, 0u, 0u};
+            if constexpr (QF32) {
+                const float4 a0 = qa[cc][0], a1 = qa[cc][1];
+                const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                uint32_t hb[8], lb[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        hb[e] = f32_to_bf16_bits(x[e]);
-                        lb[e] = f32_to_bf16_bits(x[e] - __uint_as_float(hb[e] << 16));
-                    }
-                    hi = u32x4_t{hb[0] | hb[1] << 16, hb[2] | hb[3] << 16, hb[4] | hb[5] << 16, hb[6] | hb[7] << 16};
-                    lo = u32x4_t{lb[0] | lb[1] << 16, lb[2] | lb[3] << 16, lb[4] | lb[5] << 16, lb[6] | lb[7] << 16};
-                } else {
-                    hi = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.q) + qoff);
+                for (int e = 0; e < 8; ++e) {
+                    hb[e] = f32_to_bf16_bits(x[e]);
+                    lb[e] = f32_to_bf16_bits(x[e] - __uint_as_float(hb[e] << 16));
                 }
+                hi = u32x4_t{hb[0] | hb[1] << 16, hb[2] | hb[3] << 16, hb[4] | hb[5] << 16, hb[6] | hb[7] << 16};
+                lo = u32x4_t{lb[0] | lb[1] << 16, lb[2] | lb[3] << 16, lb[4] | lb[5] << 16, lb[6] | lb[7] << 16};
             }
             qop[0][cc] = __builtin_bit_cast(bf16x8_t, hi);
             if constexpr (QF32) qop[QP - 1][cc] = __builtin_bit_cast(bf16x8_t, lo);
