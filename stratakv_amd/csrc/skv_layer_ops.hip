@@ -460,13 +460,24 @@ struct FusedRowPair {
 // `item` must be wave-uniform (the callers pass the wave index through
 // readfirstlane), so the matrix choice and the row pointers are scalar values
 // and the weight addresses never wait on a vector load of the arguments.
+// Kernel-argument arrays are indexed only with constants and the element
+// chosen by compares: an index computed at run time makes the compiler read
+// the argument buffer at that point, one dependent scalar round trip each
+// (the buffer is cold in the scalar cache at every launch).
+template <typename T>
+__device__ __forceinline__ T pick3(const T (&a)[3], int i) {
+    return i == 0 ? a[0] : (i == 1 ? a[1] : a[2]);
+}
+
 template <int MODE>
 __device__ __forceinline__ FusedRowPair fused_row_pair(const FusedGemv& f, int item) {
     FusedRowPair r{0, 0, 0, 0, 0, item, true, false};
     if constexpr (MODE == FUSED_QKV) {
-        while (r.seg < 3 && r.p >= f.n[r.seg] / 2) r.p -= f.n[r.seg] / 2, ++r.seg;
-        r.live = r.seg < 3;
-        if (!r.live) r.seg = 2, r.p = f.n[2] / 2 - 1;
+        const int h0 = f.n[0] / 2, h01 = h0 + f.n[1] / 2, h012 = h01 + f.n[2] / 2;
+        r.live = item < h012;
+        const int it = r.live ? item : h012 - 1;   // past the end: the last pair of v
+        r.seg = (it >= h0 ? 1 : 0) + (it >= h01 ? 1 : 0);
+        r.p = it - (r.seg == 0 ? 0 : (r.seg == 1 ? h0 : h01));
         const int hd = f.head_dim, half = hd / 2;
         r.rope = r.seg < 2 && f.position >= 0;
         r.ma = r.mb = r.seg;
@@ -485,7 +496,7 @@ __device__ __forceinline__ FusedRowPair fused_row_pair(const FusedGemv& f, int i
 }
 
 __device__ __forceinline__ const char* fused_row_ptr(const FusedGemv& f, int m, int r) {
-    return static_cast<const char*>(f.w[m]) + static_cast<int64_t>(r) * f.row_bytes[m];
+    return static_cast<const char*>(pick3(f.w, m)) + static_cast<int64_t>(r) * pick3(f.row_bytes, m);
 }
 
 template <bool BF16W, int MODE, int NU, int XU, bool NORM>
@@ -494,21 +505,39 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
     __shared__ float red[4];
     const int t = threadIdx.x, lane = t & 63;
     const int K = f.K;
-    auto bias_of = [&](int m, int r) { return f.bias[m] != nullptr ? f.bias[m][r] : 0.0f; };
     const FusedRowPair rp = fused_row_pair<MODE>(f, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(t >> 6));
     const int ma = rp.ma, mb = rp.mb, ra = rp.ra, rb = rp.rb, seg = rp.seg, p = rp.p;
     const bool live = rp.live, rope = rp.rope;
     // Loads in issue order: all of x (and gamma), XU per thread (K <= 256 XU),
-    // then this wavefront's weights.  Everything up to the dot products is
-    // straight-line code on registers and unconditional LDS stores (elements
-    // past K land in padding), so the waits before it count only the x and
-    // gamma loads and the weights stay in flight through the normalisation.
+    // the epilogue's operands, then this wavefront's weights.  Everything up to
+    // the dot products is straight-line code on registers and unconditional
+    // LDS stores (elements past K land in padding), so the waits before it
+    // count only the x and gamma loads and the weights stay in flight through
+    // the normalisation.  The epilogue operands (bias, residual, RoPE
+    // cos/sin) are requested here, before the barrier (a memory fence the
+    // compiler does not move loads across), not after the dot products.
     float xv[XU], gv[XU];
 #pragma unroll
     for (int u = 0; u < XU; ++u) xv[u] = f.x[min(t + 256 * u, K - 1)];
     if constexpr (NORM)
 #pragma unroll
         for (int u = 0; u < XU; ++u) gv[u] = f.gamma[min(t + 256 * u, K - 1)];
+    const float* bias_a = pick3(f.bias, ma);
+    const float* bias_b = pick3(f.bias, mb);
+    const float ba = bias_a != nullptr ? bias_a[ra] : 0.0f;
+    const float bb = bias_b != nullptr ? bias_b[rb] : 0.0f;
+    float ra_res = 0.0f, rb_res = 0.0f;
+    if constexpr (MODE == FUSED_RESIDUAL) {
+        ra_res = f.residual[ra];
+        rb_res = f.residual[rb];
+    }
+    float rope_c = 1.0f, rope_s = 0.0f;
+    if constexpr (MODE == FUSED_QKV) {
+        const int pair = rope ? p % (f.head_dim / 2) : 0;
+        rope_c = f.rope.cs[2 * pair];
+        rope_s = f.rope.cs[2 * pair + 1];
+    }
+    float* const y = pick3(f.y, seg);
     __builtin_amdgcn_sched_barrier(0);  // keep the weight loads after x's
     PairPrefetch<BF16W, NU, true> pf(fused_row_ptr(f, ma, ra), fused_row_ptr(f, mb, rb), K, lane);
     if constexpr (NORM) {
@@ -535,27 +564,24 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
     pf.finish(x_s, K, lane, a, b);
 
     if constexpr (MODE == FUSED_QKV) {
-        const int hd = f.head_dim, half = hd / 2;
         if (lane == 0) {
-            a += bias_of(seg, ra);
-            b += bias_of(seg, rb);
-            if (rope) {
-                rotate_pair(a, b, f.rope.cs[2 * (p % half)], f.rope.cs[2 * (p % half) + 1]);
-            }
-            f.y[seg][ra] = a;
-            f.y[seg][rb] = b;
+            a += ba;
+            b += bb;
+            if (rope) rotate_pair(a, b, rope_c, rope_s);
+            y[ra] = a;
+            y[rb] = b;
         }
     } else if constexpr (MODE == FUSED_GATE_UP) {
-        if (lane == 0) f.y[0][ra] = swiglu_of(a + bias_of(0, ra), b + bias_of(1, ra));
+        if (lane == 0) y[ra] = swiglu_of(a + ba, b + bb);
     } else if constexpr (MODE == FUSED_RESIDUAL) {
         if (lane == 0) {
-            f.y[0][ra] = (a + bias_of(0, ra)) + f.residual[ra];
-            if (rb != ra) f.y[0][rb] = (b + bias_of(0, rb)) + f.residual[rb];
+            y[ra] = (a + ba) + ra_res;
+            if (rb != ra) y[rb] = (b + bb) + rb_res;
         }
     } else {
         if (lane == 0) {
-            f.y[0][ra] = a + bias_of(0, ra);
-            if (rb != ra) f.y[0][rb] = b + bias_of(0, rb);
+            y[ra] = a + ba;
+            if (rb != ra) y[rb] = b + bb;
         }
     }
 }
@@ -585,8 +611,13 @@ __global__ __launch_bounds__(64 * WPG) void fused_gemv_rows_kernel(FusedGemv f) 
     const int t = threadIdx.x, lane = t & 63;
     const int K = f.K, steps = K / STEP, rows = f.rows;
     const int ntiles = cdiv(rows, T);
-    auto bias_of = [&](int m, int r) { return f.bias[m] != nullptr ? f.bias[m][r] : 0.0f; };
+    auto bias_of = [&](int m, int r) {
+        const float* bp = pick3(f.bias, m);
+        return bp != nullptr ? bp[r] : 0.0f;
+    };
     const FusedRowPair rp = fused_row_pair<MODE>(f, blockIdx.x * WPG + __builtin_amdgcn_readfirstlane(t >> 6));
+    float* const y_seg = pick3(f.y, rp.seg);
+    const int n_seg = pick3(f.n, rp.seg);
     f32x4_t st[LPT];
     auto load_step = [&](int tile, int c) __attribute__((always_inline)) {  // rows past the end repeat the last row
 #pragma unroll
@@ -664,7 +695,7 @@ __global__ __launch_bounds__(64 * WPG) void fused_gemv_rows_kernel(FusedGemv f) 
                     rope_cos_sin(f.position + m, f.rope.cs[rp.p % (f.head_dim / 2)], cs, sn);
                     rotate_pair(a, b, cs, sn);
                 }
-                float* y = f.y[rp.seg] + static_cast<int64_t>(m) * f.n[rp.seg];
+                float* y = y_seg + static_cast<int64_t>(m) * n_seg;
                 y[rp.ra] = a;
                 y[rp.rb] = b;
             } else if constexpr (MODE == FUSED_GATE_UP) {
