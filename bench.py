@@ -242,7 +242,7 @@ def run_gpu(w, steps: int, warmup: int, fused: bool = True):
 
     churn = w.get("churn")
     if churn is not None:
-        assert churn.shape[0] >= warmup + steps, "churn history shorter than the run"
+        assert churn.shape[0] >= warmup + 2 * steps, "churn history shorter than the run"
         churn_dev = skv.DeviceBuffer.from_numpy(churn)
         n_chunk = CHURN_NEW * CHURN_CHUNK * Hkv * hd
         chunk_k = skv.DeviceBuffer(n_chunk * 2)
@@ -284,15 +284,29 @@ def run_gpu(w, steps: int, warmup: int, fused: bool = True):
     skv.synchronize()
     log(f"warmup done ({warmup} steps); timing {steps} steps")
 
-    # Events on the launch stream, per step i: a before pre, b between pre and
-    # main, c after main.  When pre is empty (fused step, no churn) a is b: an
-    # extra event between two back-to-back records would itself cost ~5 us.
+    # The timed region: `steps` steps back to back, one event on the launch
+    # stream before the first and one after the last (per-step events would
+    # themselves take time between the launches of short steps).
+    e_first, e_last = skv.Event(), skv.Event()
+    skv.synchronize()
+    t0 = time.perf_counter()
+    e_first.record(stream.handle)
+    for _ in range(steps):
+        pre()
+        main()
+    e_last.record(stream.handle)
+    skv.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = e_first.elapsed_ms(e_last)
+    log(f"timed: device {total_ms:.3f} ms, host wall {wall * 1e3:.3f} ms")
+
+    # A second pass of `steps` steps for the breakdown, with events on the
+    # launch stream per step i: a before pre, b between pre and main, c after
+    # main (when pre is empty, a is b).
     has_pre = churn is not None or not fused
     ev_a = [skv.Event() for _ in range(steps)]
     ev_b = [skv.Event() for _ in range(steps)] if has_pre else ev_a
     ev_c = [skv.Event() for _ in range(steps)]
-    skv.synchronize()
-    t0 = time.perf_counter()
     for i in range(steps):
         ev_a[i].record(stream.handle)
         if has_pre:
@@ -301,11 +315,8 @@ def run_gpu(w, steps: int, warmup: int, fused: bool = True):
         main()
         ev_c[i].record(stream.handle)
     skv.synchronize()
-    wall = time.perf_counter() - t0
     pre_ms = [ev_a[i].elapsed_ms(ev_b[i]) if has_pre else 0.0 for i in range(steps)]
     main_ms = [ev_b[i].elapsed_ms(ev_c[i]) for i in range(steps)]
-    total_ms = ev_a[0].elapsed_ms(ev_c[steps - 1])
-    log(f"timed: device {total_ms:.3f} ms, host wall {wall * 1e3:.3f} ms")
     return dict(ms_per_step=total_ms / steps, pre_ms=float(np.mean(pre_ms)),
                 main_ms=float(np.mean(main_ms)), main_ms_median=float(np.median(main_ms)),
                 main_ms_min=float(np.min(main_ms)), wall_ms_per_step=wall * 1e3 / steps)
@@ -793,7 +804,7 @@ def main() -> int:
         return run_prefill(args.steps, args.warmup)
     if args.config == 1:
         return run_cfg1(args.steps, args.warmup, not args.no_cpu_baseline)
-    w = churn_workload(args.warmup + args.steps) if args.config == 5 else workload(args.config)
+    w = churn_workload(args.warmup + 2 * args.steps) if args.config == 5 else workload(args.config)
     dec_bytes, tok_bytes, churn_bytes, flops = algorithmic_bytes(w)
     log(w["desc"])
     log(f"algorithmic bytes per step: decode {dec_bytes / 1e9:.3f} GB + decode-token append "
