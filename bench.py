@@ -761,6 +761,37 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+def read_calibration(gib: int, steps: int, warmup: int) -> int:
+    """Plain streaming reads (skv_stream_read_checksum: one contiguous buffer,
+    the decode's non-temporal 16-byte loads, 4 MiB chunks per wavefront) of
+    `gib` GiB, timed with events on the launch stream: the rate reads alone
+    reach on this GPU, the ceiling beside the decode's own load pattern."""
+    import stratakv_amd as skv
+
+    skv.require_gpu()
+    nbytes = gib << 30
+    data = skv.DeviceBuffer(nbytes)
+    skv.fill_normal_bf16(data, nbytes // 2, 3)
+    out = skv.DeviceBuffer(4)
+    stream = skv.Stream()
+    h = stream.handle
+    for _ in range(warmup):
+        skv.stream_read_checksum(data, nbytes, out, stream=h)
+    ev = [skv.Event() for _ in range(steps + 1)]
+    ev[0].record(h)
+    for i in range(steps):
+        skv.stream_read_checksum(data, nbytes, out, stream=h)
+        ev[i + 1].record(h)
+    skv.synchronize()
+    ms = np.array([ev[i].elapsed_ms(ev[i + 1]) for i in range(steps)])
+    print(json.dumps({"read_calibration_bytes": nbytes, "launches": steps,
+                      "read_us": round(float(ms.mean()) * 1e3, 1),
+                      "read_gbs": round(nbytes / (float(ms.mean()) / 1e3) / 1e9, 1),
+                      "read_gbs_best": round(nbytes / (float(ms.min()) / 1e3) / 1e9, 1),
+                      "frac_of_8tbs": round(nbytes / (float(ms.mean()) / 1e3) / 8e12, 4)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -776,6 +807,8 @@ def main() -> int:
                          "(skv_kv_append + skv_paged_decode) instead of the fused call")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                     help="only run a plain copy of MIB MiB (counter calibration) and exit")
+    ap.add_argument("--read-calibration", type=int, metavar="GIB", default=0,
+                    help="only time plain streaming reads of GIB GiB (skv_stream_read_checksum) and exit")
     ap.add_argument("--load-calibration", action="store_true",
                     help="time the decode's load pattern alone (skv_paged_block_checksum) beside the "
                          "decode call on the --config 2-5 inputs, and exit")
@@ -787,6 +820,8 @@ def main() -> int:
         return cpu_compare()
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.read_calibration:
+        return read_calibration(args.read_calibration, args.steps, args.warmup)
     if args.load_calibration:
         if args.config not in (2, 3, 4, 5):
             raise SystemExit("bench.py: --load-calibration runs on --config 2, 3, 4 or 5")

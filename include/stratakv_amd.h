@@ -488,6 +488,16 @@ int skv_paged_block_checksum(const uint16_t* k_pool, const uint16_t* v_pool,
                              int head_dim, int block_size, uint32_t* checksums,
                              void* stream);
 
+/* Streaming-read calibration: reads `bytes` bytes at `data` (device, 16-byte
+ * aligned, a positive multiple of 16) once, with the non-temporal 16-byte
+ * loads the decode uses, from a persistent grid of wavefronts taking 4 MiB
+ * chunks in turn, and writes the wrapping 32-bit sum of its 32-bit words to
+ * *checksum (device).  Its duration gives the rate plain reads reach on this
+ * GPU, beside the decode's own load pattern (skv_paged_block_checksum).
+ * Clears *checksum with an asynchronous memset first (not for graph
+ * capture).  No counterpart in the reference. */
+int skv_stream_read_checksum(const void* data, int64_t bytes, uint32_t* checksum, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -100,6 +100,7 @@ _PROTOS = {
     "skv_gather_blocks": (_i32, [_vp, _i64, _vp, _i32, _i64, _vp, _vp]),
     "skv_paged_block_checksum": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32,
                                         _vp, _vp]),
+    "skv_stream_read_checksum": (_i32, [_vp, _i64, _vp, _vp]),
     "skv_rmsnorm_f32": (_i32, [_vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "skv_linear_f32": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp]),
     "skv_rope_f32": (_i32, [_vp, _i32, _i32, _i32, _vp]),
@@ -332,6 +333,12 @@ def gather_blocks(pool, total_blocks: int, table, num_blocks: int, block_elems: 
                                    _ptr(dst), stream))
 
 
+def stream_read_checksum(data, nbytes: int, checksum, stream=None) -> None:
+    """skv_stream_read_checksum: read `nbytes` of `data` once (plain streaming reads) and
+    write the wrapping 32-bit sum of its 32-bit words to `checksum` (device uint32)."""
+    _check(lib().skv_stream_read_checksum(_ptr(data), nbytes, _ptr(checksum), stream))
+
+
 def paged_block_checksum(k_pool, v_pool, total_blocks: int, block_tables, max_blocks_per_seq: int,
                          context_lens, num_seqs: int, num_q_heads: int, num_kv_heads: int,
                          head_dim: int, block_size: int, checksums, stream=None) -> None:
@@ -425,6 +432,6 @@ __all__ = [
     "header_symbols", "lib", "device_count", "require_gpu", "synchronize", "DeviceBuffer",
     "fill_normal_bf16", "kv_append", "decode_workspace_bytes",
     "decode_workspace", "single_decode_workspace", "paged_decode",
-    "paged_attention_decode", "gather_blocks", "paged_block_checksum", "Event", "Stream", "convert_to_bf16", "convert_to_f32",
+    "paged_attention_decode", "gather_blocks", "paged_block_checksum", "stream_read_checksum", "Event", "Stream", "convert_to_bf16", "convert_to_f32",
     "check_finite", "embedding", "embedding_rows", "argmax", "sample",
 ]

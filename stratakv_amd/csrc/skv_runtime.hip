@@ -111,6 +111,41 @@ __global__ void scatter_i32_kernel(int32_t* __restrict__ dst, const int32_t* __r
     if (i < n) dst[pairs[2 * i]] = pairs[2 * i + 1];
 }
 
+// Streaming read of one contiguous buffer, a measurement of the rate plain
+// reads reach: a persistent grid whose wavefronts take consecutive 4 MiB
+// chunks in turn, with kReadUnroll non-temporal 16-byte loads per lane in
+// flight.  *sum (zeroed by the caller) receives the wrapping sum of the
+// buffer's 32-bit words, so no load can be dropped; one atomic per wavefront.
+constexpr int kReadUnroll = 8;
+constexpr int64_t kReadChunk16 = (int64_t{4} << 20) / 16;   // 16-byte units per chunk
+constexpr int kReadMaxGroups = 1024;
+
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ p, int64_t n16,
+                                                          uint32_t* __restrict__ sum) {
+    typedef uint32_t u32x4s_t __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
+    uint32_t acc = 0;
+    for (int64_t c = wave * kReadChunk16; c < n16; c += nwaves * kReadChunk16) {
+        const int64_t end = c + kReadChunk16 < n16 ? c + kReadChunk16 : n16;
+        for (int64_t i = c + lane; i < end; i += 64 * kReadUnroll) {
+            u32x4s_t v[kReadUnroll];
+#pragma unroll
+            for (int u = 0; u < kReadUnroll; ++u) {
+                const int64_t k = i + 64 * u < end ? i + 64 * u : end - 1;   // in bounds; not summed
+                v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4s_t*>(p + k));
+            }
+#pragma unroll
+            for (int u = 0; u < kReadUnroll; ++u)
+                acc += i + 64 * u < end ? (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]) : 0u;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane == 0) atomicAdd(sum, acc);
+}
+
 }  // namespace skv
 
 using namespace skv;
@@ -335,6 +370,20 @@ int skv_gather_blocks(const uint16_t* pool, int64_t total_blocks, const int32_t*
     gather_blocks_kernel<<<dim3(gx, num_blocks), 256, 0, static_cast<hipStream_t>(stream)>>>(
         pool, total_blocks, table, num_blocks, block_elems, dst);
     return check_launch("gather_blocks_kernel");
+}
+
+int skv_stream_read_checksum(const void* data, int64_t bytes, uint32_t* checksum, void* stream) {
+    SKV_REQUIRE(data && checksum, "skv_stream_read_checksum: NULL pointer");
+    SKV_REQUIRE(bytes > 0 && bytes % 16 == 0 && aligned16(data),
+                "skv_stream_read_checksum: the buffer must be 16-byte aligned, of a positive multiple of 16 "
+                "bytes (got %lld)", static_cast<long long>(bytes));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    SKV_HIP_TRY(hipMemsetAsync(checksum, 0, sizeof(uint32_t), s));
+    const int64_t n16 = bytes / 16;
+    const int64_t chunks = cdiv<int64_t>(n16, kReadChunk16);
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>(cdiv<int64_t>(chunks, 4), kReadMaxGroups));
+    stream_read_kernel<<<grid, 256, 0, s>>>(static_cast<const uint4*>(data), n16, checksum);
+    return check_launch("stream_read_kernel");
 }
 
 }  // extern "C"

@@ -86,3 +86,46 @@ def test_rejects_other_geometries(gpu):
         skv.paged_block_checksum(buf, buf, 4, t, 4, lens, 1, 8, 8, 96, 16, buf)
     with pytest.raises(skv.SkvError):  # group 3
         skv.paged_block_checksum(buf, buf, 4, t, 4, lens, 1, 12, 4, 64, 16, buf)
+
+
+# ---------------------------------------------------------------------------
+# skv_stream_read_checksum (bench.py --read-calibration): the wrapping uint32
+# sum of a buffer's 32-bit words, so every 16-byte piece must be read exactly
+# once: sizes below one wave-wide load, not a multiple of the unrolled step,
+# spanning several 4 MiB chunks and more chunks than the grid has wavefronts.
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("nbytes", [16, 1008, 4 << 20, (4 << 20) + 48, (37 << 20) + 4096 + 16],
+                         ids=["one_piece", "partial_step", "one_chunk", "chunk_plus", "many_chunks"])
+def test_stream_read_checksum(gpu, nbytes):
+    skv = gpu
+    rng = np.random.default_rng(nbytes % 1000)
+    words = rng.integers(0, 1 << 32, size=nbytes // 4, dtype=np.uint32)
+    d = skv.DeviceBuffer.from_numpy(words)
+    out = skv.DeviceBuffer(4)
+    skv.stream_read_checksum(d, nbytes, out)
+    skv.synchronize()
+    got = int(out.download(np.uint32, (1,))[0])
+    assert got == int(words.astype(np.uint64).sum() & 0xFFFFFFFF)
+
+
+def test_stream_read_checksum_repeated_calls(gpu):
+    # Each call clears the sum before reading: two calls in a row give the
+    # word count of a buffer of ones (5 chunks and a 16-byte tail), not twice it.
+    skv = gpu
+    nbytes = (4 << 20) * 5 + 16
+    d = skv.DeviceBuffer.from_numpy(np.ones(nbytes // 4, np.uint32))
+    out = skv.DeviceBuffer(4)
+    for _ in range(2):
+        skv.stream_read_checksum(d, nbytes, out)
+    skv.synchronize()
+    assert int(out.download(np.uint32, (1,))[0]) == nbytes // 4
+
+
+def test_stream_read_checksum_rejects(gpu):
+    skv = gpu
+    buf = skv.DeviceBuffer(1 << 12)
+    out = skv.DeviceBuffer(4)
+    with pytest.raises(skv.SkvError):
+        skv.stream_read_checksum(buf, 24, out)   # not a multiple of 16
+    with pytest.raises(skv.SkvError):
+        skv.stream_read_checksum(buf, 0, out)
