@@ -110,6 +110,21 @@ def workload(cfg: int):
                 total=int(total), desc=desc, seed=0x5EED0000 + cfg)
 
 
+def contiguous_tables(w):
+    """The same workload with each sequence's blocks consecutive, in a pool of
+    exactly the blocks the tables use (sequence 0's first, then sequence 1's,
+    ...): the block order that reads the least scattered memory, to measure
+    what a config's own block placement costs the load pattern."""
+    nbs = [int(np.count_nonzero(row >= 0)) for row in w["tables"]]
+    tables = np.full_like(w["tables"], -1)
+    pos = 0
+    for b, nb in enumerate(nbs):
+        tables[b, :nb] = np.arange(pos, pos + nb, dtype=np.int32)
+        pos += nb
+    return dict(w, tables=tables, total=int(pos),
+                desc=w["desc"] + "; tables replaced by consecutive ids in a pool of the blocks used")
+
+
 class LifoPool:
     """Block ids in BlockPool order: the constructor's stack holds total-1 ... 0
     (block 0 on top) and freed ids are pushed in table order, so the last block
@@ -812,6 +827,9 @@ def main() -> int:
     ap.add_argument("--load-calibration", action="store_true",
                     help="time the decode's load pattern alone (skv_paged_block_checksum) beside the "
                          "decode call on the --config 2-5 inputs, and exit")
+    ap.add_argument("--contiguous-tables", action="store_true",
+                    help="with --load-calibration --config 2, 3 or 4: the same lengths with each "
+                         "sequence's blocks consecutive in a pool of the blocks used")
     ap.add_argument("--cpu-compare", action="store_true",
                     help="time the oracle's decode loops against the reference's own attention "
                          "(oracle/_ref), 1 thread, at cfg2 geometry, and exit (CPU only)")
@@ -826,6 +844,10 @@ def main() -> int:
         if args.config not in (2, 3, 4, 5):
             raise SystemExit("bench.py: --load-calibration runs on --config 2, 3, 4 or 5")
         w = workload(args.config)
+        if args.contiguous_tables:
+            if args.config == 5:
+                raise SystemExit("bench.py: --contiguous-tables applies to --config 2, 3 or 4")
+            w = contiguous_tables(w)
         log(w["desc"])
         return run_load_calibration(w, args.steps, args.warmup)
     if args.gpus != 1:
