@@ -91,6 +91,21 @@ public:
     // Reseed the sampler's uniform stream (the reference seeds it from
     // std::random_device, as the constructor here does).
     void seed_sampler(std::uint32_t seed) { sampler_ = Sampler(config_.sampler, seed); }
+    // Generations whose context fits the short-table decode (prompt + max new
+    // tokens within 16 blocks, block size 16, head_dim 64 or 128, 1-16 query
+    // heads per kv head, weights in the fused kernels' layout) replay each
+    // decode step -- embedding, every layer, final norm and lm_head -- from one
+    // HIP graph, with the position, context length and flag word in device
+    // memory (TransformerBlock::forward_into_at).  The token choice before each
+    // step stays a launch of its own.  The outputs are the bits of the
+    // step-by-step launches.  On by default; false runs every step eagerly.
+    void set_graph_replay(bool enabled);
+    bool graph_replay() const noexcept { return graph_replay_; }
+    // Whether the last generate call replayed its steps from a graph.
+    bool last_generation_replayed() const noexcept { return last_replayed_; }
+    // The logits left by the last generate call (those of the last token's
+    // choice), copied to the host; empty before any call.
+    std::vector<float> last_logits() const;
     // Teacher forcing: tokens[0..n_prompt) are the prompt, then every later
     // token is fed in turn.  Returns the logits after each of the positions
     // n_prompt-1 .. tokens.size()-1, row-major [(tokens.size() - n_prompt + 1) x vocab].
@@ -109,6 +124,13 @@ private:
     // Final norm + lm_head of one hidden row into `logits`.
     void logits_of(const float* x, float* logits);
     void raise_flags(std::int32_t flags) const;
+    // Whether generate may replay steps of a `tokens`-token context from a graph.
+    bool graph_eligible(std::size_t tokens) const;
+    // The step graph for this generation (captured, or the cached one when the
+    // buffers and tables it was recorded with are unchanged); false when a
+    // layer's weights do not allow the fused kernels.
+    bool prepare_step_graph(std::size_t tokens);
+    void release_step_graph() noexcept;
 
     GeneratorConfig config_;
     void* stream_ = nullptr;
@@ -136,6 +158,15 @@ private:
     std::vector<std::vector<int>> last_tables_;
     double last_generation_ms_ = 0.0;
     double initialization_ms_ = 0.0;
+    // Graph replay of the greedy decode step.
+    bool graph_replay_ = true;
+    bool last_replayed_ = false;
+    void* capture_stream_ = nullptr;          // created for capture when stream_ is the null stream
+    void* step_graph_ = nullptr;              // instantiated graph of one decode step
+    std::vector<const void*> graph_key_;      // buffers and tables step_graph_ was recorded with
+    std::int32_t* step_state_ = nullptr;      // device [position, context length, step flag word]
+    float* rope_table_ = nullptr;             // device cos/sin pairs of positions [0, rope_positions_)
+    int rope_positions_ = 0;
 };
 
 }  // namespace generation

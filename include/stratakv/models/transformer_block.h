@@ -17,6 +17,7 @@
 #pragma once
 
 #include <cstddef>
+#include <cstdint>
 #include <optional>
 
 #include "stratakv/layers/attention.h"
@@ -81,6 +82,24 @@ public:
     void forward_into(const Tensor& hidden_states, Tensor& output, int seq_id,
                       memory::PageTable& page_table, memory::BlockPool& block_pool,
                       bool append_tokens = true);
+
+    // One decode token at a position held in device memory, for a decode step
+    // captured once in a HIP graph and replayed per token (Generator's greedy
+    // loop).  step[0] is the token's position and step[1] the context length
+    // (position + 1), both device int32; rope_cos_sin is the
+    // [rope_positions][head_dim] table of skv_rope_cos_sin.  The caller has
+    // already done the host bookkeeping forward_into does: appended the token
+    // to the sequence's PageTable and uploaded its device block table, whose
+    // stable device pointer and capacity (row length) are passed here.  The
+    // same kernels as forward_into on bf16 or fp32 output-major weights, so with
+    // equal inputs the outputs are equal to forward_into's bits whenever the
+    // attention takes the same path (a table capacity of at most 16 blocks).
+    // Returns false, having launched nothing, when a projection's weights are
+    // not in the fused kernels' layout (forward_into then runs separate kernels).
+    // No counterpart in the reference.
+    bool forward_into_at(const Tensor& hidden_states, Tensor& output, const std::int32_t* step,
+                         const float* rope_cos_sin, int rope_positions, const int* device_table,
+                         int table_capacity, memory::BlockPool& block_pool);
 
     std::size_t last_attention_blocks_visited() const noexcept {
         return attention_.last_blocks_visited();

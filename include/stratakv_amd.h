@@ -322,6 +322,25 @@ int skv_fused_qkv_f32(const float* hidden, const float* gamma, float epsilon,
                       const float* bias_k, const float* bias_v, int hidden_dim,
                       int num_heads, int num_kv_heads, int head_dim, int position,
                       float* q, float* k, float* v, void* stream);
+/* skv_fused_qkv_f32 at a position held in device memory, for a decode step
+ * captured once in a HIP graph and replayed per token: the position is
+ * *position_at (device int32, clamped to [0, rope_positions)), and q and k are
+ * rotated by the cos/sin pairs rope_cos_sin[position][head_dim / 2][2]
+ * (device fp32, filled from skv_rope_cos_sin).  With the same position the
+ * results are bit-identical to skv_fused_qkv_f32.  No counterpart in the
+ * reference: its decode step takes the position from the host. */
+int skv_fused_qkv_at_f32(const float* hidden, const float* gamma, float epsilon,
+                         const void* wq, const void* wk, const void* wv, int weight_dtype,
+                         int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
+                         const float* bias_k, const float* bias_v, int hidden_dim,
+                         int num_heads, int num_kv_heads, int head_dim, const int32_t* position_at,
+                         const float* rope_cos_sin, int rope_positions, float* q, float* k,
+                         float* v, void* stream);
+/* Host function (no device work): cos_sin[p][i] = (cos, sin) of position
+ * first_position + p at pair i, for p < positions and i < head_dim / 2, as
+ * float pairs ([positions][head_dim] floats): the values skv_fused_qkv_f32
+ * rotates by, for the device table of skv_fused_qkv_at_f32. */
+int skv_rope_cos_sin(int head_dim, int first_position, int positions, float* cos_sin);
 /* act[n] = swiglu(gate_n, up_n), gate/up = rmsnorm(x; gamma) W + bias.
  * Replaces: rmsnorm_cuda + gate/up Linear::forward_into + swiglu_inplace_cuda
  * (src/models/transformer_block.cpp:542-575). */
@@ -434,6 +453,13 @@ int skv_embedding_f32(const void* table, int table_dtype, int vocab, int hidden,
 int skv_embedding_rows_f32(const void* table, int table_dtype, int vocab, int hidden,
                            const int32_t* token_ids, int first_index, int rows, float* out,
                            int32_t* flags, void* stream);
+/* skv_embedding_f32 with the index held in device memory (*index_at) and the
+ * flag word flags[*flag_at] (flag_at NULL: flags[0]), for a decode step
+ * captured once in a HIP graph and replayed per token.  No counterpart in the
+ * reference. */
+int skv_embedding_at_f32(const void* table, int table_dtype, int vocab, int hidden,
+                         const int32_t* token_ids, const int32_t* index_at, float* out,
+                         int32_t* flags, const int32_t* flag_at, void* stream);
 
 /* token_ids[index] = the first index of the maximum of logits[0..n) (greedy,
  * src/generation/sampler.cpp:57-62).  A non-finite logit sets
@@ -441,6 +467,12 @@ int skv_embedding_rows_f32(const void* table, int table_dtype, int vocab, int hi
  * the reference's generate loop (src/generation/generator.cpp:700-735). */
 int skv_argmax_f32(const float* logits, int n, int32_t* token_ids, int index,
                    int32_t* flags, void* stream);
+/* skv_argmax_f32 writing token_ids[*index_at] and flagging flags[*flag_at]
+ * (flag_at NULL: flags[0]), both indices in device memory, for a decode step
+ * captured once in a HIP graph and replayed per token.  No counterpart in the
+ * reference. */
+int skv_argmax_at_f32(const float* logits, int n, int32_t* token_ids, const int32_t* index_at,
+                      int32_t* flags, const int32_t* flag_at, void* stream);
 
 /* token_ids[index] = Sampler::sample(logits) (src/generation/sampler.cpp:43-147):
  * temperature 0 -> greedy as skv_argmax_f32; otherwise logits / temperature,
@@ -466,6 +498,22 @@ int skv_sample_f32(const float* logits, int n, float temperature, int top_k, flo
 int skv_gather_blocks(const uint16_t* pool, int64_t total_blocks,
                       const int32_t* table, int num_blocks,
                       int64_t block_elems, uint16_t* dst, void* stream);
+
+/* ---- HIP graphs of recorded launches ----------------------------------------
+ * For a sequence of launches replayed many times with the same arguments (the
+ * greedy decode step of Generator, whose per-token values live in device
+ * memory).  skv_graph_begin_capture starts recording the launches queued on
+ * `stream` (a created stream, not the null stream; launches from this thread
+ * only); skv_graph_end_capture stops and instantiates them into *graph_exec;
+ * skv_graph_abort_capture stops and discards a recording (after a failed
+ * launch); skv_graph_launch queues one replay on any stream; skv_graph_destroy
+ * frees an instantiated graph (NULL: nothing).  Nothing recorded may be a
+ * memset.  No counterpart in the reference. */
+int skv_graph_begin_capture(void* stream);
+int skv_graph_end_capture(void* stream, void** graph_exec);
+int skv_graph_abort_capture(void* stream);
+int skv_graph_launch(void* graph_exec, void* stream);
+int skv_graph_destroy(void* graph_exec);
 
 /* ---- measurement ----------------------------------------------------------
  * Load-pattern calibration of skv_paged_decode: the MFMA decode kernel's K/V

@@ -101,6 +101,11 @@ _PROTOS = {
     "skv_paged_block_checksum": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32,
                                         _vp, _vp]),
     "skv_stream_read_checksum": (_i32, [_vp, _i64, _vp, _vp]),
+    "skv_graph_begin_capture": (_i32, [_vp]),
+    "skv_graph_end_capture": (_i32, [_vp, _c.POINTER(_vp)]),
+    "skv_graph_abort_capture": (_i32, [_vp]),
+    "skv_graph_launch": (_i32, [_vp, _vp]),
+    "skv_graph_destroy": (_i32, [_vp]),
     "skv_rmsnorm_f32": (_i32, [_vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "skv_linear_f32": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp]),
     "skv_rope_f32": (_i32, [_vp, _i32, _i32, _i32, _vp]),
@@ -108,6 +113,10 @@ _PROTOS = {
     "skv_add_f32": (_i32, [_vp, _vp, _i32, _vp]),
     "skv_fused_qkv_f32": (_i32, [_vp, _vp, _f32, _vp, _vp, _vp, _i32, _i64, _c.POINTER(_c.c_int64),
                                  _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "skv_fused_qkv_at_f32": (_i32, [_vp, _vp, _f32, _vp, _vp, _vp, _i32, _i64, _c.POINTER(_c.c_int64),
+                                    _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _vp, _vp,
+                                    _vp]),
+    "skv_rope_cos_sin": (_i32, [_i32, _i32, _i32, _vp]),
     "skv_fused_gate_up_swiglu_f32": (_i32, [_vp, _vp, _f32, _vp, _vp, _i32, _i64, _i64, _i64, _vp,
                                             _vp, _i32, _i32, _vp, _vp]),
     "skv_linear_residual_f32": (_i32, [_vp, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
@@ -133,6 +142,8 @@ _PROTOS = {
     "skv_embedding_f32": (_i32, [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp]),
     "skv_embedding_rows_f32": (_i32, [_vp, _i32, _i32, _i32, _vp, _i32, _i32, _vp, _vp, _vp]),
     "skv_argmax_f32": (_i32, [_vp, _i32, _vp, _i32, _vp, _vp]),
+    "skv_embedding_at_f32": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "skv_argmax_at_f32": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp]),
     "skv_sample_f32": (_i32, [_vp, _i32, _f32, _i32, _f32, _c.c_double, _vp, _i32, _vp, _vp]),
 }
 

@@ -6,9 +6,10 @@
 // Weights: bf16 N(0, 0.02) generated on the device from a seed (norm gammas
 // 1.0), or a safetensors checkpoint loaded with io::load_safetensors_device
 // (then the load is timed too).  Prints one JSON line.
-//   bench_generate [--checkpoint PATH] [--repeat N] [--new N] [--prompt N]
+//   bench_generate [--checkpoint PATH] [--repeat N] [--new N] [--prompt N] [--eager]
 // --prompt N: N prompt tokens (the 16 below, then ids from a fixed 32-bit LCG)
-// instead of 16, to time the prompt pass on long prompts.
+// instead of 16, to time the prompt pass on long prompts.  --eager: every decode
+// step launched one kernel at a time (Generator::set_graph_replay(false)).
 #include <algorithm>
 #include <chrono>
 #include <cstdint>
@@ -78,12 +79,14 @@ int main(int argc, char** argv) {
     try {
         std::string checkpoint;
         int repeat = 5, n_new = 128, n_prompt = 16;
+        bool eager = false;
         for (int i = 1; i < argc; ++i) {
             const std::string a = argv[i];
             if (a == "--checkpoint" && i + 1 < argc) checkpoint = argv[++i];
             else if (a == "--repeat" && i + 1 < argc) repeat = std::max(1, std::atoi(argv[++i]));
             else if (a == "--new" && i + 1 < argc) n_new = std::max(1, std::atoi(argv[++i]));
             else if (a == "--prompt" && i + 1 < argc) n_prompt = std::max(1, std::atoi(argv[++i]));
+            else if (a == "--eager") eager = true;
         }
         int devices = 0;
         if (skv_device_count(&devices) != SKV_OK || devices == 0) {
@@ -103,6 +106,7 @@ int main(int argc, char** argv) {
         }
         generation::GeneratorConfig cfg(kHidden, kInter, kHeads, kKv, kLayers, 1024, 16, kVocab, -1);
         generation::Generator gen(cfg, std::move(weights));
+        if (eager) gen.set_graph_replay(false);
         // 16 prompt ids as numpy default_rng(42).integers(0, 32000, 16).
         std::vector<int> prompt = {2856, 24766, 20946, 14044, 13856, 27475, 2750, 22315,
                                    6447, 3013,  16847, 31219, 23544, 24356, 22959, 25154};
@@ -113,8 +117,10 @@ int main(int argc, char** argv) {
         }
         std::vector<int> out = gen.generate(prompt, n_new);  // warmup
         std::vector<double> full, one;
+        bool replayed = false;
         for (int r = 0; r < repeat; ++r) {
             out = gen.generate(prompt, n_new);
+            replayed = gen.last_generation_replayed();
             full.push_back(gen.last_generation_ms());
             (void)gen.generate(prompt, 1);
             one.push_back(gen.last_generation_ms());
@@ -124,11 +130,12 @@ int main(int argc, char** argv) {
         std::printf("{\"layers\": %zu, \"prompt\": %zu, \"new_tokens\": %zu, \"gen_ms\": %.4f, "
                     "\"tokens_per_s\": %.2f, \"prefill_and_first_token_ms\": %.4f, \"decode_ms_per_token\": %.5f, "
                     "\"decode_tokens_per_s\": %.2f, \"init_ms\": %.2f, \"load_ms\": %.2f, "
-                    "\"load_payload_bytes\": %zu, \"load_decode_ms\": %.2f, \"checkpoint\": %s, \"repeat\": %d}\n",
+                    "\"load_payload_bytes\": %zu, \"load_decode_ms\": %.2f, \"checkpoint\": %s, \"repeat\": %d, "
+                    "\"graph_replay\": %s}\n",
                     kLayers, prompt.size(), out.size() - prompt.size(), ms,
                     (out.size() - prompt.size()) / (ms / 1e3), ms1, per_token, 1e3 / per_token,
                     gen.initialization_ms(), load_ms, bd.payload_bytes, bd.tensor_decode_ms,
-                    checkpoint.empty() ? "false" : "true", repeat);
+                    checkpoint.empty() ? "false" : "true", repeat, replayed ? "true" : "false");
         return 0;
     } catch (const std::exception& e) {
         std::fprintf(stderr, "bench_generate: %s\n", e.what());

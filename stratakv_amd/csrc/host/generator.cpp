@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <chrono>
 #include <climits>
+#include <cstdint>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -207,11 +208,132 @@ Generator::Generator(GeneratorConfig config, io::WeightMap weights)
 
 Generator::~Generator() {
     (void)skv_device_synchronize();
+    release_step_graph();
     for (void* e : step_events_)
         if (e) (void)skv_event_destroy(e);
     if (ids_) (void)skv_free(ids_);
     if (flags_) (void)skv_free(flags_);
     if (host_ids_) (void)skv_host_free(host_ids_);
+    if (step_state_) (void)skv_free(step_state_);
+    if (rope_table_) (void)skv_free(rope_table_);
+    if (capture_stream_) (void)skv_stream_destroy(capture_stream_);
+}
+
+void Generator::set_graph_replay(bool enabled) {
+    graph_replay_ = enabled;
+    if (!enabled) {
+        (void)skv_stream_synchronize(stream_);
+        release_step_graph();
+    }
+}
+
+void Generator::release_step_graph() noexcept {
+    if (step_graph_) (void)skv_graph_destroy(step_graph_);
+    step_graph_ = nullptr;
+    graph_key_.clear();
+}
+
+std::vector<float> Generator::last_logits() const {
+    if (!logits_) return {};
+    std::vector<float> out(config_.vocab_size);
+    detail::check(skv_memcpy_d2h(out.data(), logits_->raw_data(), out.size() * sizeof(float), stream_),
+                  "Generator: logits");
+    return out;
+}
+
+// The decode step replays the launches of step() only where they take the same
+// kernels: the short-table attention (at most 16 blocks of 16 tokens, head_dim
+// 64 or 128, a query-head group of 1-16), whose choice depends on the table
+// length and so is fixed for the whole generation.
+bool Generator::graph_eligible(std::size_t tokens) const {
+    if (!graph_replay_ || config_.block_size != 16) return false;
+    const std::size_t heads = config_.num_heads;
+    const std::size_t kv = config_.num_kv_heads == 0 ? heads : config_.num_kv_heads;
+    if (heads == 0 || kv == 0 || heads % kv != 0 || config_.hidden_dim % heads != 0) return false;
+    const std::size_t hd = config_.hidden_dim / heads, group = heads / kv;
+    const std::size_t blocks = tokens / 16 + (tokens % 16 != 0);
+    return blocks <= 16 && (hd == 64 || hd == 128) &&
+           (group == 1 || group == 2 || group == 4 || group == 8 || group == 16);
+}
+
+bool Generator::prepare_step_graph(std::size_t tokens) {
+    const int hd = static_cast<int>(config_.hidden_dim / config_.num_heads);
+    const int blocks = static_cast<int>(tokens / 16 + (tokens % 16 != 0));
+    if (step_state_ == nullptr) {
+        void* d = nullptr;
+        detail::check(skv_malloc(&d, 3 * sizeof(std::int32_t)), "Generator: step state");
+        step_state_ = static_cast<std::int32_t*>(d);
+    }
+    if (rope_positions_ < static_cast<int>(tokens)) {
+        // The cos/sin pairs forward_into computes on the host, for every position.
+        std::vector<float> host(tokens * static_cast<std::size_t>(hd));
+        detail::check(skv_rope_cos_sin(hd, 0, static_cast<int>(tokens), host.data()), "Generator: RoPE table");
+        void* d = nullptr;
+        detail::check(skv_malloc(&d, host.size() * sizeof(float)), "Generator: RoPE table");
+        detail::check(skv_memcpy_h2d(d, host.data(), host.size() * sizeof(float), nullptr), "Generator: RoPE table");
+        if (rope_table_) {
+            (void)skv_device_synchronize();   // the old table may be read by queued replays
+            release_step_graph();
+            (void)skv_free(rope_table_);
+        }
+        rope_table_ = static_cast<float*>(d);
+        rope_positions_ = static_cast<int>(tokens);
+    }
+    std::vector<const int*> tables(blocks_.size());
+    for (std::size_t l = 0; l < blocks_.size(); ++l) tables[l] = pages_[l].get_device_block_table(0, stream_);
+    std::vector<const void*> key = {ids_, flags_, hidden_->raw_data(), logits_->raw_data(), step_state_,
+                                    rope_table_, reinterpret_cast<const void*>(static_cast<std::intptr_t>(blocks))};
+    for (const int* t : tables) key.push_back(t);
+    if (step_graph_ && key == graph_key_) return true;
+    (void)skv_stream_synchronize(stream_);
+    release_step_graph();
+
+    // Record one step() on a created stream (the null stream cannot be
+    // recorded), then put every stream back.
+    void* cs = stream_;
+    if (cs == nullptr) {
+        if (!capture_stream_) detail::check(skv_stream_create(&capture_stream_), "Generator: capture stream");
+        cs = capture_stream_;
+    }
+    void* const saved = stream_;
+    auto use_stream = [&](void* st) {
+        stream_ = st;
+        for (auto& b : blocks_) b.set_stream(st);
+    };
+    const int dtype = embeddings_->dtype() == DataType::BF16 ? SKV_DTYPE_BF16 : SKV_DTYPE_FP32;
+    const int h = static_cast<int>(config_.hidden_dim);
+    const int vocab = static_cast<int>(config_.vocab_size);
+    auto* x = static_cast<float*>(hidden_->raw_data());
+    use_stream(cs);
+    bool recorded = true;
+    try {
+        detail::check(skv_graph_begin_capture(cs), "Generator: step graph");
+        try {
+            detail::check(skv_embedding_at_f32(embeddings_->raw_data(), dtype, vocab, h, ids_, step_state_, x, flags_,
+                                               step_state_ + 2, cs),
+                          "Generator: embedding");
+            for (std::size_t l = 0; l < blocks_.size() && recorded; ++l)
+                recorded = blocks_[l].forward_into_at(*hidden_, *hidden_, step_state_, rope_table_, rope_positions_,
+                                                      tables[l], blocks, pools_[l]);
+            if (recorded) logits_of(x, static_cast<float*>(logits_->raw_data()));
+        } catch (...) {
+            (void)skv_graph_abort_capture(cs);
+            throw;
+        }
+        if (!recorded) {
+            detail::check(skv_graph_abort_capture(cs), "Generator: step graph");
+        } else {
+            void* exec = nullptr;
+            detail::check(skv_graph_end_capture(cs, &exec), "Generator: step graph");
+            step_graph_ = exec;
+            graph_key_ = std::move(key);
+        }
+    } catch (...) {
+        use_stream(saved);
+        throw;
+    }
+    use_stream(saved);
+    return recorded;
 }
 
 void Generator::set_stream(void* stream) {
@@ -379,6 +501,9 @@ std::vector<int> Generator::generate(const std::vector<int>& prompt, int max_new
         const int vocab = static_cast<int>(config_.vocab_size);
         if (P >= 2) prompt_pass(P, logits, flags_);
         else step(0, logits, flags_);
+        // Decode steps replayed from a graph where that gives the same launches.
+        const bool replay = max_new_tokens >= 2 && graph_eligible(required) && prepare_step_graph(required);
+        last_replayed_ = replay;
 
         const int R = static_cast<int>(step_events_.size());
         // The sampler's stream before each queued draw (a ring as deep as the
@@ -413,7 +538,19 @@ std::vector<int> Generator::generate(const std::vector<int>& prompt, int max_new
             while (!stop && checked < queued && read_one(queued - checked > kLookahead)) {
             }
             if (stop || s + 1 == max_new_tokens) break;
-            step(pos, logits, flags_ + 2 + 2 * s);  // embeds the token just chosen
+            if (replay) {
+                // forward_into's host bookkeeping for every layer, then the
+                // step's position, context length and flag word for the replay.
+                for (std::size_t l = 0; l < pages_.size(); ++l) {
+                    pages_[l].append_token(0, pools_[l]);
+                    (void)pages_[l].get_device_block_table(0, stream_);
+                }
+                const std::int32_t state[3] = {pos, pos + 1, 2 + 2 * s};
+                detail::check(skv_write_i32(step_state_, state, 3, stream_), "Generator: step state");
+                detail::check(skv_graph_launch(step_graph_, stream_), "Generator: step replay");
+            } else {
+                step(pos, logits, flags_ + 2 + 2 * s);  // embeds the token just chosen
+            }
         }
         while (!stop && checked < queued) read_one(true);
         // Draws made for steps queued past the EOS step are taken back.

@@ -156,6 +156,98 @@ void TransformerBlock::parity_check_attention(const Tensor& queries, const Tenso
                  cpu.size() > 1 ? cpu[1] : 0.0f, cpu.size() > 2 ? cpu[2] : 0.0f);
 }
 
+// forward_into's device work with the position, context length and block
+// table read on the device (see the header); no host bookkeeping, so the
+// launches can be captured once and replayed per token.
+bool TransformerBlock::forward_into_at(const Tensor& hidden_states, Tensor& output, const std::int32_t* step,
+                                       const float* rope_cos_sin, int rope_positions, const int* device_table,
+                                       int table_capacity, memory::BlockPool& block_pool) {
+    if (hidden_states.ndim() != 2 || hidden_states.shape()[0] != 1 || hidden_states.shape()[1] != hidden_dim_ ||
+        output.shape() != hidden_states.shape() || output.device() != Device::GPU ||
+        hidden_states.device() != Device::GPU || hidden_states.dtype() != DataType::FP32 ||
+        output.dtype() != DataType::FP32)
+        throw std::invalid_argument("TransformerBlock::forward_into_at: one FP32 GPU row in and out required");
+    if (!step || !rope_cos_sin || rope_positions <= 0 || !device_table || table_capacity <= 0)
+        throw std::invalid_argument("TransformerBlock::forward_into_at: invalid step state or block table");
+    if (!query_workspace_ || !decode_workspace_ || block_pool.device() != Device::GPU ||
+        block_pool.key_cache() == nullptr)
+        throw std::runtime_error("TransformerBlock::forward_into_at: GPU workspace is not initialized");
+    const layers::Linear& wq = attention_.query_projection();
+    const layers::Linear& wk = attention_.key_projection();
+    const layers::Linear& wv = attention_.value_projection();
+    const layers::Linear& wo = attention_.output_projection();
+    auto wdtype = [](const layers::Linear& l) {
+        return l.weight().dtype() == DataType::BF16 ? SKV_DTYPE_BF16 : SKV_DTYPE_FP32;
+    };
+    auto stride_k = [](const layers::Linear& l) { return static_cast<int64_t>(l.weight().strides()[0]); };
+    auto stride_n = [](const layers::Linear& l) { return static_cast<int64_t>(l.weight().strides()[1]); };
+    auto cfp = [](const Tensor& t) { return static_cast<const float*>(t.raw_data()); };
+    auto fp = [](Tensor& t) { return static_cast<float*>(t.raw_data()); };
+    auto bias_of = [&](const layers::Linear& l) { return l.bias() ? cfp(*l.bias()) : nullptr; };
+    // Every projection must take its fused kernel (checked before anything is
+    // launched): the same-dtype and same-layout conditions forward_into tests,
+    // and the fused kernels' layout rules (output-major 16-byte aligned rows,
+    // at least one wave-wide load long, inputs staged whole in LDS).
+    auto fusable = [&](const layers::Linear& l) {
+        const int esz = wdtype(l) == SKV_DTYPE_BF16 ? 2 : 4;
+        const std::size_t K = l.input_dim();
+        return stride_k(l) == 1 && K >= static_cast<std::size_t>(esz == 2 ? 512 : 256) && K <= 8192 &&
+               reinterpret_cast<std::uintptr_t>(l.weight().raw_data()) % 16 == 0 &&
+               (stride_n(l) * esz) % 16 == 0 && static_cast<std::size_t>(stride_n(l)) >= K;
+    };
+    if (!(wdtype(wq) == wdtype(wk) && wdtype(wq) == wdtype(wv) && stride_k(wq) == stride_k(wk) &&
+          stride_k(wq) == stride_k(wv) && wdtype(gate_proj_) == wdtype(up_proj_) &&
+          stride_k(gate_proj_) == stride_k(up_proj_)))
+        return false;
+    const layers::Linear* const projections[] = {&wq, &wk, &wv, &wo, &gate_proj_, &up_proj_, &down_proj_};
+    for (const layers::Linear* l : projections)
+        if (!fusable(*l)) return false;
+
+    const int head_dim = static_cast<int>(attention_.head_dim());
+    const int num_heads = static_cast<int>(attention_.num_heads());
+    const int num_kv_heads = static_cast<int>(attention_.num_kv_heads());
+    const int hidden = static_cast<int>(hidden_dim_);
+    const int inter = static_cast<int>(gate_proj_.output_dim());
+    void* s = stream_;
+    Tensor& queries = *query_workspace_;
+    Tensor& keys = *key_workspace_;
+    Tensor& values = *value_workspace_;
+    Tensor& context = *context_workspace_;
+    Tensor& gate = *gate_workspace_;
+    Tensor& down = *down_workspace_;
+    Tensor& ws = *decode_workspace_;
+    const int64_t qkv_strides[3] = {stride_n(wq), stride_n(wk), stride_n(wv)};
+    detail::check(skv_fused_qkv_at_f32(cfp(hidden_states), cfp(norm1_.gamma()), norm1_.epsilon(),
+                                       wq.weight().raw_data(), wk.weight().raw_data(), wv.weight().raw_data(),
+                                       wdtype(wq), stride_k(wq), qkv_strides, bias_of(wq), bias_of(wk),
+                                       bias_of(wv), hidden, num_heads, num_kv_heads, head_dim, step,
+                                       rope_cos_sin, rope_positions, fp(queries), fp(keys), fp(values), s),
+                  "forward_into_at: fused rmsnorm + q/k/v + rope");
+    detail::check(skv_paged_decode_append(cfp(queries), SKV_DTYPE_FP32, cfp(keys), cfp(values), SKV_DTYPE_FP32,
+                                          block_pool.key_cache(), block_pool.value_cache(),
+                                          block_pool.total_blocks(), device_table, table_capacity, step + 1, 1,
+                                          num_heads, num_kv_heads, head_dim, block_pool.block_size(),
+                                          1.0f / std::sqrt(static_cast<float>(head_dim)), fp(context),
+                                          ws.raw_data(), ws.num_elements() * ws.element_size(), s),
+                  "forward_into_at: KV append + paged attention");
+    detail::check(skv_linear_residual_f32(cfp(context), wo.weight().raw_data(), wdtype(wo), stride_k(wo),
+                                          stride_n(wo), static_cast<int>(wo.input_dim()),
+                                          static_cast<int>(wo.output_dim()), bias_of(wo), cfp(hidden_states),
+                                          fp(down), s),
+                  "forward_into_at: fused o_proj + residual");
+    detail::check(skv_fused_gate_up_swiglu_f32(cfp(down), cfp(norm2_.gamma()), norm2_.epsilon(),
+                                               gate_proj_.weight().raw_data(), up_proj_.weight().raw_data(),
+                                               wdtype(gate_proj_), stride_k(gate_proj_), stride_n(gate_proj_),
+                                               stride_n(up_proj_), bias_of(gate_proj_), bias_of(up_proj_), hidden,
+                                               inter, fp(gate), s),
+                  "forward_into_at: fused rmsnorm + gate/up + swiglu");
+    detail::check(skv_linear_residual_f32(cfp(gate), down_proj_.weight().raw_data(), wdtype(down_proj_),
+                                          stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
+                                          bias_of(down_proj_), cfp(down), fp(output), s),
+                  "forward_into_at: fused down_proj + residual");
+    return true;
+}
+
 void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output, int seq_id,
                                     memory::PageTable& page_table, memory::BlockPool& block_pool,
                                     bool append_tokens) {

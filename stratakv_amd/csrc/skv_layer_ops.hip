@@ -447,6 +447,13 @@ struct FusedGemv {
     RopeTable rope;           // QKV with position >= 0: cos/sin of `position` (one token),
                               // or the inverse frequencies (fused_gemv_rows_kernel)
     int rows;                 // tokens (fused_gemv_rows_kernel; x, y, residual row-major)
+    // QKV of one token at a position held in device memory (launches captured
+    // once and replayed per token): the position is *position_at, clamped to
+    // [0, rope_positions), and its cos/sin pairs are read from rope_dev
+    // ([rope_positions][head_dim / 2][cos, sin], rope_table's values).
+    const int32_t* position_at;
+    const float* rope_dev;
+    int rope_positions;
 };
 
 // The two rows of work item `item` (one wavefront): matrix ma row ra and
@@ -499,7 +506,7 @@ __device__ __forceinline__ const char* fused_row_ptr(const FusedGemv& f, int m, 
     return static_cast<const char*>(pick3(f.w, m)) + static_cast<int64_t>(r) * pick3(f.row_bytes, m);
 }
 
-template <bool BF16W, int MODE, int NU, int XU, bool NORM>
+template <bool BF16W, int MODE, int NU, int XU, bool NORM, bool DEVPOS = false>
 __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
     extern __shared__ float x_s[];  // [256 XU] input, normalised when NORM (padding past K unused)
     __shared__ float red[4];
@@ -534,8 +541,15 @@ __global__ __launch_bounds__(256) void fused_gemv_kernel(FusedGemv f) {
     float rope_c = 1.0f, rope_s = 0.0f;
     if constexpr (MODE == FUSED_QKV) {
         const int pair = rope ? p % (f.head_dim / 2) : 0;
-        rope_c = f.rope.cs[2 * pair];
-        rope_s = f.rope.cs[2 * pair + 1];
+        if constexpr (DEVPOS) {
+            const int pos = min(max(*f.position_at, 0), f.rope_positions - 1);
+            const float* cs = f.rope_dev + static_cast<int64_t>(pos) * f.head_dim + 2 * pair;
+            rope_c = cs[0];
+            rope_s = cs[1];
+        } else {
+            rope_c = f.rope.cs[2 * pair];
+            rope_s = f.rope.cs[2 * pair + 1];
+        }
     }
     float* const y = pick3(f.y, seg);
     __builtin_amdgcn_sched_barrier(0);  // keep the weight loads after x's
@@ -728,12 +742,20 @@ int launch_fused(const FusedGemv& f, bool bf16, int items, hipStream_t s) {
     // requested at once.
     const bool norm = f.gamma != nullptr;
     auto go = [&](auto kern, int xu) { kern<<<grid, 256, sizeof(float) * 256 * static_cast<size_t>(xu), s>>>(f); };
-#define SKV_FUSED(NU_B, NU_F, XU_)                                                              \
-    {                                                                                           \
-        if (bf16 && norm) go(fused_gemv_kernel<true, MODE, NU_B, XU_, MODE <= FUSED_GATE_UP>, XU_);  \
-        else if (bf16) go(fused_gemv_kernel<true, MODE, NU_B, XU_, false>, XU_);                \
-        else if (norm) go(fused_gemv_kernel<false, MODE, NU_F, XU_, MODE <= FUSED_GATE_UP>, XU_);    \
-        else go(fused_gemv_kernel<false, MODE, NU_F, XU_, false>, XU_);                         \
+    // A device-held position (QKV only) selects the DEVPOS instance.
+    constexpr bool QKV = MODE == FUSED_QKV;
+    const bool devpos = QKV && f.position_at != nullptr;
+#define SKV_FUSED(NU_B, NU_F, XU_)                                                                       \
+    {                                                                                                    \
+        if (devpos) {                                                                                    \
+            if (bf16 && norm) go(fused_gemv_kernel<true, MODE, NU_B, XU_, QKV, QKV>, XU_);               \
+            else if (bf16) go(fused_gemv_kernel<true, MODE, NU_B, XU_, false, QKV>, XU_);                \
+            else if (norm) go(fused_gemv_kernel<false, MODE, NU_F, XU_, QKV, QKV>, XU_);                 \
+            else go(fused_gemv_kernel<false, MODE, NU_F, XU_, false, QKV>, XU_);                         \
+        } else if (bf16 && norm) go(fused_gemv_kernel<true, MODE, NU_B, XU_, MODE <= FUSED_GATE_UP>, XU_);  \
+        else if (bf16) go(fused_gemv_kernel<true, MODE, NU_B, XU_, false>, XU_);                         \
+        else if (norm) go(fused_gemv_kernel<false, MODE, NU_F, XU_, MODE <= FUSED_GATE_UP>, XU_);        \
+        else go(fused_gemv_kernel<false, MODE, NU_F, XU_, false>, XU_);                                  \
     }
     if (f.K <= 2048) SKV_FUSED(4, 8, 8)
     else if (f.K <= 4096) SKV_FUSED(8, 12, 16)
@@ -1184,7 +1206,8 @@ int fused_qkv(const char* fn, const float* hidden, int rows, const float* gamma,
               const void* wq, const void* wk, const void* wv, int weight_dtype, int64_t stride_k,
               const int64_t stride_n[3], const float* bias_q, const float* bias_k, const float* bias_v,
               int hidden_dim, int num_heads, int num_kv_heads, int head_dim, int position, float* q,
-              float* k, float* v, float* normalized, void* stream, bool mm = false) {
+              float* k, float* v, float* normalized, void* stream, bool mm = false,
+              const int32_t* position_at = nullptr, const float* rope_dev = nullptr, int rope_positions = 0) {
     SKV_REQUIRE(hidden && stride_n && q && k && v && rows > 0 && hidden_dim > 0 && num_heads > 0 &&
                     num_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
                 "%s: invalid pointers or sizes", fn);
@@ -1234,7 +1257,14 @@ int fused_qkv(const char* fn, const float* hidden, int rows, const float* gamma,
         return launch_mm<FUSED_QKV>(f, (ns[0] + ns[1] + ns[2]) / 32, s);
     }
     if (rows == 1) {
-        if (position >= 0) f.rope = rope_table(head_dim, position);
+        if (position_at != nullptr) {
+            f.position = 0;   // RoPE on; the position itself is read on the device
+            f.position_at = position_at;
+            f.rope_dev = rope_dev;
+            f.rope_positions = rope_positions;
+        } else if (position >= 0) {
+            f.rope = rope_table(head_dim, position);
+        }
         return launch_fused<FUSED_QKV>(f, esz == 2, items, s);
     }
     if (position >= 0) f.rope = rope_inv_freq(head_dim);
@@ -1340,6 +1370,35 @@ extern "C" int skv_fused_qkv_f32(const float* hidden, const float* gamma, float 
     return fused_qkv("skv_fused_qkv_f32", hidden, 1, gamma, epsilon, wq, wk, wv, weight_dtype, stride_k,
                      stride_n, bias_q, bias_k, bias_v, hidden_dim, num_heads, num_kv_heads, head_dim, position,
                      q, k, v, nullptr, stream);
+}
+
+extern "C" int skv_fused_qkv_at_f32(const float* hidden, const float* gamma, float epsilon,
+                                    const void* wq, const void* wk, const void* wv, int weight_dtype,
+                                    int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
+                                    const float* bias_k, const float* bias_v, int hidden_dim,
+                                    int num_heads, int num_kv_heads, int head_dim, const int32_t* position_at,
+                                    const float* rope_cos_sin, int rope_positions, float* q, float* k, float* v,
+                                    void* stream) {
+    SKV_REQUIRE(position_at && rope_cos_sin && rope_positions > 0,
+                "skv_fused_qkv_at_f32: NULL position or RoPE table, or no positions");
+    SKV_REQUIRE(head_dim / 2 <= kMaxRopePairs, "skv_fused_qkv_at_f32: head_dim %d exceeds %d", head_dim,
+                2 * kMaxRopePairs);
+    return fused_qkv("skv_fused_qkv_at_f32", hidden, 1, gamma, epsilon, wq, wk, wv, weight_dtype, stride_k, stride_n,
+                     bias_q, bias_k, bias_v, hidden_dim, num_heads, num_kv_heads, head_dim, 0, q, k, v, nullptr,
+                     stream, false, position_at, rope_cos_sin, rope_positions);
+}
+
+extern "C" int skv_rope_cos_sin(int head_dim, int first_position, int positions, float* cos_sin) {
+    SKV_REQUIRE(cos_sin && head_dim > 0 && head_dim % 2 == 0 && first_position >= 0 && positions > 0 &&
+                    first_position <= INT32_MAX - positions,
+                "skv_rope_cos_sin: invalid arguments");
+    SKV_REQUIRE(head_dim / 2 <= kMaxRopePairs, "skv_rope_cos_sin: head_dim %d exceeds %d", head_dim,
+                2 * kMaxRopePairs);
+    for (int i = 0; i < positions; ++i) {
+        const RopeTable& t = rope_table(head_dim, first_position + i);
+        std::copy(t.cs, t.cs + head_dim, cos_sin + static_cast<size_t>(i) * head_dim);
+    }
+    return SKV_OK;
 }
 
 extern "C" int skv_fused_qkv_rows_f32(const float* hidden, int rows, const float* gamma, float epsilon,

@@ -81,10 +81,15 @@ int launch_convert(const void* src, int src_dtype, size_t count, void* dst, int 
 // Embedding lookup: out[i] = table[ids[index] * hidden + i] widened to fp32.
 // An id outside [0, vocab) gives zeros and sets bit SKV_FLAG_BAD_TOKEN.
 // ---------------------------------------------------------------------------
-// Row blockIdx.y: out[y][i] = table[ids[index + y]][i].
+// Row blockIdx.y: out[y][i] = table[ids[index + y]][i].  index_at (device,
+// may be null) is added to index and flag_at (device, may be null) selects
+// the flag word, for launches captured once and replayed per token.
 __global__ void embedding_kernel(const void* __restrict__ table, int dtype, int vocab, int hidden,
                                  const int32_t* __restrict__ ids, int index, float* __restrict__ out,
-                                 int32_t* __restrict__ flags) {
+                                 int32_t* __restrict__ flags, const int32_t* __restrict__ index_at,
+                                 const int32_t* __restrict__ flag_at) {
+    if (index_at != nullptr) index += *index_at;
+    if (flags != nullptr && flag_at != nullptr) flags += *flag_at;
     const int id = ids[index + static_cast<int>(blockIdx.y)];
     out += static_cast<size_t>(blockIdx.y) * static_cast<size_t>(hidden);
     const bool ok = id >= 0 && id < vocab;
@@ -212,7 +217,9 @@ constexpr int kArgmaxBatch = 8;
 template <bool VEC>
 __global__ __launch_bounds__(kPickThreads) void argmax_kernel(const float* __restrict__ logits, int n,
                                                              int32_t* __restrict__ ids, int out_index,
-                                                             int32_t* __restrict__ flags) {
+                                                             int32_t* __restrict__ flags,
+                                                             const int32_t* __restrict__ index_at,
+                                                             const int32_t* __restrict__ flag_at) {
     __shared__ PickShared sh;
     float best = -INFINITY;
     int bi = n;                      // "none": loses every comparison
@@ -259,8 +266,10 @@ __global__ __launch_bounds__(kPickThreads) void argmax_kernel(const float* __res
             const int oi = sh.wave_j[i];
             if (oi != n && (j == n || sh.wave_f[i] > b || (sh.wave_f[i] == b && oi < j))) { b = sh.wave_f[i]; j = oi; }
         }
-        ids[out_index] = j == n ? 0 : j;
-        if (any_bad && flags != nullptr) atomicOr(flags, SKV_FLAG_NONFINITE_LOGITS);
+        // index_at / flag_at (device, may be null): the output index and flag
+        // word of launches captured once and replayed per token.
+        ids[out_index + (index_at != nullptr ? *index_at : 0)] = j == n ? 0 : j;
+        if (any_bad && flags != nullptr) atomicOr(flags + (flag_at != nullptr ? *flag_at : 0), SKV_FLAG_NONFINITE_LOGITS);
     }
 }
 
@@ -585,7 +594,8 @@ extern "C" int skv_check_finite(const void* src, int src_dtype, size_t count, in
 
 namespace {
 int embedding_rows(const char* fn, const void* table, int table_dtype, int vocab, int hidden,
-                   const int32_t* token_ids, int first_index, int rows, float* out, int32_t* flags, void* stream) {
+                   const int32_t* token_ids, int first_index, int rows, float* out, int32_t* flags, void* stream,
+                   const int32_t* index_at = nullptr, const int32_t* flag_at = nullptr) {
     SKV_REQUIRE(table && token_ids && out, "%s: NULL pointer", fn);
     SKV_REQUIRE(table_dtype == SKV_DTYPE_BF16 || table_dtype == SKV_DTYPE_FP32 || table_dtype == SKV_DTYPE_F16,
                 "%s: unknown table dtype %d", fn, table_dtype);
@@ -593,8 +603,8 @@ int embedding_rows(const char* fn, const void* table, int table_dtype, int vocab
                     first_index <= INT32_MAX - rows,
                 "%s: invalid dimensions", fn);
     const dim3 grid(static_cast<unsigned>(std::min(cdiv(hidden, 256), 64)), static_cast<unsigned>(rows));
-    embedding_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(table, table_dtype, vocab, hidden,
-                                                                         token_ids, first_index, out, flags);
+    embedding_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+        table, table_dtype, vocab, hidden, token_ids, first_index, out, flags, index_at, flag_at);
     return check_launch(fn);
 }
 }  // namespace
@@ -606,6 +616,14 @@ extern "C" int skv_embedding_f32(const void* table, int table_dtype, int vocab, 
                           stream);
 }
 
+extern "C" int skv_embedding_at_f32(const void* table, int table_dtype, int vocab, int hidden,
+                                    const int32_t* token_ids, const int32_t* index_at, float* out, int32_t* flags,
+                                    const int32_t* flag_at, void* stream) {
+    SKV_REQUIRE(index_at != nullptr, "skv_embedding_at_f32: NULL index");
+    return embedding_rows("skv_embedding_at_f32", table, table_dtype, vocab, hidden, token_ids, 0, 1, out, flags,
+                          stream, index_at, flag_at);
+}
+
 extern "C" int skv_embedding_rows_f32(const void* table, int table_dtype, int vocab, int hidden,
                                       const int32_t* token_ids, int first_index, int rows, float* out,
                                       int32_t* flags, void* stream) {
@@ -614,9 +632,11 @@ extern "C" int skv_embedding_rows_f32(const void* table, int table_dtype, int vo
 }
 
 namespace {
-int launch_argmax(const float* logits, int n, int32_t* ids, int index, int32_t* flags, hipStream_t s) {
-    if (aligned16(logits)) argmax_kernel<true><<<1, kPickThreads, 0, s>>>(logits, n, ids, index, flags);
-    else argmax_kernel<false><<<1, kPickThreads, 0, s>>>(logits, n, ids, index, flags);
+int launch_argmax(const float* logits, int n, int32_t* ids, int index, int32_t* flags, hipStream_t s,
+                  const int32_t* index_at = nullptr, const int32_t* flag_at = nullptr) {
+    if (aligned16(logits))
+        argmax_kernel<true><<<1, kPickThreads, 0, s>>>(logits, n, ids, index, flags, index_at, flag_at);
+    else argmax_kernel<false><<<1, kPickThreads, 0, s>>>(logits, n, ids, index, flags, index_at, flag_at);
     return check_launch("argmax_kernel");
 }
 }  // namespace
@@ -626,6 +646,13 @@ extern "C" int skv_argmax_f32(const float* logits, int n, int32_t* token_ids, in
     SKV_REQUIRE(logits && token_ids, "skv_argmax_f32: NULL pointer");
     SKV_REQUIRE(n > 0 && index >= 0, "skv_argmax_f32: invalid dimensions");
     return launch_argmax(logits, n, token_ids, index, flags, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int skv_argmax_at_f32(const float* logits, int n, int32_t* token_ids, const int32_t* index_at,
+                                 int32_t* flags, const int32_t* flag_at, void* stream) {
+    SKV_REQUIRE(logits && token_ids && index_at, "skv_argmax_at_f32: NULL pointer");
+    SKV_REQUIRE(n > 0, "skv_argmax_at_f32: invalid dimensions");
+    return launch_argmax(logits, n, token_ids, 0, flags, static_cast<hipStream_t>(stream), index_at, flag_at);
 }
 
 extern "C" int skv_sample_f32(const float* logits, int n, float temperature, int top_k, float top_p,

@@ -372,6 +372,50 @@ int skv_gather_blocks(const uint16_t* pool, int64_t total_blocks, const int32_t*
     return check_launch("gather_blocks_kernel");
 }
 
+int skv_graph_begin_capture(void* stream) {
+    SKV_REQUIRE(stream != nullptr, "skv_graph_begin_capture: capture needs a created stream, not the null stream");
+    SKV_HIP_TRY(hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal));
+    return SKV_OK;
+}
+
+int skv_graph_end_capture(void* stream, void** graph_exec) {
+    SKV_REQUIRE(stream && graph_exec, "skv_graph_end_capture: NULL argument");
+    *graph_exec = nullptr;
+    hipGraph_t g = nullptr;
+    SKV_HIP_TRY(hipStreamEndCapture(static_cast<hipStream_t>(stream), &g));
+    hipGraphExec_t e = nullptr;
+    const hipError_t rc = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (rc != hipSuccess)
+        return set_error(SKV_ERR_HIP, "skv_graph_end_capture: hipGraphInstantiate: %s", hipGetErrorString(rc));
+    *graph_exec = e;
+    return SKV_OK;
+}
+
+int skv_graph_abort_capture(void* stream) {
+    SKV_REQUIRE(stream != nullptr, "skv_graph_abort_capture: NULL stream");
+    hipGraph_t g = nullptr;
+    const hipError_t rc = hipStreamEndCapture(static_cast<hipStream_t>(stream), &g);
+    if (g != nullptr) (void)hipGraphDestroy(g);
+    (void)hipGetLastError();   // an invalidated capture reports its error here; it is discarded with the graph
+    return rc == hipSuccess || rc == hipErrorStreamCaptureInvalidated ? SKV_OK
+                                                                       : set_error(SKV_ERR_HIP,
+                                                                                   "skv_graph_abort_capture: %s",
+                                                                                   hipGetErrorString(rc));
+}
+
+int skv_graph_launch(void* graph_exec, void* stream) {
+    SKV_REQUIRE(graph_exec != nullptr, "skv_graph_launch: NULL graph");
+    SKV_HIP_TRY(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), static_cast<hipStream_t>(stream)));
+    return SKV_OK;
+}
+
+int skv_graph_destroy(void* graph_exec) {
+    if (graph_exec == nullptr) return SKV_OK;
+    SKV_HIP_TRY(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)));
+    return SKV_OK;
+}
+
 int skv_stream_read_checksum(const void* data, int64_t bytes, uint32_t* checksum, void* stream) {
     SKV_REQUIRE(data && checksum, "skv_stream_read_checksum: NULL pointer");
     SKV_REQUIRE(bytes > 0 && bytes % 16 == 0 && aligned16(data),

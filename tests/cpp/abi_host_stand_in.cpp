@@ -33,6 +33,8 @@ int copy(void* dst, const void* src, size_t bytes) {
 
 extern "C" {
 
+int skv_argmax_at_f32(const float*, int, int32_t*, const int32_t*, int32_t*, const int32_t*, void*) { return fail("skv_argmax_at_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
+
 int skv_add_f32(float*, const float*, int, void*) { return fail("skv_add_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
 int skv_check_finite(const void*, int, size_t, int32_t*, void*) { return fail("skv_check_finite: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
@@ -42,6 +44,8 @@ int skv_convert_to_bf16(const void*, int, size_t, uint16_t*, int32_t*, void*) { 
 int skv_convert_to_f32(const void*, int, size_t, float*, int32_t*, void*) { return fail("skv_convert_to_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
 int skv_device_synchronize(void) { return SKV_OK; }
+
+int skv_embedding_at_f32(const void*, int, int, int, const int32_t*, const int32_t*, float*, int32_t*, const int32_t*, void*) { return fail("skv_embedding_at_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
 int skv_embedding_f32(const void*, int, int, int, const int32_t*, int, float*, int32_t*, void*) { return fail("skv_embedding_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
@@ -78,6 +82,18 @@ int skv_fused_gate_up_swiglu_f32(const float*, const float*, float, const void*,
 int skv_fused_gate_up_swiglu_mm_f32(const float*, int, const float*, float, const void*, const void*, int, int64_t, int64_t, int64_t, const float*, const float*, int, int, float*, float*, void*) { return fail("skv_fused_gate_up_swiglu_mm_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
 int skv_fused_gate_up_swiglu_rows_f32(const float*, int, const float*, float, const void*, const void*, int, int64_t, int64_t, int64_t, const float*, const float*, int, int, float*, float*, void*) { return fail("skv_fused_gate_up_swiglu_rows_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
+
+int skv_fused_qkv_at_f32(const float*, const float*, float, const void*, const void*, const void*, int, int64_t, const int64_t*, const float*, const float*, const float*, int, int, int, int, const int32_t*, const float*, int, float*, float*, float*, void*) { return fail("skv_fused_qkv_at_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
+
+int skv_graph_abort_capture(void*) { return fail("skv_graph_abort_capture: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
+
+int skv_graph_begin_capture(void*) { return fail("skv_graph_begin_capture: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
+
+int skv_graph_destroy(void* exec) { return exec ? fail("skv_graph_destroy: no GPU in the host-only build", SKV_ERR_UNSUPPORTED) : SKV_OK; }
+
+int skv_graph_end_capture(void*, void**) { return fail("skv_graph_end_capture: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
+
+int skv_graph_launch(void*, void*) { return fail("skv_graph_launch: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
 int skv_fused_qkv_f32(const float*, const float*, float, const void*, const void*, const void*, int, int64_t, const int64_t*, const float*, const float*, const float*, int, int, int, int, int, float*, float*, float*, void*) { return fail("skv_fused_qkv_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
@@ -134,9 +150,13 @@ int skv_paged_attention_decode_append(const float*, const void*, const void*, in
 
 size_t skv_paged_attention_decode_workspace_bytes(int, int, int) { return 0; }
 
+int skv_paged_decode_append(const void*, int, const void*, const void*, int, uint16_t*, uint16_t*, int64_t, const int32_t*, int, const int32_t*, int, int, int, int, int, float, float*, void*, size_t, void*) { return fail("skv_paged_decode_append: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
+
 int skv_paged_prefill(const void*, int, const uint16_t*, const uint16_t*, int64_t, const int32_t*, int, const int32_t*, const int32_t*, int, int, int, int, int, int, float, float*, void*) { return fail("skv_paged_prefill: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
 int skv_rmsnorm_f32(const float*, float*, const float*, int, int, float, void*) { return fail("skv_rmsnorm_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
+
+int skv_rope_cos_sin(int, int, int, float*) { return fail("skv_rope_cos_sin: not in the host-only build", SKV_ERR_UNSUPPORTED); }
 
 int skv_rope_f32(float*, int, int, int, void*) { return fail("skv_rope_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
@@ -150,6 +170,10 @@ int skv_scatter_i32(int32_t* dst, const int32_t* pairs, int n, void*) {
     for (int i = 0; i < n; ++i) dst[pairs[2 * i]] = pairs[2 * i + 1];
     return SKV_OK;
 }
+
+int skv_stream_create(void**) { return fail("skv_stream_create: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
+
+int skv_stream_destroy(void* stream) { return stream ? fail("skv_stream_destroy: no GPU in the host-only build", SKV_ERR_UNSUPPORTED) : SKV_OK; }
 
 int skv_stream_synchronize(void*) { return SKV_OK; }
 

@@ -19,6 +19,7 @@
 // CLI does (src/cli.cpp:80-140).
 #include <chrono>
 #include <cstdio>
+#include <cstring>
 #include <cstdlib>
 #include <fstream>
 #include <iostream>
@@ -163,6 +164,7 @@ struct GenArgs {
     int repeat = 1;
     long long seed = -1;  // >= 0: Generator::seed_sampler
     int first_max = -1;   // >= 0: max_new of the first call (later calls use MAX_NEW)
+    bool eager = false;   // Generator::set_graph_replay(false)
     std::vector<int> tokens;
 };
 
@@ -182,6 +184,7 @@ GenArgs parse_gen(int first, int argc, char** argv) {
         else if (s == "--repeat") a.repeat = std::stoi(argv[++i]);
         else if (s == "--seed") a.seed = std::stoll(argv[++i]);
         else if (s == "--first-max") a.first_max = std::stoi(argv[++i]);
+        else if (s == "--eager") a.eager = true;
     }
     for (; i < argc; ++i) a.tokens.push_back(std::stoi(argv[i]));
     return a;
@@ -215,14 +218,26 @@ int cmd_generate(int argc, char** argv) {
         cfg.sampler = a.sampler;
         generation::Generator gen(cfg, std::move(l.weights));
         if (a.seed >= 0) gen.seed_sampler(static_cast<std::uint32_t>(a.seed));
+        if (a.eager) gen.set_graph_replay(false);
         std::vector<int> out;
         std::vector<std::vector<int>> runs, tables;
         std::vector<double> gen_ms;
+        std::vector<int> replayed;
+        std::vector<std::uint64_t> logit_hashes;
         for (int r = 0; r < a.repeat; ++r) {
             out = gen.generate(a.tokens, r == 0 && a.first_max >= 0 ? a.first_max : max_new);
             runs.push_back(out);
             tables.push_back(gen.last_block_table(0));
             gen_ms.push_back(gen.last_generation_ms());
+            replayed.push_back(gen.last_generation_replayed() ? 1 : 0);
+            // FNV-1a over the bits of the last logits: equal hashes for equal bits.
+            std::uint64_t hsh = 1469598103934665603ull;
+            for (float v : gen.last_logits()) {
+                std::uint32_t bits;
+                std::memcpy(&bits, &v, 4);
+                for (int b = 0; b < 4; ++b) hsh = (hsh ^ ((bits >> (8 * b)) & 0xFFu)) * 1099511628211ull;
+            }
+            logit_hashes.push_back(hsh);
         }
         std::printf("{\"ok\": true, \"runs\": [");
         for (std::size_t r = 0; r < runs.size(); ++r) {
@@ -236,6 +251,11 @@ int cmd_generate(int argc, char** argv) {
             for (std::size_t i = 0; i < tables[r].size(); ++i) std::printf("%s%d", i ? ", " : "", tables[r][i]);
             std::printf("]");
         }
+        std::printf("], \"replayed\": [");
+        for (std::size_t r = 0; r < replayed.size(); ++r) std::printf("%s%d", r ? ", " : "", replayed[r]);
+        std::printf("], \"logits_fnv\": [");
+        for (std::size_t r = 0; r < logit_hashes.size(); ++r)
+            std::printf("%s\"%016llx\"", r ? ", " : "", static_cast<unsigned long long>(logit_hashes[r]));
         std::printf("], \"tokens\": [");
         for (std::size_t i = 0; i < out.size(); ++i) std::printf("%s%d", i ? ", " : "", out[i]);
         std::printf("], \"load_ms\": %.3f, \"payload_bytes\": %zu, \"decode_ms\": %.3f, \"init_ms\": %.3f, "

@@ -18,7 +18,7 @@ in that order, all BF16.  Matrices are numpy PCG64(seed).standard_normal
 gammas are 1.0.  The JSON header is padded with spaces to a multiple of 8
 bytes.
 
-Usage: python tests/golden/make_checkpoint.py {tinyllama|mini} OUT.safetensors
+Usage: python tests/golden/make_checkpoint.py {tinyllama|mini|small} OUT.safetensors
 """
 from __future__ import annotations
 
@@ -35,6 +35,9 @@ GEOMETRIES = {
     "tinyllama": dict(layers=22, hidden=2048, heads=32, kv_heads=4, ffn=5632, vocab=32000, seed=1234),
     # small model for fast CPU/GPU tests (head_dim 64, GQA group 2)
     "mini": dict(layers=2, hidden=256, heads=4, kv_heads=2, ffn=512, vocab=1000, seed=77),
+    # small model whose projections take the fused one-token kernels (inputs of
+    # at least 512): the decode step the Generator replays from a graph
+    "small": dict(layers=3, hidden=512, heads=8, kv_heads=2, ffn=1024, vocab=2000, seed=91),
 }
 
 

@@ -181,6 +181,54 @@ def test_fused_projections_match_separate_kernels(gpu, with_bias, position):
         assert np.array_equal(a.download(np.uint32, (n,)), b.download(np.uint32, (n,)))
 
 
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_fused_qkv_at_device_position(gpu, with_bias):
+    """skv_fused_qkv_at_f32 (position read on the device, cos/sin from the
+    skv_rope_cos_sin table) gives the bits of skv_fused_qkv_f32 at the same
+    position; a position past the table is clamped to its last row."""
+    rng = np.random.default_rng(5)
+    H, Hq, Hkv, hd, P = 1024, 16, 4, 64, 300
+    lib, D = gpu.lib(), gpu.DeviceBuffer
+    h = rng.standard_normal(H).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    W = {n: _bf16_rows(rng, o, H) for n, o in (("q", Hq * hd), ("k", Hkv * hd), ("v", Hkv * hd))}
+    dW = {n: D.from_numpy(w) for n, w in W.items()}
+    dB = {n: (D.from_numpy(rng.standard_normal(W[n].shape[0]).astype(np.float32)) if with_bias else None)
+          for n in W}
+    bp = lambda n: dB[n].ptr if dB[n] is not None else None
+    dh, dg = D.from_numpy(h), D.from_numpy(gamma)
+    table = np.zeros((P, hd), np.float32)
+    gpu._check(lib.skv_rope_cos_sin(hd, 0, P, table.ctypes.data))
+    d_table = D.from_numpy(table)
+    strides = (ctypes.c_int64 * 3)(H, H, H)
+    for position, want_pos in ((0, 0), (1, 1), (17, 17), (299, 299), (450, 299)):
+        pos_buf = D.from_numpy(np.array([position], np.int32))
+        outs = {}
+        for mode in ("host", "device"):
+            q, k, v = D(4 * Hq * hd), D(4 * Hkv * hd), D(4 * Hkv * hd)
+            if mode == "host":
+                gpu._check(lib.skv_fused_qkv_f32(dh.ptr, dg.ptr, ctypes.c_float(1e-5), dW["q"].ptr, dW["k"].ptr,
+                                                 dW["v"].ptr, gpu.DTYPE_BF16, 1, strides, bp("q"), bp("k"), bp("v"),
+                                                 H, Hq, Hkv, hd, want_pos, q.ptr, k.ptr, v.ptr, None))
+            else:
+                gpu._check(lib.skv_fused_qkv_at_f32(dh.ptr, dg.ptr, ctypes.c_float(1e-5), dW["q"].ptr, dW["k"].ptr,
+                                                    dW["v"].ptr, gpu.DTYPE_BF16, 1, strides, bp("q"), bp("k"),
+                                                    bp("v"), H, Hq, Hkv, hd, pos_buf.ptr, d_table.ptr, P, q.ptr,
+                                                    k.ptr, v.ptr, None))
+            gpu.synchronize()
+            outs[mode] = [b.download(np.uint32, (n,)) for b, n in ((q, Hq * hd), (k, Hkv * hd), (v, Hkv * hd))]
+        for a, b in zip(outs["host"], outs["device"]):
+            assert np.array_equal(a, b), position
+
+
+def test_rope_cos_sin_table_rejects(gpu):
+    buf = np.zeros(64, np.float32)
+    with pytest.raises(gpu.SkvError):
+        gpu._check(gpu.lib().skv_rope_cos_sin(63, 0, 1, buf.ctypes.data))    # odd head_dim
+    with pytest.raises(gpu.SkvError):
+        gpu._check(gpu.lib().skv_rope_cos_sin(64, 0, 0, buf.ctypes.data))    # no positions
+
+
 def test_fused_projections_refuse_unsupported_layouts(gpu):
     """GEMM-ready (input-major) or misaligned weights: SKV_ERR_UNSUPPORTED, nothing written."""
     lib = gpu.lib()

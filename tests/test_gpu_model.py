@@ -131,6 +131,44 @@ def test_argmax_first_index(gpu):
         assert list(ids.download(np.int32, len(cases))) == want, f"shift {shift}"
 
 
+def test_embedding_and_argmax_at_device_index(gpu):
+    """skv_embedding_at_f32 / skv_argmax_at_f32 (index and flag word held in
+    device memory) give what the host-index calls give."""
+    rng = np.random.default_rng(21)
+    vocab, hidden = 300, 96
+    table = rng.standard_normal((vocab, hidden)).astype(np.float32)
+    ids = np.array([5, 17, 299, 1000, 42], np.int32)   # 1000: outside the vocabulary
+    d_t, d_ids = skv.DeviceBuffer.from_numpy(table), skv.DeviceBuffer.from_numpy(ids)
+    for idx in range(len(ids)):
+        state = skv.DeviceBuffer.from_numpy(np.array([idx, 3], np.int32))   # [index, flag word]
+        flags = skv.DeviceBuffer.from_numpy(np.zeros(5, np.int32))
+        out = skv.DeviceBuffer(4 * hidden)
+        gpu._check(skv.lib().skv_embedding_at_f32(d_t.ptr, skv.DTYPE_FP32, vocab, hidden, d_ids.ptr, state.ptr,
+                                                  out.ptr, flags.ptr, state.ptr + 4, None))
+        ref = skv.DeviceBuffer(4 * hidden)
+        ref_flags = skv.DeviceBuffer.from_numpy(np.zeros(1, np.int32))
+        skv.embedding(d_t, skv.DTYPE_FP32, vocab, hidden, d_ids, idx, ref, ref_flags)
+        np.testing.assert_array_equal(out.download(np.uint32, hidden), ref.download(np.uint32, hidden))
+        f = flags.download(np.int32, 5)
+        assert f[3] == ref_flags.download(np.int32, 1)[0] and not f[[0, 1, 2, 4]].any()
+    logits = rng.standard_normal((4, 32000)).astype(np.float32)
+    logits[2, [7, 31999]] = 9.0
+    logits[3, 11] = np.nan
+    for r in range(4):
+        d_l = skv.DeviceBuffer.from_numpy(logits[r])
+        out_ids = skv.DeviceBuffer.from_numpy(np.full(8, -1, np.int32))
+        state = skv.DeviceBuffer.from_numpy(np.array([r + 2, 1], np.int32))
+        flags = skv.DeviceBuffer.from_numpy(np.zeros(3, np.int32))
+        gpu._check(skv.lib().skv_argmax_at_f32(d_l.ptr, 32000, out_ids.ptr, state.ptr, flags.ptr, state.ptr + 4,
+                                               None))
+        ref_ids = skv.DeviceBuffer.from_numpy(np.full(8, -1, np.int32))
+        ref_flags = skv.DeviceBuffer.from_numpy(np.zeros(1, np.int32))
+        skv.argmax(d_l, 32000, ref_ids, r + 2, ref_flags)
+        assert list(out_ids.download(np.int32, 8)) == list(ref_ids.download(np.int32, 8))
+        f = flags.download(np.int32, 3)
+        assert f[1] == ref_flags.download(np.int32, 1)[0] and f[0] == 0 and f[2] == 0
+
+
 def _device_sample(logits_row, temp, k, p, u):
     ids = skv.DeviceBuffer.from_numpy(np.zeros(1, np.int32))
     flags = skv.DeviceBuffer.from_numpy(np.zeros(1, np.int32))
@@ -389,3 +427,62 @@ def test_generate_tinyllama_matches_reference(gpu, ckpt_dir):
     # tokens teacher-forced through the cache it wrote: the same bounds.
     _, err = _check_forced(path, golden, n_prompt=100)
     print(f"tinyllama max logit error after a 100-token prompt pass {err:.3e}")
+
+
+# ---------------------------------------------------------------------------
+# Decode steps replayed from a HIP graph against step-by-step launches
+# ---------------------------------------------------------------------------
+def _small(ckpt_dir):
+    path, _ = make_checkpoint.ensure("small", ckpt_dir)
+    return path
+
+
+@pytest.mark.parametrize("max_new", [2, 40, 240])
+def test_graph_replay_matches_eager(gpu, ckpt_dir, max_new):
+    """Generations whose steps are replayed from one captured graph give the
+    tokens, block tables and last logits (bits) of the same generations
+    launched step by step, over three generations in a row (the graph is
+    recorded once and reused).  240 new tokens fill the 16-block short-table
+    limit exactly (16 + 240 = 256)."""
+    path = _small(ckpt_dir)
+    prompt = [3, 141, 59, 265, 358, 979, 323, 846, 264, 338, 327, 950, 288, 419, 716, 939]
+    g = tool("generate", path, max_new, -1, "--repeat", 3, "--", *prompt)
+    e = tool("generate", path, max_new, -1, "--repeat", 3, "--eager", "--", *prompt)
+    assert g["ok"] and e["ok"], (g, e)
+    assert g["replayed"] == [1, 1, 1] and e["replayed"] == [0, 0, 0]
+    assert g["runs"] == e["runs"] and len(g["tokens"]) == 16 + max_new
+    assert g["runs"][0] == g["runs"][1] == g["runs"][2]
+    assert g["tables"] == e["tables"]
+    assert g["logits_fnv"] == e["logits_fnv"] and len(set(g["logits_fnv"])) == 1
+
+
+def test_graph_replay_past_the_short_table_limit_runs_eagerly(gpu, ckpt_dir):
+    path = _small(ckpt_dir)
+    g = tool("generate", path, 241, -1, "--", *range(1, 17))   # 257 tokens: 17 blocks
+    assert g["ok"] and g["replayed"] == [0]
+
+
+def test_graph_replay_eos_and_sampling(gpu, ckpt_dir):
+    """EOS in the middle of a replayed generation, and sampled generations
+    (the draws stay launches of their own before each replayed step): the same
+    tokens, tables and flags behaviour as step-by-step launches."""
+    path = _small(ckpt_dir)
+    prompt = [11, 22, 33, 44, 55]
+    base = tool("generate", path, 60, -1, "--eager", "--", *prompt)
+    assert base["ok"]
+    # A token chosen at step 20 or later (and not in the prompt) ends the
+    # generation at its first occurrence.
+    eos = next(t for t in base["tokens"][len(prompt) + 20:] if t not in prompt)
+    first = base["tokens"].index(eos, len(prompt))
+    for extra in ([], ["--eager"]):
+        r = tool("generate", path, 60, eos, *extra, "--", *prompt)
+        assert r["ok"] and r["tokens"] == base["tokens"][:first + 1], (extra, r)
+    runs = {}
+    for extra in ([], ["--eager"]):
+        r = tool("generate", path, 50, -1, "--temp", 0.9, "--top-k", 20, "--top-p", 0.95, "--seed", 7,
+                 "--repeat", 2, *extra, "--", *prompt)
+        assert r["ok"], r
+        runs[bool(extra)] = r
+    assert runs[False]["replayed"] == [1, 1] and runs[True]["replayed"] == [0, 0]
+    assert runs[False]["runs"] == runs[True]["runs"]
+    assert runs[False]["logits_fnv"] == runs[True]["logits_fnv"]
