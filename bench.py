@@ -692,8 +692,9 @@ def run_prefill(steps: int, warmup: int):
                      "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
                      "traffic": profile_traffic("cfg5", "prefill"),
                      "algorithmic_flops": flops,
-                     "note": ("P.V runs as two bf16 MFMAs (P split into hi + lo parts), so the "
-                              "matrix cores execute 1.5x the algorithmic flops")},
+                     "note": ("Q.K^T in bf16 and P.V in fp16 (V converted exactly as it is "
+                              "staged, P rounded to fp16) on the matrix cores with fp32 "
+                              "accumulation: they execute the algorithmic flops")},
         "kv_gbs": round(kv_bytes / (ms / 1e3) / 1e9, 2),
     }), flush=True)
     return 0

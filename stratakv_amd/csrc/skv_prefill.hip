@@ -16,9 +16,12 @@
 // * Keys are walked 64 at a time (four 16-token blocks) up to the tile's last
 //   position, through two LDS buffers: the next step's K/V are loaded into
 //   registers while the current step is computed, then stored into the other
-//   buffer; one barrier per step.  Rows are padded (K by 16 bytes, V by 32) so
-//   the operand reads below hit distinct banks.  The heaviest tiles (the
-//   latest tokens of each sequence) are scheduled first.
+//   buffer; one barrier per step.  K rows are unpadded, each 16-byte chunk c
+//   of row r stored at chunk position c ^ (r % chunks per row); V rows are
+//   padded by 32 bytes.  Both make the operand reads below conflict-free (a
+//   16-byte padding of K had left half of the K reads' LDS cycles in bank
+//   conflicts).  The heaviest tiles (the latest tokens of each sequence) are
+//   scheduled first.
 // * The step loop keeps its K/V loads in flight through the compute: they are
 //   unconditional buffer loads through a per-(wavefront, block) descriptor that
 //   spans exactly the block's existing rows (rows past the context and absent
@@ -38,10 +41,14 @@
 //   lane group j), and the V^T operand comes out of the row-major V tile with
 //   the LDS transpose read (ds_read_b64_tr_b16: in each 16-lane group, lane
 //   4a + c receives element c of the 8-byte rows addressed by lanes a, a+4,
-//   a+8, a+12), in the same key order.  P is split into hi + lo bf16 parts
-//   (two MFMAs) so the P.V products keep ~16 mantissa bits, like the fp32
-//   loops of the reference.
-// * Online softmax in the exp2 domain with lazy rescaling (threshold 2^8).
+//   a+8, a+12), in the same key order.  This product runs in fp16
+//   (v_mfma_f32_16x16x32_f16, fp32 accumulation): V is converted from bf16
+//   as it is staged (exact for |v| in [2^-14, 65504]; below, an absolute error
+//   under 2^-25), P is rounded to the nearest fp16 (11 significant bits,
+//   against bf16's 8).  A tile that stages a V element above 65504 (finite
+//   in bf16, or infinite) has its rows recomputed in fp32 instead.
+// * Online softmax in the exp2 domain with lazy rescaling (threshold 2^8, so
+//   P <= 256 stays well inside the fp16 range).
 // Other shapes run a simple kernel (one wavefront per token and query head).
 #include "skv_common.h"
 
@@ -51,6 +58,9 @@
 namespace skv {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -130,11 +140,16 @@ constexpr int kPrefillKeys = 64;                   // keys per step
 
 template <int HD>
 struct PrefillLds {
-    static constexpr int KRS = HD * 2 + 16;        // K row stride (bytes)
+    // K rows unpadded: 16-byte chunk c of row r stored at chunk position
+    // c ^ (r % chunks per row).
+    static constexpr int KRS = HD * 2;             // K row stride (bytes)
     static constexpr int VRS = HD * 2 + 32;        // V row stride (bytes)
     static constexpr int KB = kPrefillKeys * KRS;
     static constexpr int BUF = KB + kPrefillKeys * VRS;
     static constexpr int TOTAL = 2 * BUF;          // two buffers; the tile scan follows
+    __device__ static constexpr int k_chunk(int row, int c) {
+        return row * KRS + (c ^ (row & (HD / 8 - 1))) * 16;
+    }
 };
 
 typedef short v4s_t __attribute__((ext_vector_type(4)));
@@ -143,6 +158,67 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
     const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
     return __builtin_bit_cast(uint32_t, v);
+}
+
+// fp32 recomputation of wavefront wv's rows of a tile (the MFMA kernel's
+// path when a V element of the tile is beyond the fp16 range): lanes over 64
+// keys for the scores, over head dims for P.V, the keys' probabilities and
+// rows broadcast by shuffles.  Row r = token r / G, head r % G of kv head kvh.
+template <int HD, int G, bool QF32>
+__device__ __forceinline__ void prefill_rows_fp32(const PrefillParams& p, int b, int kvh, int wv, int ntok, int tok0,
+                                               int base_pos, int keys_end, const int32_t* table) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row_elems = static_cast<int64_t>(p.Hkv) * HD;
+    for (int rr = 0; rr < 32; ++rr) {
+        const int r = wv * 32 + rr;
+        const int qtok = r / G;
+        if (qtok >= ntok) break;
+        const int64_t qoff = (static_cast<int64_t>(p.offsets[b] + tok0 + qtok) * p.Hq + kvh * G + r % G) * HD;
+        const int nkeys = min(base_pos + qtok + 1, keys_end);
+        float m = -INFINITY, l = 0.0f;
+        float acc[HD / 64];
+#pragma unroll
+        for (int k = 0; k < HD / 64; ++k) acc[k] = 0.0f;
+        for (int t0 = 0; t0 < nkeys; t0 += 64) {
+            const int tk = t0 + lane;
+            float score = -INFINITY;
+            int64_t roff = -1;
+            if (tk < nkeys) {
+                const int64_t pb = table[tk >> 4];
+                if (pb >= 0 && pb < p.total_blocks) {
+                    roff = (pb * 16 + (tk & 15)) * row_elems + static_cast<int64_t>(kvh) * HD;
+                    float dot = 0.0f;
+                    for (int d = 0; d < HD; ++d) {
+                        const float qv = QF32 ? static_cast<const float*>(p.q)[qoff + d]
+                                              : bf16_to_f32(static_cast<const uint16_t*>(p.q)[qoff + d]);
+                        dot = fmaf(qv, bf16_to_f32(p.k[roff + d]), dot);
+                    }
+                    score = dot * p.qscale;
+                }
+            }
+            const float mn = fmaxf(m, wave_max(score));
+            const float ms = mn == -INFINITY ? 0.0f : mn;
+            const float alpha = fast_exp2(m - ms);
+            const float pp = fast_exp2(score - ms);
+            l = l * alpha + wave_sum(pp);
+            m = mn;
+#pragma unroll
+            for (int k = 0; k < HD / 64; ++k) acc[k] *= alpha;
+            const int cnt = min(64, nkeys - t0);
+            for (int jj = 0; jj < cnt; ++jj) {
+                const int64_t vr = (static_cast<int64_t>(__shfl(static_cast<int>(roff >> 32), jj, 64)) << 32) |
+                                   static_cast<uint32_t>(__shfl(static_cast<int>(roff), jj, 64));
+                const float pj = __shfl(pp, jj, 64);
+                if (vr < 0) continue;
+#pragma unroll
+                for (int k = 0; k < HD / 64; ++k) acc[k] = fmaf(pj, bf16_to_f32(p.v[vr + lane + 64 * k]), acc[k]);
+            }
+        }
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        float* o = p.out + qoff;
+#pragma unroll
+        for (int k = 0; k < HD / 64; ++k) o[lane + 64 * k] = acc[k] * inv;
+    }
 }
 
 template <int HD, int G, bool QF32>
@@ -160,7 +236,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
     static_assert(LOADS >= 1 && KS * CH % NT == 0, "load split");
 
     extern __shared__ __align__(16) unsigned char lds[];
-    int* T_s = reinterpret_cast<int*>(lds + Lds::TOTAL);   // [B + 2]
+    int* T_s = reinterpret_cast<int*>(lds + Lds::TOTAL);   // [B + 3]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -169,6 +245,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
     const int kvh = blockIdx.x % p.Hkv;
     const int slot = blockIdx.x / p.Hkv;
 
+    if (tid == 0) T_s[p.B + 2] = 0;   // set when the tile's rows must be recomputed in fp32
     const int ntiles = prefill_tile_scan(p, T_s);
     if (slot >= ntiles) return;
     // Heaviest first: with equal tile counts, the last tile of every sequence,
@@ -313,6 +390,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
     };
     // Rows of keys that do not exist are stored as zeros (V must not carry
     // NaN from unused slots into 0 * V).
+    // V is stored as fp16 (exact for |v| in [2^-14, 65504]; smaller values
+    // keep an absolute error below 2^-25); vmax tracks the largest |V| this
+    // thread stored.
+    float vmax = 0.0f;
     auto store_step = [&](int buf, const u32x4_t (&kr)[LOADS], const u32x4_t (&vr)[LOADS]) {
         unsigned char* kb = lds + buf * Lds::BUF;
         unsigned char* vb = kb + Lds::KB;
@@ -320,8 +401,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
         for (int u = 0; u < LOADS; ++u) {
             const int idx = tid + NT * u;
             const int lr = idx / CH, lc = idx % CH;
-            *reinterpret_cast<u32x4_t*>(kb + lr * Lds::KRS + lc * 16) = kr[u];
-            *reinterpret_cast<u32x4_t*>(vb + lr * Lds::VRS + lc * 16) = vr[u];
+            *reinterpret_cast<u32x4_t*>(kb + Lds::k_chunk(lr, lc)) = kr[u];
+            u32x4_t w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = __uint_as_float(vr[u][e] << 16), hi = __uint_as_float(vr[u][e] & 0xFFFF0000u);
+                vmax = fmaxf(vmax, fmaxf(fabsf(lo), fabsf(hi)));
+                w[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t));
+            }
+            *reinterpret_cast<u32x4_t*>(vb + lr * Lds::VRS + lc * 16) = w;
         }
     };
 
@@ -361,7 +449,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
             s[1][kt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int cc = 0; cc < NKC; ++cc) {
-                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(kb + (kt * 16 + t) * Lds::KRS + (4 * cc + j) * 16);
+                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(kb + Lds::k_chunk(kt * 16 + t, 4 * cc + j));
 #pragma unroll
                 for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -376,7 +464,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
         // all exist and precede the wave's first query position (all but the
         // diagonal steps of a tile) skip the mask.
         const bool need_mask = !(valid_cur == ~0ull && k0 + KS - 1 <= wave_first_pos);
-        bf16x8_t phi[2][KS / 32], plo[2][KS / 32];
+        f16x8_t pf[2][KS / 32];   // P^T operands
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             float sc[KS / 4];
@@ -417,15 +505,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
             // 32-key chunk h: keys {4j..4j+3} = kt 2h, {16+4j..} = kt 2h+1.
 #pragma unroll
             for (int h = 0; h < KS / 32; ++h) {
-                uint32_t hw[4], lw[4];
+                uint32_t hw[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float x0 = pr[8 * h + 2 * e], x1 = pr[8 * h + 2 * e + 1];
-                    hw[e] = pack2_bf16(x0, x1);
-                    lw[e] = pack2_bf16(x0 - __uint_as_float(hw[e] << 16), x1 - __uint_as_float(hw[e] & 0xFFFF0000u));
-                }
-                phi[c][h] = __builtin_bit_cast(bf16x8_t, u32x4_t{hw[0], hw[1], hw[2], hw[3]});
-                plo[c][h] = __builtin_bit_cast(bf16x8_t, u32x4_t{lw[0], lw[1], lw[2], lw[3]});
+                for (int e = 0; e < 4; ++e)
+                    hw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                        f32x2_t{pr[8 * h + 2 * e], pr[8 * h + 2 * e + 1]}, f16x2_t));
+                pf[c][h] = __builtin_bit_cast(f16x8_t, u32x4_t{hw[0], hw[1], hw[2], hw[3]});
             }
         }
 
@@ -446,12 +531,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
                 }
                 const u32x4_t w = {__builtin_bit_cast(uint2, part[0]).x, __builtin_bit_cast(uint2, part[0]).y,
                                    __builtin_bit_cast(uint2, part[1]).x, __builtin_bit_cast(uint2, part[1]).y};
-                const bf16x8_t a = __builtin_bit_cast(bf16x8_t, w);
+                const f16x8_t a = __builtin_bit_cast(f16x8_t, w);
 #pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    acc[dt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, phi[c][h], acc[dt][c], 0, 0, 0);
-                    acc[dt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, plo[c][h], acc[dt][c], 0, 0, 0);
-                }
+                for (int c = 0; c < 2; ++c)
+                    acc[dt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pf[c][h], acc[dt][c], 0, 0, 0);
             }
         }
 
@@ -460,6 +543,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
         valid_cur = valid_next;
 #pragma unroll
         for (int hb = 0; hb < KS / 16; ++hb) blk1[hb] = blk2[hb];
+    }
+
+    // A V element beyond the fp16 range (finite above 65504, or infinite)
+    // anywhere in the tile: its rows are recomputed in fp32.
+    if (vmax > 65504.0f) T_s[p.B + 2] = 1;
+    __syncthreads();
+    if (T_s[p.B + 2] != 0) {
+        prefill_rows_fp32<HD, G, QF32>(p, b, kvh, wv, ntok, tok0, base_pos, keys_end, table);
+        return;
     }
 
     // ---- output: O[row][dims 16 dt + 4j + i] = acc / l
@@ -565,7 +657,7 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillParams p, in
 
 template <int HD, int G, bool QF32>
 int launch_prefill_shape(const PrefillParams& p, unsigned grid, hipStream_t s) {
-    const size_t lds = PrefillLds<HD>::TOTAL + sizeof(int) * (static_cast<size_t>(p.B) + 2);
+    const size_t lds = PrefillLds<HD>::TOTAL + sizeof(int) * (static_cast<size_t>(p.B) + 3);
     auto kern = prefill_mfma_kernel<HD, G, QF32>;
     static size_t granted = 0;   // largest dynamic LDS size requested so far
     if (lds > granted) {

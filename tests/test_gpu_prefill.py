@@ -4,7 +4,8 @@ loops of src/layers/attention.cpp:263-337, pinned in test_oracle_prefill.py
 against the reference's own chunked PagedAttention::forward).
 
 Tolerance: |gpu - ref| <= 2e-3 + 1e-2 * |ref| (fp32 accumulation on the GPU,
-bf16 K/V; P.V on the matrix cores with P split into hi + lo bf16 parts).
+bf16 K/V; P.V on the matrix cores in fp16, V above the fp16 range recomputed
+in fp32).
 Outputs start as NaN so a missing store fails; unused slots of the last block
 hold NaN so a key past the chunk that leaked into P.V fails too.
 """
@@ -117,3 +118,25 @@ def test_prefill_long_chunk_sampled(gpu):
     ref = oracle.paged_decode(c["q_ref"][rows], c["kp"], c["vp"], c["tables"][seqs[rows]],
                               (pos[rows] + 1).astype(np.int32), 8, 16, c["scale"], threads=8)
     assert_close(got[rows], ref, what="long chunk rows")
+
+
+@pytest.mark.parametrize("geom", [(32, 4, 64), (64, 8, 128)], ids=["tl", "l70"])
+@pytest.mark.parametrize("q_dtype", ["bf16", "fp32"])
+def test_prefill_v_beyond_fp16_range(gpu, geom, q_dtype):
+    """V elements the matrix-core P.V cannot take as fp16 (finite bf16 values
+    above 65504) in a few keys: the tiles that read them are recomputed in
+    fp32, the others keep the fp16 P.V.  65280, the largest bf16 value within
+    the fp16 range, takes the fp16 path exactly."""
+    Hq, Hkv, hd = geom
+    c = _case(Hq, Hkv, hd, 16, CHUNKS[1], CHUNKS[0], q_dtype, seed=hd + 7)
+    big = oracle.f32_to_bf16(np.array([1.0e6, -3.0e5, 65280.0, 7.0e4], np.float32))
+    assert oracle.bf16_to_f32(big)[2] == 65280.0
+    tables = c["tables"]
+    # (sequence, key, kv head, dim, value): keys inside each sequence's context
+    for b, key, h, d, v in ((5, 3, 0, 1, big[0]), (5, 1500, Hkv - 1, hd - 1, big[1]), (4, 320, 1, 5, big[2]),
+                            (6, 6, 0, 0, big[3])):
+        assert key < c["lens"][b]
+        c["vp"][tables[b, key // 16], key % 16, h, d] = v
+    got = _gpu(gpu, c)
+    assert_close(got, _ref(c), what=f"prefill with large V {geom} q={q_dtype}")
+    assert_close(got, _ref(c, "f64"), what=f"prefill with large V {geom} q={q_dtype} vs f64")
