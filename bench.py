@@ -29,6 +29,7 @@ bounded sample of sequences of the same workload.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import math
 import os
@@ -746,15 +747,40 @@ def cpu_compare(reps: int = 5):
     return 0
 
 
+# The kernel sources behind each traffic summary: the file with the kernels and
+# the device headers it includes (the C ABI header declares no device code).
+TRAFFIC_SOURCES = {"decode": ("skv_decode.hip", "skv_append.h", "skv_common.h"),
+                   "prefill": ("skv_prefill.hip", "skv_common.h")}
+
+
+def kernel_fingerprint(kind: str) -> str:
+    """First 16 hex digits of the SHA-256 of the kernel sources of `kind`, in
+    TRAFFIC_SOURCES order: what a counter summary was measured on."""
+    h = hashlib.sha256()
+    for name in TRAFFIC_SOURCES[kind]:
+        with open(os.path.join(ROOT, "stratakv_amd", "csrc", name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def profile_traffic(workload_key: str, kind: str = "decode"):
     """HBM bytes per launch of the measured kernel(s) from the committed
     rocprof counter summary profiles/<kind>_traffic_<workload_key>.md, if one
-    exists for this workload."""
+    exists for this workload and was measured on the current kernel sources
+    (its kernel_sources_sha256 line equals kernel_fingerprint(kind)); None
+    otherwise, with the reason on stderr."""
     path = os.path.join(ROOT, "profiles", f"{kind}_traffic_{workload_key}.md")
     if not os.path.exists(path):
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
-    return float(m.group(1)) if m else None
+    text = open(path).read()
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
+    f = re.search(r"kernel_sources_sha256:\s*([0-9a-f]+)", text)
+    current = kernel_fingerprint(kind)
+    if not m or not f or f.group(1) != current:
+        log(f"{os.path.basename(path)} was measured on other kernel sources "
+            f"({f.group(1) if f else 'no fingerprint'}, now {current}): traffic reported as null")
+        return None
+    return float(m.group(1))
 
 
 def copy_calibration(mib: int) -> int:
@@ -831,10 +857,16 @@ def main() -> int:
     ap.add_argument("--contiguous-tables", action="store_true",
                     help="with --load-calibration --config 2, 3 or 4: the same lengths with each "
                          "sequence's blocks consecutive in a pool of the blocks used")
+    ap.add_argument("--kernel-fingerprint", choices=sorted(TRAFFIC_SOURCES),
+                    help="print the fingerprint of the decode or prefill kernel sources that a "
+                         "traffic summary under profiles/ records, and exit")
     ap.add_argument("--cpu-compare", action="store_true",
                     help="time the oracle's decode loops against the reference's own attention "
                          "(oracle/_ref), 1 thread, at cfg2 geometry, and exit (CPU only)")
     args = ap.parse_args()
+    if args.kernel_fingerprint:
+        print(kernel_fingerprint(args.kernel_fingerprint))
+        return 0
     if args.cpu_compare:
         return cpu_compare()
     if args.copy_calibration:
