@@ -140,3 +140,45 @@ def test_prefill_v_beyond_fp16_range(gpu, geom, q_dtype):
     got = _gpu(gpu, c)
     assert_close(got, _ref(c), what=f"prefill with large V {geom} q={q_dtype}")
     assert_close(got, _ref(c, "f64"), what=f"prefill with large V {geom} q={q_dtype} vs f64")
+
+
+def _ref_skipping_invalid_blocks(c):
+    """float64 causal attention over exactly the keys whose block id lies in
+    the pool (the kernels skip absent and out-of-pool table entries; the
+    oracle, like the reference, refuses them)."""
+    seqs, pos = oracle.prefill_positions(c["offsets"], c["lens"])
+    G = c["Hq"] // c["Hkv"]
+    kp = oracle.bf16_to_f32(c["kp"]).astype(np.float64)
+    vp = oracle.bf16_to_f32(c["vp"]).astype(np.float64)
+    out = np.zeros((c["N"], c["Hq"], c["hd"]))
+    for n in range(c["N"]):
+        keys = np.arange(pos[n] + 1)
+        blk = c["tables"][seqs[n], keys // c["bs"]].astype(np.int64)
+        ok = (blk >= 0) & (blk < c["total"])
+        keys, blk = keys[ok], blk[ok]
+        for h in range(c["Hq"]):
+            kvh = h // G
+            K = kp[blk, keys % c["bs"], kvh]
+            V = vp[blk, keys % c["bs"], kvh]
+            s = K @ c["q_ref"][n, h].astype(np.float64) * c["scale"]
+            w = np.exp(s - s.max())
+            out[n, h] = (w / w.sum()) @ V
+    return out
+
+
+@pytest.mark.parametrize("geom", [(32, 4, 64), (64, 8, 128)], ids=["tl", "l70"])
+def test_prefill_skips_absent_and_out_of_pool_blocks(gpu, geom):
+    """Table entries inside a context that are absent (-1) or outside the pool
+    are skipped: at the start of a 64-key step (the step's existing keys are
+    then not a prefix), at its end, and a sequence's first block."""
+    Hq, Hkv, hd = geom
+    c = _case(Hq, Hkv, hd, 16, [40, 333, 200], [17, 64, 30], seed=hd + 23)
+    # The brute force is the oracle where the oracle applies (no invalid ids).
+    assert_close(_ref_skipping_invalid_blocks(c), _ref(c), what="brute force vs oracle")
+    t = c["tables"]
+    t[1, 4] = -1                     # keys 64..79: the first block of step 1
+    t[1, 11] = c["total"] + 7        # keys 176..191: the last block of step 2
+    t[1, 16] = -1                    # keys 256..271 (the chunk's diagonal steps)
+    t[2, 0] = -1                     # the sequence's first block
+    got = _gpu(gpu, c)
+    assert_close(got, _ref_skipping_invalid_blocks(c), what=f"prefill with invalid blocks {geom}")
