@@ -31,11 +31,19 @@
 //   the query operands are complete before the loop.  With per-lane branches
 //   around the loads and a scalar table read per block, the compiler had
 //   waited for all of them (vmcnt(0)) before the step's first MFMA.
+// * Little scalar work per step: the CU's 8 wavefronts share one scalar unit
+//   and all reach the step's load issue together after the barrier.  Each
+//   wavefront stages half of one block per step; its byte offset and extent
+//   come precomputed from the table window (once per 64 entries, on the
+//   VALU), and a step carries a 4-bit mask of its existing blocks instead of
+//   a 64-bit mask of keys.  (Four block ids, their products and a key mask
+//   per wavefront and step had taken ~19 % of the step.)
 // * S^T = K Q^T on the matrix cores (v_mfma_f32_16x16x32_bf16: keys as rows,
 //   query rows as columns), so each lane holds the scores of ONE query row:
 //   the causal/validity mask, the row max (2 shuffles) and the rescale of that
 //   row's output are lane-local.  Each K operand read serves both column
-//   groups.
+//   groups.  An fp32 query is split into hi + lo bf16 parts (two MFMAs), so
+//   its products keep ~16 significant bits.
 // * O^T += V^T P^T, also on the matrix cores: P goes from the S^T output
 //   registers straight into the B operand (keys {4j..4j+3, 16+4j..16+4j+3} of
 //   lane group j), and the V^T operand comes out of the row-major V tile with
@@ -327,65 +335,68 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
             }
 
     // Table entries 64 per VGPR (lane i holds entry tb + i), the next 64
-    // loaded one chunk ahead; a step's four block ids are read with
-    // v_readlane, so the loop issues no scalar load (whose out-of-order
-    // return would make every LDS wait a full lgkmcnt(0)) and no K/V load
-    // waits on a table read.  -1: absent or outside the pool.
+    // loaded one chunk ahead.  Once per 64 entries each lane turns its entry
+    // into the block's byte offset and the bytes of its existing rows (0 for
+    // an absent block, an id outside the pool, or a block at or past
+    // keys_end), and a ballot gives wmask (bit i: block tb + i exists); a step
+    // then reads its block with three v_readlane and no scalar arithmetic on
+    // the id.  The loop issues no scalar load (whose out-of-order return would
+    // make every LDS wait a full lgkmcnt(0)) and no K/V load waits on a table
+    // read.
+    static_assert(kPrefillWaves * 8 == KS && LOADS * (64 / CH) == 8, "a wavefront stages half a block per step");
+    const int64_t row_bytes = row_stride * 2;
     const int nb_tab = max(nb_seq, 1);
     auto tab_load = [&](int first) -> int { return table[min(first + lane, nb_tab - 1)]; };
     int tb = 0;
-    int tv = tab_load(0);
     int tvn = tab_load(64);
-    auto step_blocks = [&](int k0s, int (&blk)[KS / 16]) {   // keys k0s .. k0s + KS - 1
-        const int b0 = k0s >> 4;
-        if (b0 - tb >= 64) {   // steps are visited in order: advance one chunk
+    uint32_t off_lo = 0, off_hi = 0;   // this lane's window entry: byte offset of the block's rows
+    int nrec_v = 0;                    // and the bytes of its existing rows of one kv head
+    uint64_t wmask = 0;
+    auto set_window = [&](int e) {
+        const bool ok = (tb + lane) * 16 < keys_end && e >= 0 && e < p.total_blocks;
+        const uint64_t off = ok ? static_cast<uint64_t>(e) * static_cast<uint64_t>(16 * row_bytes) : 0ull;
+        off_lo = static_cast<uint32_t>(off);
+        off_hi = static_cast<uint32_t>(off >> 32);
+        nrec_v = ok ? static_cast<int>(min(16, keys_end - (tb + lane) * 16) * row_bytes) : 0;
+        wmask = __ballot(ok);
+    };
+    set_window(tab_load(0));
+    auto window = [&](int s) {   // blocks 4 s .. 4 s + 3; steps are visited in order
+        if (4 * s - tb >= 64) {
             tb += 64;
-            tv = tvn;
+            set_window(tvn);
             tvn = tab_load(tb + 64);
         }
-#pragma unroll
-        for (int hb = 0; hb < KS / 16; ++hb) {
-            const int kb = (b0 + hb) * 16;
-            const int e = __builtin_amdgcn_readlane(tv, b0 + hb - tb);
-            blk[hb] = kb < keys_end && e >= 0 && e < p.total_blocks ? e : -1;
-        }
     };
-    // Loads of a step: thread -> (key row lr, chunk lc) for each of LOADS
-    // passes, CH consecutive threads per row slice; a wavefront's rows of one
-    // pass lie in one block, read through a buffer descriptor that spans
-    // exactly the block's existing rows (0 for an absent block), so rows that
-    // do not exist load as zeros and every load is issued unconditionally.
-    // `valid` (the same in every thread) has bit k set when key k0 + k exists.
-    const int64_t row_bytes = row_stride * 2;
-    auto load_step = [&](int k0, const int (&blk)[KS / 16], u32x4_t (&kr)[LOADS], u32x4_t (&vr)[LOADS],
-                         uint64_t& valid) {
-        valid = 0;
+    // Bit hb set when block hb of step s exists.
+    auto step_nib = [&](int s) -> uint32_t { return static_cast<uint32_t>(wmask >> (4 * s - tb)) & 0xFu; };
+    // Loads of a step: wavefront wv stages rows 8 (wv & 1) .. + 7 of the
+    // step's block wv >> 1 (LOADS passes of 64 / CH rows, CH consecutive lanes
+    // per row slice), through a buffer descriptor that spans exactly the
+    // block's existing rows (0 for an absent block), so rows that do not exist
+    // load as zeros and every load is issued unconditionally.
+    const int blk_w = wv >> 1;
+    const uint16_t* const kbase = p.k + static_cast<int64_t>(kvh) * HD;
+    const uint16_t* const vbase = p.v + static_cast<int64_t>(kvh) * HD;
+    int row_w[LOADS], voff_w[LOADS];
 #pragma unroll
-        for (int hb = 0; hb < KS / 16; ++hb) {
-            const int kb = k0 + 16 * hb;
-            if (blk[hb] >= 0) {
-                const int cnt = min(16, keys_end - kb);
-                valid |= static_cast<uint64_t>(cnt == 16 ? 0xFFFFu : ((1u << cnt) - 1u)) << (16 * hb);
-            }
-        }
+    for (int u = 0; u < LOADS; ++u) {
+        row_w[u] = 8 * (wv & 1) + u * (64 / CH) + lane / CH;   // row within the block
+        voff_w[u] = static_cast<int>(row_w[u] * row_bytes + (lane % CH) * 16);
+    }
+    auto load_step = [&](int s, u32x4_t (&kr)[LOADS], u32x4_t (&vr)[LOADS]) {
+        const int slot = 4 * s + blk_w - tb;
+        const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(off_lo, slot))) |
+                             static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(off_hi, slot))) << 32;
+        const int nrec = __builtin_amdgcn_readlane(nrec_v, slot);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<unsigned char*>(reinterpret_cast<const unsigned char*>(kbase)) + off, 0, nrec, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<unsigned char*>(reinterpret_cast<const unsigned char*>(vbase)) + off, 0, nrec, 0x00020000);
 #pragma unroll
         for (int u = 0; u < LOADS; ++u) {
-            const int idx = tid + NT * u;
-            const int lr = idx / CH, lc = idx % CH;
-            const int hb = __builtin_amdgcn_readfirstlane((wv * 64 + NT * u) / CH) >> 4;
-            int pb = blk[0];
-#pragma unroll
-            for (int h2 = 1; h2 < KS / 16; ++h2) pb = hb == h2 ? blk[h2] : pb;
-            const int cnt = pb >= 0 ? min(16, keys_end - (k0 + 16 * hb)) : 0;
-            const int64_t base = static_cast<int64_t>(pb >= 0 ? pb : 0) * 16 * row_stride + static_cast<int64_t>(kvh) * HD;
-            const int nrec = static_cast<int>(cnt * row_bytes);
-            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint16_t*>(p.k + base), 0, nrec, 0x00020000);
-            const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint16_t*>(p.v + base), 0, nrec, 0x00020000);
-            const int voff = static_cast<int>((lr & 15) * row_bytes + lc * 16);
-            kr[u] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, voff, 0, 0));
-            vr[u] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0));
+            kr[u] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, voff_w[u], 0, 0));
+            vr[u] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff_w[u], 0, 0));
         }
     };
     // Rows of keys that do not exist are stored as zeros (V must not carry
@@ -399,8 +410,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
         unsigned char* vb = kb + Lds::KB;
 #pragma unroll
         for (int u = 0; u < LOADS; ++u) {
-            const int idx = tid + NT * u;
-            const int lr = idx / CH, lc = idx % CH;
+            const int lr = 16 * blk_w + row_w[u], lc = lane % CH;
             *reinterpret_cast<u32x4_t*>(kb + Lds::k_chunk(lr, lc)) = kr[u];
             u32x4_t w;
 #pragma unroll
@@ -423,20 +433,20 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
 
     const int nsteps = cdiv(keys_end, KS);
     u32x4_t kr[LOADS], vr[LOADS];
-    uint64_t valid_cur = 0, valid_next = 0;
-    int blk1[KS / 16], blk2[KS / 16];   // block ids of steps st + 1 and st + 2
+    uint32_t nib_cur = 0, nib_next = 0;   // blocks of the current and next step that exist
     if (nsteps > 0) {
-        int blk0[KS / 16];
-        step_blocks(0, blk0);
-        step_blocks(KS, blk1);
-        load_step(0, blk0, kr, vr, valid_cur);
+        nib_cur = step_nib(0);
+        load_step(0, kr, vr);
         store_step(0, kr, vr);
     }
     __syncthreads();
     for (int st = 0; st < nsteps; ++st) {
         const int cur = st & 1;
-        step_blocks((st + 2) * KS, blk2);
-        if (st + 1 < nsteps) load_step((st + 1) * KS, blk1, kr, vr, valid_next);  // in flight during compute
+        if (st + 1 < nsteps) {   // in flight during compute
+            window(st + 1);
+            nib_next = step_nib(st + 1);
+            load_step(st + 1, kr, vr);
+        }
         const unsigned char* kb = lds + cur * Lds::BUF;
         const unsigned char* vb = kb + Lds::KB;
         const int k0 = st * KS;
@@ -458,12 +468,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
             }
         }
 
-        // ---- online softmax per row, P^T operands (hi + lo bf16 parts).
+        // ---- online softmax per row, P^T operands (fp16).
         // Scores stay unscaled: qscale > 0, so max(s) * qscale is the max of
         // the scaled scores, and the exponent is one fma.  Steps whose keys
         // all exist and precede the wave's first query position (all but the
         // diagonal steps of a tile) skip the mask.
-        const bool need_mask = !(valid_cur == ~0ull && k0 + KS - 1 <= wave_first_pos);
+        const bool need_mask = !(nib_cur == 0xFu && keys_end - k0 >= KS && k0 + KS - 1 <= wave_first_pos);
         f16x8_t pf[2][KS / 32];   // P^T operands
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
@@ -473,14 +483,16 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
 #pragma unroll
                 for (int i = 0; i < 4; ++i) sc[kt * 4 + i] = s[c][kt][i];
             if (need_mask) {
+                // Key kl exists when its block does (bit kt of nib_cur) and
+                // k0 + kl < keys_end; it is visible when k0 + kl <= qpos.
+                const int lim = min(qpos[c] - k0, keys_end - k0 - 1);
 #pragma unroll
-                for (int kt = 0; kt < KS / 16; ++kt)
+                for (int kt = 0; kt < KS / 16; ++kt) {
+                    const bool present = (nib_cur >> kt) & 1u;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int kl = kt * 16 + 4 * j + i;
-                        const bool keep = ((valid_cur >> kl) & 1u) && (k0 + kl <= qpos[c]);
-                        sc[kt * 4 + i] = keep ? sc[kt * 4 + i] : -INFINITY;
-                    }
+                    for (int i = 0; i < 4; ++i)
+                        sc[kt * 4 + i] = present && kt * 16 + 4 * j + i <= lim ? sc[kt * 4 + i] : -INFINITY;
+                }
             }
             float mb = sc[0];
 #pragma unroll
@@ -540,9 +552,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
 
         if (st + 1 < nsteps) store_step(cur ^ 1, kr, vr);
         __syncthreads();
-        valid_cur = valid_next;
-#pragma unroll
-        for (int hb = 0; hb < KS / 16; ++hb) blk1[hb] = blk2[hb];
+        nib_cur = nib_next;
     }
 
     // A V element beyond the fp16 range (finite above 65504, or infinite)
