@@ -224,6 +224,11 @@ int skv_paged_decode_append_noalloc(const void* q, int q_dtype,
  * arrays; num_tokens (= seq_offsets[num_seqs]) sizes the grid on the host.
  * num_seqs <= 4096.  Blocks outside the pool and positions past the table are
  * skipped as in skv_paged_decode; a row with no visible key gives zeros.
+ * Numerics (block_size 16, head_dim 64 or 128): scores in bf16 x bf16 (an fp32
+ * query split into hi + lo parts) and P.V in fp16 x fp16 on the matrix cores,
+ * fp32 accumulation; V converts to fp16 exactly in [2^-14, 65504], and a
+ * workgroup whose keys hold a V element beyond 65504 recomputes its rows in
+ * fp32.  Other shapes run in fp32 throughout.
  * Replaces: the CPU-only multi-token path of PagedAttention::forward
  * (src/layers/attention.cpp:197-337), which the reference has no GPU kernel
  * for. */
