@@ -18,6 +18,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <memory>
 #include <optional>
 
 #include "stratakv/layers/attention.h"
@@ -65,7 +66,8 @@ public:
     // 348-351); its CPU forward computes these rows (:300-332).  Chunks of
     // fewer than kPrefillMmRows tokens give every projection row the bits
     // forward_into gives for that token; longer ones (bf16 weights) run the
-    // projections on the matrix cores, equal to fp32 rounding.  The attention
+    // projections on the matrix cores (from kPrefillGemmRows tokens as
+    // hipBLASLt GEMMs), equal to fp32 rounding.  The attention
     // of the chunk runs the prefill kernel instead of the decode kernel.
     void prefill_into(const Tensor& hidden_states, Tensor& output, int seq_id,
                       memory::PageTable& page_table, memory::BlockPool& block_pool);
@@ -79,6 +81,18 @@ public:
     int prefill_chunk_rows() const noexcept;
     // Chunk length from which the projections run on the matrix cores.
     static constexpr int kPrefillMmRows = 32;
+    // Chunk length from which the projections run as hipBLASLt GEMMs
+    // (skv_*_gemm_f32), equal to the matrix-core kernels to fp32 rounding.
+    static constexpr int kPrefillGemmRows = 256;
+    // The GEMMs' workspace (skv_prompt_gemm_workspace_bytes for the chunk).
+    // Blocks may share one when they run one after another on one stream (a
+    // Generator's layers); a block with none allocates its own on first use.
+    struct PrefillGemmWorkspace {
+        std::optional<Tensor> buffer;
+    };
+    void share_prefill_gemm_workspace(std::shared_ptr<PrefillGemmWorkspace> ws) noexcept {
+        pf_gemm_ = std::move(ws);
+    }
     void forward_into(const Tensor& hidden_states, Tensor& output, int seq_id,
                       memory::PageTable& page_table, memory::BlockPool& block_pool,
                       bool append_tokens = true);
@@ -156,6 +170,9 @@ private:
     std::optional<Tensor> pf_queries_, pf_keys_, pf_values_, pf_context_, pf_residual_, pf_act_;
     std::optional<Tensor> pf_normalized_, pf_up_, pf_down_;
     std::optional<Tensor> pf_meta_;  // 4 int32: position, chunk offsets {0, n}, context length
+    std::shared_ptr<PrefillGemmWorkspace> pf_gemm_;
+    // The shared workspace grown to at least `bytes`; its 256-byte aligned start.
+    void* prefill_gemm_workspace(std::size_t bytes);
 };
 
 }  // namespace models

@@ -134,6 +134,14 @@ _PROTOS = {
                                                _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
     "skv_linear_residual_mm_f32": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp,
                                           _vp, _vp]),
+    "skv_prompt_gemm_workspace_bytes": (_sz, [_i32, _i32, _i32]),
+    "skv_fused_qkv_gemm_f32": (_i32, [_vp, _i32, _vp, _f32, _vp, _vp, _vp, _i32, _i64,
+                                      _c.POINTER(_c.c_int64), _vp, _vp, _vp, _i32, _i32, _i32, _i32,
+                                      _i32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "skv_fused_gate_up_swiglu_gemm_f32": (_i32, [_vp, _i32, _vp, _f32, _vp, _vp, _i32, _i64, _i64,
+                                                 _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "skv_linear_residual_gemm_f32": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp,
+                                            _vp, _vp, _sz, _vp]),
     "skv_rope_rows_f32": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
     "skv_write_i32": (_i32, [_vp, _c.POINTER(_c.c_int32), _i32, _vp]),
     "skv_convert_to_bf16": (_i32, [_vp, _i32, _sz, _vp, _vp, _vp]),

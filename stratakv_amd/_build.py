@@ -88,7 +88,8 @@ def build_library() -> str:
         cmds.append([HIPCC, *HIP_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj])
         objs.append(obj)
     _run_all(cmds)
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", *objs, "-o", LIB + ".tmp"])
+    # hipBLASLt: the GEMMs of the prompt-pass projections (skv_prompt_gemm.hip).
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", *objs, "-lhipblaslt", "-o", LIB + ".tmp"])
     os.replace(LIB + ".tmp", LIB)
     return LIB
 

@@ -18,6 +18,7 @@
 #include <cstring>
 #include <initializer_list>
 #include <limits>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <random>
@@ -189,6 +190,9 @@ Generator::Generator(GeneratorConfig config, io::WeightMap weights)
     (void)kv_dim;
 
     for (auto& b : blocks_) b.to(Device::GPU);
+    // The layers run one after another on one stream: one prompt-GEMM workspace serves them all.
+    const auto gemm_ws = std::make_shared<models::TransformerBlock::PrefillGemmWorkspace>();
+    for (auto& b : blocks_) b.share_prefill_gemm_workspace(gemm_ws);
     // STRATAKV_PARITY=1 (src/generation/generator.cpp:33-36): the reference
     // compares every layer with its CPU copy; this build has no CPU layers and
     // runs each block's attention check instead.

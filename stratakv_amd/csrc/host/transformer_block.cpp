@@ -450,6 +450,15 @@ void TransformerBlock::ensure_prefill_workspace(int rows) {
     prefill_rows_ = rows;
 }
 
+void* TransformerBlock::prefill_gemm_workspace(std::size_t bytes) {
+    if (!pf_gemm_) pf_gemm_ = std::make_shared<PrefillGemmWorkspace>();
+    std::optional<Tensor>& b = pf_gemm_->buffer;
+    if (!b || b->num_elements() * sizeof(float) < bytes)
+        b.emplace(std::vector<std::size_t>{(bytes + sizeof(float) - 1) / sizeof(float)}, DataType::FP32,
+                  Device::GPU);
+    return b->raw_data();
+}
+
 void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output, int seq_id,
                                     memory::PageTable& page_table, memory::BlockPool& block_pool) {
     if (hidden_states.ndim() != 2 || hidden_states.shape()[1] != hidden_dim_ || hidden_states.shape()[0] == 0 ||
@@ -543,15 +552,36 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
         // (or when it does not take the shape) the rows kernels, else the
         // separate kernels.
         const bool mm = n >= kPrefillMmRows;
-
+        // From kPrefillGemmRows tokens every projection runs as library GEMMs
+        // (one workspace sized for the widest): the 2,048-token prompt of the
+        // TinyLlama shape took 14.8 ms so against 15.2 ms with q/k/v and
+        // o_proj on the matrix-core kernels and 17.2 ms with all four there.
+        const bool lib = n >= kPrefillGemmRows;
+        std::size_t gemm_bytes = 0;
+        void* gemm_ws = nullptr;
+        if (lib) {
+            const int kv_dim = num_kv_heads * head_dim;
+            for (const auto& [in, outs] : {std::pair<int, int>{hidden, q_dim + 2 * kv_dim}, {hidden, 2 * inter},
+                                           {q_dim, hidden}, {inter, hidden}})
+                gemm_bytes = std::max(gemm_bytes, skv_prompt_gemm_workspace_bytes(n, in, outs));
+            gemm_ws = prefill_gemm_workspace(gemm_bytes);
+        }
         // Input RMSNorm, q/k/v projections and RoPE at p0 + row.
         auto qkv = [&](auto entry, float* scratch) {
             return entry(x, n, cfp(norm1_.gamma()), norm1_.epsilon(), wq.weight().raw_data(), wk.weight().raw_data(),
                          wv.weight().raw_data(), wdtype(wq), stride_k(wq), qkv_strides, bias_of(wq), bias_of(wk),
                          bias_of(wv), hidden, num_heads, num_kv_heads, head_dim, p0, q, k, v, scratch, s);
         };
+        auto qkv_gemm_entry = [&](const float* xx, int rows, const float* g, float e, const void* a, const void* b,
+                                  const void* c, int dt, int64_t sk, const int64_t* sn, const float* ba,
+                                  const float* bb, const float* bc, int hd_, int nh, int nkv, int hdim, int pos,
+                                  float* qq, float* kk, float* vv, float* scratch, void* st) {
+            return skv_fused_qkv_gemm_f32(xx, rows, g, e, a, b, c, dt, sk, sn, ba, bb, bc, hd_, nh, nkv, hdim, pos, qq,
+                                          kk, vv, scratch, gemm_ws, gemm_bytes, st);
+        };
         if (!(same_dtype &&
-              ((mm && fused(qkv(skv_fused_qkv_mm_f32, fp(*pf_normalized_)), "prefill_into: q/k/v on the matrix cores")) ||
+              ((lib && fused(qkv(qkv_gemm_entry, fp(*pf_normalized_)), "prefill_into: q/k/v as library GEMMs")) ||
+               (mm && fused(qkv(skv_fused_qkv_mm_f32, fp(*pf_normalized_)), "prefill_into: q/k/v on the matrix cores")) ||
                fused(qkv(skv_fused_qkv_rows_f32, fp(*pf_normalized_)), "prefill_into: fused rmsnorm + q/k/v + rope")))) {
             float* xn = fp(*pf_normalized_);
             detail::check(skv_rmsnorm_f32(x, xn, cfp(norm1_.gamma()), n, hidden, norm1_.epsilon(), s),
@@ -577,7 +607,11 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                       "prefill_into: paged prefill attention");
 
         // o_proj + residual (reads x before y is written: aliasing-safe).
-        if (!((mm && fused(skv_linear_residual_mm_f32(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
+        if (!((lib && fused(skv_linear_residual_gemm_f32(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
+                                                         stride_n(wo), q_dim, hidden, bias_of(wo), x, h, gemm_ws,
+                                                         gemm_bytes, s),
+                            "prefill_into: o_proj as a library GEMM")) ||
+              (mm && fused(skv_linear_residual_mm_f32(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
                                                       stride_n(wo), q_dim, hidden, bias_of(wo), x, h, s),
                            "prefill_into: o_proj on the matrix cores")) ||
               fused(skv_linear_residual_rows_f32(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
@@ -592,8 +626,16 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                          up_proj_.weight().raw_data(), wdtype(gate_proj_), stride_k(gate_proj_), stride_n(gate_proj_),
                          stride_n(up_proj_), bias_of(gate_proj_), bias_of(up_proj_), hidden, inter, act, scratch, s);
         };
+        // The library-GEMM entry point in the shape of the others (workspace bound here).
+        auto gate_up_gemm_entry = [&](const float* xx, int rows, const float* g, float e, const void* a,
+                                      const void* b, int dt, int64_t sk, int64_t sa, int64_t sb, const float* ba,
+                                      const float* bb, int in, int out, float* y_, float* scratch, void* st) {
+            return skv_fused_gate_up_swiglu_gemm_f32(xx, rows, g, e, a, b, dt, sk, sa, sb, ba, bb, in, out, y_,
+                                                     scratch, gemm_ws, gemm_bytes, st);
+        };
         if (!(ffn_same &&
-              ((mm && fused(gate_up(skv_fused_gate_up_swiglu_mm_f32, fp(*pf_normalized_)),
+              ((lib && fused(gate_up(gate_up_gemm_entry, fp(*pf_normalized_)), "prefill_into: gate/up as library GEMMs")) ||
+               (mm && fused(gate_up(skv_fused_gate_up_swiglu_mm_f32, fp(*pf_normalized_)),
                             "prefill_into: gate/up on the matrix cores")) ||
                fused(gate_up(skv_fused_gate_up_swiglu_rows_f32, fp(*pf_normalized_)),
                      "prefill_into: fused rmsnorm + gate/up + swiglu")))) {
@@ -606,7 +648,11 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
             detail::check(skv_swiglu_f32(act, up, n * inter, s), "prefill_into: swiglu");
         }
         // down_proj + residual into the output rows.
-        if (!((mm && fused(skv_linear_residual_mm_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
+        if (!((lib && fused(skv_linear_residual_gemm_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
+                                                         stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
+                                                         bias_of(down_proj_), h, y, gemm_ws, gemm_bytes, s),
+                            "prefill_into: down_proj as a library GEMM")) ||
+              (mm && fused(skv_linear_residual_mm_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
                                                       stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
                                                       bias_of(down_proj_), h, y, s),
                            "prefill_into: down_proj on the matrix cores")) ||

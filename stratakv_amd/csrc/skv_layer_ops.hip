@@ -13,6 +13,7 @@
 //            frequency 10000^(-2i/hd) rounded to float, angle in double)
 //   swiglu   src/models/transformer_block.cpp:315-323 (overflow-safe sigmoid)
 #include "skv_common.h"
+#include "skv_prompt_gemm.h"
 
 #include <algorithm>
 #include <cmath>
@@ -1091,6 +1092,166 @@ int launch_mm(const FusedGemv& f, int groups, hipStream_t s) {
     };
     if (grid_of(kMmWaves) < 256 && f.K % 256 == 0) return go(proj_mm_kernel<MODE, 2>, 2);
     return go(proj_mm_kernel<MODE, 1>, 1);
+}
+
+// ---------------------------------------------------------------------------
+// Kernels around the library GEMMs of the prompt-pass projections
+// (skv_prompt_gemm.hip): the input split before them and the epilogues after.
+// ---------------------------------------------------------------------------
+typedef __bf16 pg_bf16x2_t __attribute__((ext_vector_type(2)));
+
+// hi = bf16(v) (round to nearest even) of two values and lo = bf16 of the
+// exact remainders v - hi, packed two to a word.
+__device__ __forceinline__ void split_pair(float v0, float v1, uint32_t& hi, uint32_t& lo) {
+    const pg_bf16x2_t h = {static_cast<__bf16>(v0), static_cast<__bf16>(v1)};
+    hi = __builtin_bit_cast(uint32_t, h);
+    const pg_bf16x2_t l = {static_cast<__bf16>(v0 - bf16_lo(hi)), static_cast<__bf16>(v1 - bf16_hi(hi))};
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+
+// One workgroup per row; each thread splits 4 consecutive values per pass.
+// With a RoPE table (rope.cs != nullptr) the workgroup also writes its token's
+// cos / sin per rotation pair (rope_cos_sin of position first + row), which
+// the q/k/v epilogue then reads for every head.
+struct SplitRope {
+    float* cs;        // [rows][head_dim / 2][cos, sin], or nullptr
+    int first, head_dim;
+};
+
+template <bool NORM>
+__global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ x, int rows, int K,
+                                                         const float* __restrict__ gamma, float eps,
+                                                         float* __restrict__ normalized,
+                                                         uint16_t* __restrict__ parts, SplitRope rope,
+                                                         RopeTable freq) {
+    extern __shared__ float xg_s[];  // NORM: [2][K], the row and gamma
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    if (rope.cs != nullptr && static_cast<int>(threadIdx.x) < rope.head_dim / 2) {
+        float c, sn;
+        rope_cos_sin(rope.first + row, freq.cs[threadIdx.x], c, sn);
+        *reinterpret_cast<float2*>(rope.cs + (static_cast<int64_t>(row) * (rope.head_dim / 2) + threadIdx.x) * 2) =
+            float2{c, sn};
+    }
+    const float* xr = x + static_cast<int64_t>(row) * K;
+    float inv = 1.0f;
+    if constexpr (NORM) {
+        stage_to_lds(xr, xg_s, K);
+        stage_to_lds(gamma, xg_s + K, K);
+        __syncthreads();
+        inv = rms_inverse([&](int i) { return xg_s[i]; }, K, eps, red);
+    }
+    uint16_t* hi_row = parts + static_cast<int64_t>(row) * K;
+    uint16_t* lo_row = parts + (static_cast<int64_t>(rows) + row) * K;
+    for (int i = 4 * threadIdx.x; i < K; i += 4 * 256) {
+        f32x4_t v;
+        if constexpr (NORM) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = xg_s[i + e] * inv * xg_s[K + i + e];   // rmsnorm_kernel's rounding
+            *reinterpret_cast<f32x4_t*>(normalized + static_cast<int64_t>(row) * K + i) = v;
+        } else {
+            v = *reinterpret_cast<const f32x4_t*>(xr + i);
+        }
+        uint2 h, l;
+        split_pair(v[0], v[1], h.x, l.x);
+        split_pair(v[2], v[3], h.y, l.y);
+        *reinterpret_cast<uint2*>(hi_row + i) = h;
+        *reinterpret_cast<uint2*>(lo_row + i) = l;
+    }
+}
+
+__device__ __forceinline__ f32x4_t ld4(const float* p) { return *reinterpret_cast<const f32x4_t*>(p); }
+__device__ __forceinline__ f32x4_t bias4_at(const float* b, int j) {
+    return b != nullptr ? ld4(b + j) : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+}
+// Output j..j+3 of token r from the two halves of d, plus bias.
+__device__ __forceinline__ f32x4_t gemm_out4(const float* d, const float* bias, int n, int rows, int r, int j) {
+    return (ld4(d + static_cast<int64_t>(r) * n + j) + ld4(d + (static_cast<int64_t>(rows) + r) * n + j)) +
+           bias4_at(bias, j);
+}
+
+// qkv: each thread takes 8 outputs of one token: 4 rotation pairs
+// (p .. p+3 with p + hd/2 .. p+3 + hd/2 of one head) of q or k, or 8
+// consecutive outputs of v (or of q and k without RoPE).
+__global__ __launch_bounds__(256) void qkv_epilogue_kernel(GemmEpilogue e) {
+    const int units = (e.n[0] + e.n[1] + e.n[2]) / 8;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(e.rows) * units) return;
+    const int r = static_cast<int>(i / units);
+    int u = static_cast<int>(i - static_cast<int64_t>(r) * units), m = 0;
+    while (m < 2 && u >= e.n[m] / 8) u -= e.n[m] / 8, ++m;
+    const bool rope = m < 2 && e.first >= 0;
+    const int half = e.head_dim / 2;
+    const int ja = rope ? (u / (half / 4)) * e.head_dim + (u % (half / 4)) * 4 : 8 * u;
+    const int jb = rope ? ja + half : ja + 4;
+    f32x4_t a = gemm_out4(e.d[m], e.bias[m], e.n[m], e.rows, r, ja);
+    f32x4_t b = gemm_out4(e.d[m], e.bias[m], e.n[m], e.rows, r, jb);
+    if (rope) {
+        const float* cs = e.rope_cs + (static_cast<int64_t>(r) * half + ja % e.head_dim) * 2;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float va = a[t], vb = b[t];
+            rotate_pair(va, vb, cs[2 * t], cs[2 * t + 1]);
+            a[t] = va;
+            b[t] = vb;
+        }
+    }
+    float* y = e.y[m] + static_cast<int64_t>(r) * e.n[m];
+    *reinterpret_cast<f32x4_t*>(y + ja) = a;
+    *reinterpret_cast<f32x4_t*>(y + jb) = b;
+}
+
+__global__ __launch_bounds__(256) void gate_up_epilogue_kernel(GemmEpilogue e) {
+    const int units = e.n[0] / 4;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(e.rows) * units) return;
+    const int r = static_cast<int>(i / units), j = 4 * static_cast<int>(i - static_cast<int64_t>(r) * units);
+    const f32x4_t g = gemm_out4(e.d[0], e.bias[0], e.n[0], e.rows, r, j);
+    const f32x4_t u = gemm_out4(e.d[1], e.bias[1], e.n[0], e.rows, r, j);
+    *reinterpret_cast<f32x4_t*>(e.y[0] + static_cast<int64_t>(r) * e.n[0] + j) =
+        f32x4_t{swiglu_of(g[0], u[0]), swiglu_of(g[1], u[1]), swiglu_of(g[2], u[2]), swiglu_of(g[3], u[3])};
+}
+
+__global__ __launch_bounds__(256) void residual_epilogue_kernel(GemmEpilogue e) {
+    const int units = e.n[0] / 4;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(e.rows) * units) return;
+    const int r = static_cast<int>(i / units), j = 4 * static_cast<int>(i - static_cast<int64_t>(r) * units);
+    const int64_t at = static_cast<int64_t>(r) * e.n[0] + j;
+    *reinterpret_cast<f32x4_t*>(e.y[0] + at) = gemm_out4(e.d[0], e.bias[0], e.n[0], e.rows, r, j) + ld4(e.residual + at);
+}
+
+int launch_split_rows(const float* x, int rows, int K, const float* gamma, float eps, float* normalized,
+                      uint16_t* parts, hipStream_t s, float* rope_cs, int first, int head_dim) {
+    const SplitRope rope{rope_cs, first, head_dim};
+    const RopeTable& inv = rope_cs != nullptr ? rope_inv_freq(head_dim) : RopeTable{};
+    if (gamma != nullptr)
+        split_rows_kernel<true><<<rows, 256, 2 * sizeof(float) * K, s>>>(x, rows, K, gamma, eps, normalized, parts,
+                                                                          rope, inv);
+    else
+        split_rows_kernel<false><<<rows, 256, 0, s>>>(x, rows, K, nullptr, eps, nullptr, parts, rope, inv);
+    return check_launch("split_rows_kernel");
+}
+
+namespace {
+unsigned epilogue_grid(int rows, int units) {
+    return static_cast<unsigned>(cdiv<int64_t>(static_cast<int64_t>(rows) * units, 256));
+}
+}  // namespace
+
+int launch_qkv_epilogue(const GemmEpilogue& e, hipStream_t s) {
+    qkv_epilogue_kernel<<<epilogue_grid(e.rows, (e.n[0] + e.n[1] + e.n[2]) / 8), 256, 0, s>>>(e);
+    return check_launch("qkv_epilogue_kernel");
+}
+
+int launch_gate_up_epilogue(const GemmEpilogue& e, hipStream_t s) {
+    gate_up_epilogue_kernel<<<epilogue_grid(e.rows, e.n[0] / 4), 256, 0, s>>>(e);
+    return check_launch("gate_up_epilogue_kernel");
+}
+
+int launch_residual_epilogue(const GemmEpilogue& e, hipStream_t s) {
+    residual_epilogue_kernel<<<epilogue_grid(e.rows, e.n[0] / 4), 256, 0, s>>>(e);
+    return check_launch("residual_epilogue_kernel");
 }
 
 }  // namespace skv

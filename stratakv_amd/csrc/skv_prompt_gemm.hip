@@ -1,0 +1,289 @@
+// skv_prompt_gemm.hip -- the projections of long prompt chunks with their
+// products on hipBLASLt: bf16 weights x bf16 parts of the fp32 inputs, fp32
+// accumulation.  The library GEMMs run the multiply-adds; the kernels around
+// them (skv_layer_ops.hip) split the inputs and apply the layer's epilogue.
+//
+// Why hi and lo parts: the activations are fp32 and the weights bf16 (the
+// reference multiplies fp32 activations by bf16 weights in fp32,
+// src/cuda/gemm_cuda.cu:445-560).  Each input v becomes hi = bf16(v) and
+// lo = bf16(v - hi); W hi + W lo keeps ~16 significant bits of v and every
+// product is exact, so the result is the fp32 projection up to fp32 rounding.
+// The two parts are stacked as 2 * rows GEMM columns, so each weight matrix
+// is one GEMM of twice the tokens instead of two.
+//
+// Layout, column-major as hipBLASLt sees it: a weight matrix of N
+// output-major rows with row stride ld is the K x N matrix W^T (op T, lda =
+// ld); the parts are K x 2 rows (op N, ldb = K); the output is N x 2 rows
+// (ldc = N), i.e. [2 * rows][N] row-major with token r's hi products in row r
+// and its lo products in row rows + r.
+#include "skv_common.h"
+#include "skv_prompt_gemm.h"
+
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+namespace skv {
+namespace {
+
+constexpr size_t kLibWorkspace = size_t{32} << 20;   // hipBLASLt's own scratch, the algorithm search's limit
+
+size_t align256(size_t b) { return (b + 255) & ~size_t{255}; }
+
+// One GEMM shape's descriptors and the algorithm hipBLASLt ranks first for it.
+struct Plan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+    size_t workspace = 0;
+    bool ok = false;
+};
+
+// Per device: the library handle (created on first use, kept for the process)
+// and the plans of the shapes seen.  Plans are never erased, so a pointer to
+// one stays valid after the lock is released.
+struct DeviceState {
+    hipblasLtHandle_t handle = nullptr;
+    bool failed = false;
+    std::map<std::tuple<int, int, int, int64_t>, Plan> plans;
+};
+
+std::mutex g_mutex;
+std::map<int, DeviceState> g_devices;
+
+// The plan of an m x n x k GEMM with lda, or nullptr when hipBLASLt has none
+// (or cannot start on this device).
+const Plan* plan_for(int m, int n, int k, int64_t lda) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    DeviceState& ds = g_devices[dev];
+    if (ds.handle == nullptr && !ds.failed && hipblasLtCreate(&ds.handle) != HIPBLAS_STATUS_SUCCESS) {
+        ds.handle = nullptr;
+        ds.failed = true;
+    }
+    if (ds.failed) return nullptr;
+    const auto key = std::make_tuple(m, n, k, lda);
+    auto it = ds.plans.find(key);
+    if (it != ds.plans.end()) return it->second.ok ? &it->second : nullptr;
+    Plan& p = ds.plans[key];
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) ==
+                  HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) ==
+                  HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, k, m, lda) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, k, n, k) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p.c, HIP_R_32F, m, n, m) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                    &kLibWorkspace, sizeof(kLibWorkspace)) == HIPBLAS_STATUS_SUCCESS;
+    if (ok) {
+        hipblasLtMatmulHeuristicResult_t best{};
+        int found = 0;
+        ok = hipblasLtMatmulAlgoGetHeuristic(ds.handle, p.desc, p.a, p.b, p.c, p.c, pref, 1, &best, &found) ==
+                 HIPBLAS_STATUS_SUCCESS &&
+             found > 0 && best.workspaceSize <= kLibWorkspace;
+        if (ok) {
+            p.algo = best.algo;
+            p.workspace = best.workspaceSize;
+        }
+    }
+    if (pref != nullptr) hipblasLtMatmulPreferenceDestroy(pref);
+    p.ok = ok;
+    return ok ? &p : nullptr;
+}
+
+// The plans of every weight matrix of one call, looked up before anything is
+// launched: a shape hipBLASLt does not take leaves the call unlaunched.
+struct Gemm {
+    const void* w;
+    int64_t ld;
+    int n;
+    float* d;
+    const Plan* plan;
+};
+
+// Workspace: [2 rows][K] bf16 parts, then [2 rows][outputs] fp32 GEMM
+// outputs, the RoPE table of q/k/v, then the library's scratch.
+struct Workspace {
+    uint16_t* parts;
+    float* out;
+    float* rope_cs;
+    void* lib;
+};
+
+Workspace carve(void* ws, int rows, int K, int outputs) {
+    char* p = static_cast<char*>(ws);
+    const size_t parts = align256(size_t{4} * rows * K), out = align256(size_t{8} * rows * outputs);
+    const size_t rope = align256(size_t{4} * rows * (outputs / 3));
+    return Workspace{reinterpret_cast<uint16_t*>(p), reinterpret_cast<float*>(p + parts),
+                     reinterpret_cast<float*>(p + parts + out), p + parts + out + rope};
+}
+
+int check_workspace(const char* fn, void* ws, size_t bytes, int rows, int K, int outputs) {
+    SKV_REQUIRE(ws != nullptr && (reinterpret_cast<std::uintptr_t>(ws) & 255u) == 0,
+                "%s: workspace must be 256-byte aligned", fn);
+    const size_t need = skv_prompt_gemm_workspace_bytes(rows, K, outputs);
+    SKV_REQUIRE(bytes >= need, "%s: workspace of %zu bytes, %zu needed", fn, bytes, need);
+    return SKV_OK;
+}
+
+// The common layout rules; SKV_ERR_UNSUPPORTED when a shape is not taken.
+bool layout_ok(const void* w, int weight_dtype, int64_t stride_k, int64_t stride_n, int K, int n) {
+    return w != nullptr && weight_dtype == SKV_DTYPE_BF16 && stride_k == 1 && stride_n >= K &&
+           (stride_n * 2) % 16 == 0 && aligned16(w) && n % 8 == 0;
+}
+
+// Plans every GEMM of the call (nothing launched yet).
+bool plan_all(Gemm* g, int count, int rows, int K) {
+    for (int i = 0; i < count; ++i)
+        if ((g[i].plan = plan_for(g[i].n, 2 * rows, K, g[i].ld)) == nullptr) return false;
+    return true;
+}
+
+int run_gemms(const char* fn, const Gemm* g, int count, const uint16_t* parts, void* lib, hipStream_t s) {
+    const float alpha = 1.0f, beta = 0.0f;
+    int dev = 0;
+    SKV_HIP_TRY(hipGetDevice(&dev));
+    hipblasLtHandle_t handle;
+    {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        handle = g_devices[dev].handle;
+    }
+    for (int i = 0; i < count; ++i) {
+        const Plan& p = *g[i].plan;
+        const hipblasStatus_t st = hipblasLtMatmul(handle, p.desc, &alpha, g[i].w, p.a, parts, p.b, &beta, g[i].d,
+                                                   p.c, g[i].d, p.c, &p.algo, lib, kLibWorkspace, s);
+        if (st != HIPBLAS_STATUS_SUCCESS) return set_error(SKV_ERR_HIP, "%s: hipblasLtMatmul failed (%d)", fn, st);
+    }
+    return check_launch("hipblasLtMatmul");
+}
+
+}  // namespace
+}  // namespace skv
+
+using namespace skv;
+
+extern "C" size_t skv_prompt_gemm_workspace_bytes(int rows, int in_dim, int outputs) {
+    if (rows <= 0 || in_dim <= 0 || outputs <= 0) return 0;
+    // + the RoPE table of q/k/v, [rows][head_dim / 2][cos, sin] with head_dim <= outputs / 3.
+    return align256(size_t{4} * rows * in_dim) + align256(size_t{8} * rows * outputs) +
+           align256(size_t{4} * rows * (outputs / 3)) + kLibWorkspace;
+}
+
+extern "C" int skv_fused_qkv_gemm_f32(const float* hidden, int rows, const float* gamma, float epsilon,
+                                      const void* wq, const void* wk, const void* wv, int weight_dtype,
+                                      int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
+                                      const float* bias_k, const float* bias_v, int hidden_dim, int num_heads,
+                                      int num_kv_heads, int head_dim, int first_position, float* q, float* k,
+                                      float* v, float* normalized, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+    const char* fn = "skv_fused_qkv_gemm_f32";
+    SKV_REQUIRE(hidden && stride_n && q && k && v && rows > 0 && hidden_dim > 0 && num_heads > 0 &&
+                    num_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
+                "%s: invalid pointers or sizes", fn);
+    SKV_REQUIRE(gamma == nullptr || normalized != nullptr, "%s: normalized scratch required with gamma", fn);
+    SKV_REQUIRE(head_dim <= 512, "%s: head_dim %d exceeds 512", fn, head_dim);
+    const int n[3] = {num_heads * head_dim, num_kv_heads * head_dim, num_kv_heads * head_dim};
+    const int K = hidden_dim;
+    if (int rc = check_workspace(fn, workspace, workspace_bytes, rows, K, n[0] + n[1] + n[2])) return rc;
+    const bool rope = first_position >= 0;
+    const void* w[3] = {wq, wk, wv};
+    bool ok = K % 8 == 0 && K <= 8192 && (!rope || head_dim % 8 == 0) && aligned16(hidden) && aligned16(q) &&
+              aligned16(k) && aligned16(v) && (gamma == nullptr || aligned16(normalized));
+    for (int m = 0; m < 3 && ok; ++m) ok = layout_ok(w[m], weight_dtype, stride_k, stride_n[m], K, n[m]);
+    if (!ok) return set_error(SKV_ERR_UNSUPPORTED, "%s: layout not taken by the library GEMMs", fn);
+    Workspace ws = carve(workspace, rows, K, n[0] + n[1] + n[2]);
+    float* y[3] = {q, k, v};
+    Gemm g[3];
+    float* d = ws.out;
+    for (int m = 0; m < 3; ++m) {
+        g[m] = Gemm{w[m], stride_n[m], n[m], d, nullptr};
+        d += size_t{2} * rows * n[m];
+    }
+    if (!plan_all(g, 3, rows, K)) return set_error(SKV_ERR_UNSUPPORTED, "%s: no hipBLASLt algorithm", fn);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (int rc = launch_split_rows(hidden, rows, K, gamma, epsilon, normalized, ws.parts, s,
+                                   rope ? ws.rope_cs : nullptr, first_position, head_dim))
+        return rc;
+    if (int rc = run_gemms(fn, g, 3, ws.parts, ws.lib, s)) return rc;
+    GemmEpilogue e{};
+    const float* bias[3] = {bias_q, bias_k, bias_v};
+    for (int m = 0; m < 3; ++m) {
+        e.d[m] = g[m].d;
+        e.bias[m] = bias[m];
+        e.y[m] = y[m];
+        e.n[m] = n[m];
+    }
+    e.rope_cs = ws.rope_cs;
+    e.rows = rows;
+    e.head_dim = head_dim;
+    e.first = first_position;
+    return launch_qkv_epilogue(e, s);
+}
+
+extern "C" int skv_fused_gate_up_swiglu_gemm_f32(const float* x, int rows, const float* gamma, float epsilon,
+                                                 const void* w_gate, const void* w_up, int weight_dtype,
+                                                 int64_t stride_k, int64_t stride_n_gate, int64_t stride_n_up,
+                                                 const float* bias_gate, const float* bias_up, int in_dim,
+                                                 int out_dim, float* act, float* normalized, void* workspace,
+                                                 size_t workspace_bytes, void* stream) {
+    const char* fn = "skv_fused_gate_up_swiglu_gemm_f32";
+    SKV_REQUIRE(x && act && rows > 0 && in_dim > 0 && out_dim > 0, "%s: invalid pointers or sizes", fn);
+    SKV_REQUIRE(gamma == nullptr || normalized != nullptr, "%s: normalized scratch required with gamma", fn);
+    const int K = in_dim;
+    if (int rc = check_workspace(fn, workspace, workspace_bytes, rows, K, 2 * out_dim)) return rc;
+    const bool ok = K % 8 == 0 && K <= 8192 && aligned16(x) && aligned16(act) &&
+                    (gamma == nullptr || aligned16(normalized)) &&
+                    layout_ok(w_gate, weight_dtype, stride_k, stride_n_gate, K, out_dim) &&
+                    layout_ok(w_up, weight_dtype, stride_k, stride_n_up, K, out_dim);
+    if (!ok) return set_error(SKV_ERR_UNSUPPORTED, "%s: layout not taken by the library GEMMs", fn);
+    Workspace ws = carve(workspace, rows, K, 2 * out_dim);
+    Gemm g[2] = {{w_gate, stride_n_gate, out_dim, ws.out, nullptr},
+                 {w_up, stride_n_up, out_dim, ws.out + size_t{2} * rows * out_dim, nullptr}};
+    if (!plan_all(g, 2, rows, K)) return set_error(SKV_ERR_UNSUPPORTED, "%s: no hipBLASLt algorithm", fn);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (int rc = launch_split_rows(x, rows, K, gamma, epsilon, normalized, ws.parts, s)) return rc;
+    if (int rc = run_gemms(fn, g, 2, ws.parts, ws.lib, s)) return rc;
+    GemmEpilogue e{};
+    e.d[0] = g[0].d;
+    e.d[1] = g[1].d;
+    e.bias[0] = bias_gate;
+    e.bias[1] = bias_up;
+    e.y[0] = act;
+    e.n[0] = e.n[1] = out_dim;
+    e.rows = rows;
+    return launch_gate_up_epilogue(e, s);
+}
+
+extern "C" int skv_linear_residual_gemm_f32(const float* x, int rows, const void* weight, int weight_dtype,
+                                            int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
+                                            const float* bias, const float* residual, float* y, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+    const char* fn = "skv_linear_residual_gemm_f32";
+    SKV_REQUIRE(x && residual && y && rows > 0 && in_dim > 0 && out_dim > 0, "%s: invalid pointers or sizes", fn);
+    const int K = in_dim;
+    if (int rc = check_workspace(fn, workspace, workspace_bytes, rows, K, out_dim)) return rc;
+    const bool ok = K % 8 == 0 && K <= 8192 && aligned16(x) && aligned16(residual) && aligned16(y) &&
+                    layout_ok(weight, weight_dtype, stride_k, stride_n, K, out_dim);
+    if (!ok) return set_error(SKV_ERR_UNSUPPORTED, "%s: layout not taken by the library GEMMs", fn);
+    Workspace ws = carve(workspace, rows, K, out_dim);
+    Gemm g[1] = {{weight, stride_n, out_dim, ws.out, nullptr}};
+    if (!plan_all(g, 1, rows, K)) return set_error(SKV_ERR_UNSUPPORTED, "%s: no hipBLASLt algorithm", fn);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (int rc = launch_split_rows(x, rows, K, nullptr, 0.0f, nullptr, ws.parts, s)) return rc;
+    if (int rc = run_gemms(fn, g, 1, ws.parts, ws.lib, s)) return rc;
+    GemmEpilogue e{};
+    e.d[0] = g[0].d;
+    e.bias[0] = bias;
+    e.y[0] = y;
+    e.n[0] = out_dim;
+    e.residual = residual;
+    e.rows = rows;
+    return launch_residual_epilogue(e, s);
+}

@@ -156,3 +156,42 @@ def test_matrix_core_projections_and_prompt_embedding_reject_invalid_arguments()
     assert emb(FAKE, 0, 65536) == skv.SKV_ERR_INVALID_ARGUMENT                      # more than one launch takes
     assert emb(FAKE, -1, 4) == skv.SKV_ERR_INVALID_ARGUMENT
     assert emb(None, 0, 4) == skv.SKV_ERR_INVALID_ARGUMENT
+
+
+def test_library_gemm_projections_reject_invalid_arguments():
+    """The *_gemm_f32 projections validate before any device work:
+    INVALID_ARGUMENT for bad sizes, a missing scratch or a workspace that is
+    misaligned or smaller than skv_prompt_gemm_workspace_bytes; UNSUPPORTED
+    (nothing launched, hipBLASLt not asked) for fp32 weights, in_dim not a
+    multiple of 8, an output count not a multiple of 8, a rotated head_dim not
+    a multiple of 8."""
+    lib = skv.lib()
+    eps = ctypes.c_float(1e-5)
+    wsb = lib.skv_prompt_gemm_workspace_bytes
+    # [2 rows][K] bf16 parts, [2 rows][outputs] fp32 and a RoPE table of 4 rows (outputs / 3) bytes, each
+    # rounded up to 256 bytes, + 32 MiB
+    assert wsb(1024, 2048, 2560) == 4 * 1024 * 2048 + 8 * 1024 * 2560 + 4 * 1024 * 853 + (32 << 20)
+    assert wsb(3, 8, 8) == 256 + 256 + 256 + (32 << 20)
+    assert wsb(0, 2048, 2048) == 0
+    B = skv.DTYPE_BF16
+    strides = (ctypes.c_int64 * 3)(2048, 2048, 2048)
+    big = wsb(64, 8192, 16384)
+    qkv = lambda rows, gamma, dt, K, hd, position, normalized, ws=FAKE, nbytes=big: lib.skv_fused_qkv_gemm_f32(
+        FAKE, rows, gamma, eps, FAKE, FAKE, FAKE, dt, 1, strides, None, None, None, K, 32, 4, hd, position,
+        FAKE, FAKE, FAKE, normalized, ws, nbytes, None)
+    assert qkv(0, FAKE, B, 2048, 64, 0, FAKE) == skv.SKV_ERR_INVALID_ARGUMENT       # no rows
+    assert qkv(4, FAKE, B, 2048, 64, 0, None) == skv.SKV_ERR_INVALID_ARGUMENT       # gamma without scratch
+    assert qkv(4, FAKE, B, 2048, 64, 0, FAKE, ws=FAKE + 16) == skv.SKV_ERR_INVALID_ARGUMENT   # misaligned
+    assert qkv(4, FAKE, B, 2048, 64, 0, FAKE, nbytes=wsb(4, 2048, 2560) - 1) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert qkv(4, FAKE, skv.DTYPE_FP32, 2048, 64, 0, FAKE) == skv.SKV_ERR_UNSUPPORTED
+    assert qkv(4, FAKE, B, 2044, 64, 0, FAKE) == skv.SKV_ERR_UNSUPPORTED            # K not a multiple of 8
+    assert qkv(4, FAKE, B, 2048, 12, 0, FAKE) == skv.SKV_ERR_UNSUPPORTED            # rotated head_dim 12
+    gate_up = lambda rows, K, out: lib.skv_fused_gate_up_swiglu_gemm_f32(
+        FAKE, rows, FAKE, eps, FAKE, FAKE, B, 1, K, K, None, None, K, out, FAKE, FAKE, FAKE, big, None)
+    assert gate_up(0, 2048, 5632) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert gate_up(3, 2048, 5636) == skv.SKV_ERR_UNSUPPORTED                        # out_dim not a multiple of 8
+    res = lambda rows, K, out, nbytes=big: lib.skv_linear_residual_gemm_f32(
+        FAKE, rows, FAKE, B, 1, K, K, out, None, FAKE, FAKE, FAKE, nbytes, None)
+    assert res(-1, 2048, 2048) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert res(2, 2048, 2048, nbytes=0) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert res(2, 2048, 2052) == skv.SKV_ERR_UNSUPPORTED                            # out_dim not a multiple of 8

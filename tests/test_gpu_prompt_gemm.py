@@ -1,0 +1,144 @@
+"""The library-GEMM projections of long prompt chunks (skv_*_gemm_f32:
+hipBLASLt bf16 GEMMs over the hi and lo parts of the fp32 inputs, with the
+split and the epilogues as kernels of this library) against the float64
+restatement of rmsnorm + projection + bias + RoPE / SwiGLU / residual, and
+against the matrix-core kernels (skv_*_mm_f32) they replace on the prompt
+path."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from test_gpu_layer_ops import _bf16_rows, _mm_reference
+
+pytestmark = pytest.mark.gpu
+
+
+def _padded(W, pad):
+    """W's rows in a buffer with a row stride of in_dim + pad elements."""
+    if pad == 0:
+        return W, W.shape[1]
+    out = np.zeros((W.shape[0], W.shape[1] + pad), W.dtype)
+    out[:, :W.shape[1]] = W
+    return out, W.shape[1] + pad
+
+
+def _run_all(gpu, entry, dW, ld, bp, dims, n, position, dx, dg, dctx, dact, dres, out, normalized, ws, wsb):
+    """The four projections of a layer through the gemm (entry = "gemm") or mm
+    (entry = "mm") entry points."""
+    lib = gpu.lib()
+    H, Hq, Hkv, hd, inter = dims
+    eps = ctypes.c_float(1e-5)
+    strides = (ctypes.c_int64 * 3)(ld["q"], ld["k"], ld["v"])
+    extra = (ws.ptr, wsb) if entry == "gemm" else ()
+    fn = lambda name: getattr(lib, f"skv_{name}_{entry}_f32")
+    gpu._check(fn("fused_qkv")(dx.ptr, n, dg.ptr, eps, dW["q"].ptr, dW["k"].ptr, dW["v"].ptr, gpu.DTYPE_BF16, 1,
+                               strides, bp("q"), bp("k"), bp("v"), H, Hq, Hkv, hd, position, out["q"].ptr,
+                               out["k"].ptr, out["v"].ptr, normalized.ptr, *extra, None))
+    gpu._check(fn("fused_gate_up_swiglu")(dx.ptr, n, dg.ptr, eps, dW["g"].ptr, dW["u"].ptr, gpu.DTYPE_BF16, 1,
+                                          ld["g"], ld["u"], bp("g"), bp("u"), H, inter, out["act"].ptr,
+                                          normalized.ptr, *extra, None))
+    gpu._check(fn("linear_residual")(dctx.ptr, n, dW["o"].ptr, gpu.DTYPE_BF16, 1, ld["o"], Hq * hd, H, bp("o"),
+                                     dres.ptr, out["o"].ptr, *extra, None))
+    gpu._check(fn("linear_residual")(dact.ptr, n, dW["d"].ptr, gpu.DTYPE_BF16, 1, ld["d"], inter, H, bp("d"),
+                                     dres.ptr, out["d"].ptr, *extra, None))
+
+
+@pytest.mark.parametrize("dims", [(2048, 32, 4, 64, 5632), (1024, 8, 2, 128, 1536)], ids=["tinyllama", "hd128"])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_gemm_projections_match_float64_and_mm(gpu, dims, with_bias):
+    """Every output within 1e-4 of its matrix's rms of the float64 result (a
+    dropped lo part errs by ~2e-3 relative, a wrong RoPE pair, token or half
+    by O(1)), each within 5e-5 (|ref| + rms) of the matrix-core kernels'
+    (fp32 sums in another order), and the normalised rows bit-identical to
+    theirs.  Tokens 1 .. 1,024 (the 1,024-token chunk of
+    the prompt path), RoPE positions up to 16,381 and none, and weight rows
+    with a padded stride for o_proj and gate."""
+    H, Hq, Hkv, hd, inter = dims
+    rng = np.random.default_rng(7 * H + inter + with_bias)
+    lib, D = gpu.lib(), gpu.DeviceBuffer
+    shapes = (("q", Hq * hd, H), ("k", Hkv * hd, H), ("v", Hkv * hd, H), ("o", H, Hq * hd),
+              ("g", inter, H), ("u", inter, H), ("d", H, inter))
+    W = {n: _bf16_rows(rng, o, i, 0.03) for n, o, i in shapes}
+    dW, ld = {}, {}
+    for name, _, _ in shapes:
+        buf, ld[name] = _padded(W[name], 64 if name in "og" else 0)
+        dW[name] = D.from_numpy(buf)
+    B = {n: (rng.standard_normal(o).astype(np.float32) if with_bias else None) for n, o, _ in shapes}
+    dB = {n: (D.from_numpy(B[n]) if B[n] is not None else None) for n, _, _ in shapes}
+    bp = lambda n: dB[n].ptr if dB[n] is not None else None
+    max_rows = 1024
+    wsb = max(lib.skv_prompt_gemm_workspace_bytes(max_rows, K, outs)
+              for K, outs in ((H, (Hq + 2 * Hkv) * hd), (H, 2 * inter), (Hq * hd, H), (inter, H)))
+    ws = D(wsb)
+    sizes = {"q": Hq * hd, "k": Hkv * hd, "v": Hkv * hd, "act": inter, "o": H, "d": H}
+    for n, position in ((1, 0), (16, 7), (37, 1000), (64, -1), (300, 16381), (max_rows, 5)):
+        x = rng.standard_normal((n, H)).astype(np.float32)
+        gamma = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+        ctx = rng.standard_normal((n, Hq * hd)).astype(np.float32)
+        act_in = rng.standard_normal((n, inter)).astype(np.float32)
+        res = rng.standard_normal((n, H)).astype(np.float32)
+        dx, dg, dctx, dact, dres = (D.from_numpy(a) for a in (x, gamma, ctx, act_in, res))
+        got = {}
+        for entry in ("gemm", "mm"):
+            out = {k: D(4 * n * m) for k, m in sizes.items()}
+            for buf in out.values():
+                buf.upload(np.full(buf.nbytes // 4, np.nan, np.float32))
+            normalized = D.from_numpy(np.full((n, H), np.nan, np.float32))
+            _run_all(gpu, entry, dW, ld, bp, dims, n, position, dx, dg, dctx, dact, dres, out, normalized, ws, wsb)
+            gpu.synchronize()
+            got[entry] = {k: out[k].download(np.float32, (n, m)) for k, m in sizes.items()}
+            got[entry]["xn"] = normalized.download(np.float32, (n, H))
+        assert np.array_equal(got["gemm"]["xn"].view(np.uint32), got["mm"]["xn"].view(np.uint32)), n
+        ref = _mm_reference(W, B, x, gamma, ctx, act_in, res, dims, position)
+        for k in sizes:
+            g = got["gemm"][k].astype(np.float64)
+            rms = np.sqrt((ref[k] ** 2).mean())
+            err = np.abs(g - ref[k]).max()
+            assert np.isfinite(g).all() and err <= 1e-4 * rms, f"{k}: rows={n} position={position} err={err:.3g}"
+            dmm = (np.abs(g - got["mm"][k]) / (np.abs(ref[k]) + rms)).max()
+            assert dmm <= 5e-5, f"{k}: rows={n} position={position} gemm-mm={dmm:.3g} of |ref| + rms"
+
+
+def test_gemm_residual_in_place_and_repeated_calls(gpu):
+    """y aliasing the residual, and one workspace reused by calls of other
+    sizes one after another (the second smaller): each result as the float64
+    restatement."""
+    lib, D = gpu.lib(), gpu.DeviceBuffer
+    rng = np.random.default_rng(11)
+    K, N = 1024, 512
+    W = _bf16_rows(rng, N, K, 0.03)
+    dW = D.from_numpy(W)
+    wsb = lib.skv_prompt_gemm_workspace_bytes(200, K, N)
+    ws = D(wsb)
+    w64 = oracle.bf16_to_f32(W).astype(np.float64)
+    for n in (200, 8, 131):
+        x = rng.standard_normal((n, K)).astype(np.float32)
+        res = rng.standard_normal((n, N)).astype(np.float32)
+        dx, dy = D.from_numpy(x), D.from_numpy(res)
+        gpu._check(lib.skv_linear_residual_gemm_f32(dx.ptr, n, dW.ptr, gpu.DTYPE_BF16, 1, K, K, N, None, dy.ptr,
+                                                    dy.ptr, ws.ptr, wsb, None))
+        gpu.synchronize()
+        ref = x.astype(np.float64) @ w64.T + res
+        got = dy.download(np.float32, (n, N)).astype(np.float64)
+        assert np.abs(got - ref).max() <= 1e-4 * np.sqrt((ref ** 2).mean()), n
+
+
+def test_gemm_projections_refuse_unsupported_shapes(gpu):
+    """fp32 weights, in_dim not a multiple of 8, an output count not a multiple
+    of 8: SKV_ERR_UNSUPPORTED and nothing written."""
+    lib, D = gpu.lib(), gpu.DeviceBuffer
+    y = D.from_numpy(np.full((3, 64), 7.0, np.float32))
+    res = D.from_numpy(np.zeros((3, 64), np.float32))
+    for K, out_dim, dt in ((1024, 64, gpu.DTYPE_FP32), (1020, 64, gpu.DTYPE_BF16), (1024, 60, gpu.DTYPE_BF16)):
+        esz = 2 if dt == gpu.DTYPE_BF16 else 4
+        w = D(64 * K * esz)
+        x = D.from_numpy(np.ones((3, K), np.float32))
+        wsb = lib.skv_prompt_gemm_workspace_bytes(3, K, out_dim)
+        ws = D(wsb)
+        rc = lib.skv_linear_residual_gemm_f32(x.ptr, 3, w.ptr, dt, 1, K, K, out_dim, None, res.ptr, y.ptr, ws.ptr,
+                                              wsb, None)
+        assert rc == gpu.SKV_ERR_UNSUPPORTED, (K, out_dim, dt)
+    gpu.synchronize()
+    assert np.array_equal(y.download(np.float32, (3, 64)), np.full((3, 64), 7.0, np.float32))
