@@ -602,8 +602,8 @@ def run_cfg1(steps: int, warmup: int, with_cpu: bool):
             line["prompt_2048"] = {
                 "ms": ms, "prompt_tokens_per_s": round(2048 / (ms / 1e3), 1),
                 "note": ("Generator::generate(prompt of 2,048 ids, 1 new token): embedding, prefill_into of 22 "
-                         "TinyLlama-shaped layers (q/k/v, o, gate/up, down on the matrix cores with inputs split "
-                         "into bf16 hi + lo, causal prefill attention), lm_head and the first greedy token")}
+                         "TinyLlama-shaped layers (q/k/v, o, gate/up, down as hipBLASLt bf16 GEMMs over the inputs "
+                         "split into bf16 hi + lo, causal prefill attention), lm_head and the first greedy token")}
         else:
             log(f"long-prompt driver failed ({proc.returncode}): {proc.stderr.strip()[-300:]}")
     if with_cpu:
