@@ -49,6 +49,10 @@ public:
     Tensor to(Device target) const;
     // Shared-storage BF16 matrix transpose view (logical [K, N] over [N, K] rows).
     Tensor transpose_2d() const;
+    // Shared-storage view of rows [first, first + count) of a contiguous 2-D
+    // tensor (the projections of one layer packed in one allocation).  No
+    // counterpart in the reference.
+    Tensor rows_view(std::size_t first, std::size_t count) const;
     bool is_contiguous() const noexcept {
         return ndim() != 2 || (strides_[0] == shape_[1] && strides_[1] == 1);
     }

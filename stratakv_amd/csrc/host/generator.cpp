@@ -127,6 +127,37 @@ public:
         layer.set_weight(t.transpose_2d());
     }
 
+    // Several checkpoint linears with one input width as consecutive row
+    // blocks of ONE bf16 allocation ([sum of out, in]), each layer holding a
+    // view of its block: the same values and strides as take_linear gives, so
+    // every kernel reads the same bits, and the prompt path's library GEMMs
+    // then run q/k/v (or gate/up) as one GEMM (skv_*_gemm_f32 detect rows
+    // that follow one another).
+    void take_linears_packed(std::initializer_list<std::pair<std::string, layers::Linear*>> items) {
+        std::size_t in = 0, rows = 0;
+        for (const auto& [key, layer] : items) {
+            if (in != 0 && layer->input_dim() != in) throw std::invalid_argument("Wrong shape/storage: " + key);
+            in = layer->input_dim();
+            rows += layer->output_dim();
+        }
+        Tensor packed({rows, in}, DataType::BF16, Device::GPU);
+        std::size_t first = 0;
+        for (const auto& [key, layer] : items) {
+            const std::size_t out = layer->output_dim();
+            Tensor t = take(key, {out, in});
+            auto* dst = static_cast<std::uint16_t*>(packed.raw_data()) + first * in;
+            if (t.dtype() == DataType::BF16)
+                detail::check(skv_memcpy_d2d(dst, t.raw_data(), out * in * sizeof(std::uint16_t), stream_),
+                              "Generator: linear weight");
+            else
+                detail::check(skv_convert_to_bf16(t.raw_data(), SKV_DTYPE_FP32, out * in, dst, nullptr, stream_),
+                              "Generator: linear weight");
+            detail::check(skv_stream_synchronize(stream_), "Generator: linear weight");
+            layer->set_weight(packed.rows_view(first, out).transpose_2d());
+            first += out;
+        }
+    }
+
 private:
     io::WeightMap& weights_;
     void* stream_;
@@ -162,12 +193,12 @@ Generator::Generator(GeneratorConfig config, io::WeightMap weights)
             auto& b = blocks_[l];
             b.input_norm() = layers::RMSNorm(w.take_f32(p + "input_layernorm.weight", h));
             b.post_attention_norm() = layers::RMSNorm(w.take_f32(p + "post_attention_layernorm.weight", h));
-            w.take_linear(p + "self_attn.q_proj.weight", b.attention().query_projection());
-            w.take_linear(p + "self_attn.k_proj.weight", b.attention().key_projection());
-            w.take_linear(p + "self_attn.v_proj.weight", b.attention().value_projection());
+            w.take_linears_packed({{p + "self_attn.q_proj.weight", &b.attention().query_projection()},
+                                   {p + "self_attn.k_proj.weight", &b.attention().key_projection()},
+                                   {p + "self_attn.v_proj.weight", &b.attention().value_projection()}});
             w.take_linear(p + "self_attn.o_proj.weight", b.attention().output_projection());
-            w.take_linear(p + "mlp.gate_proj.weight", b.gate_projection());
-            w.take_linear(p + "mlp.up_proj.weight", b.up_projection());
+            w.take_linears_packed({{p + "mlp.gate_proj.weight", &b.gate_projection()},
+                                   {p + "mlp.up_proj.weight", &b.up_projection()}});
             w.take_linear(p + "mlp.down_proj.weight", b.down_projection());
         }
     } else {

@@ -146,6 +146,16 @@ Tensor Tensor::transpose_2d() const {
     return view;
 }
 
+Tensor Tensor::rows_view(std::size_t first, std::size_t count) const {
+    if (ndim() != 2 || !is_contiguous() || !owner_ || count == 0 || first > shape_[0] || count > shape_[0] - first)
+        throw std::invalid_argument("Tensor::rows_view: expected rows of a contiguous matrix");
+    Tensor view(*this, AliasTag{});
+    view.data_ptr_ = static_cast<char*>(data_ptr_) + first * shape_[1] * element_size();
+    view.shape_[0] = count;
+    view.total_elements_ = count * shape_[1];
+    return view;
+}
+
 std::size_t Tensor::storage_index(std::size_t i) const noexcept {
     if (is_contiguous()) return i;
     return (i / shape_[1]) * strides_[0] + (i % shape_[1]) * strides_[1];

@@ -1164,9 +1164,9 @@ __device__ __forceinline__ f32x4_t ld4(const float* p) { return *reinterpret_cas
 __device__ __forceinline__ f32x4_t bias4_at(const float* b, int j) {
     return b != nullptr ? ld4(b + j) : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 }
-// Output j..j+3 of token r from the two halves of d, plus bias.
-__device__ __forceinline__ f32x4_t gemm_out4(const float* d, const float* bias, int n, int rows, int r, int j) {
-    return (ld4(d + static_cast<int64_t>(r) * n + j) + ld4(d + (static_cast<int64_t>(rows) + r) * n + j)) +
+// Output j..j+3 of token r from the two halves of d (row stride ld), plus bias.
+__device__ __forceinline__ f32x4_t gemm_out4(const float* d, const float* bias, int ld, int rows, int r, int j) {
+    return (ld4(d + static_cast<int64_t>(r) * ld + j) + ld4(d + (static_cast<int64_t>(rows) + r) * ld + j)) +
            bias4_at(bias, j);
 }
 
@@ -1184,8 +1184,8 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(GemmEpilogue e) {
     const int half = e.head_dim / 2;
     const int ja = rope ? (u / (half / 4)) * e.head_dim + (u % (half / 4)) * 4 : 8 * u;
     const int jb = rope ? ja + half : ja + 4;
-    f32x4_t a = gemm_out4(e.d[m], e.bias[m], e.n[m], e.rows, r, ja);
-    f32x4_t b = gemm_out4(e.d[m], e.bias[m], e.n[m], e.rows, r, jb);
+    f32x4_t a = gemm_out4(e.d[m], e.bias[m], e.ld[m], e.rows, r, ja);
+    f32x4_t b = gemm_out4(e.d[m], e.bias[m], e.ld[m], e.rows, r, jb);
     if (rope) {
         const float* cs = e.rope_cs + (static_cast<int64_t>(r) * half + ja % e.head_dim) * 2;
 #pragma unroll
@@ -1206,8 +1206,8 @@ __global__ __launch_bounds__(256) void gate_up_epilogue_kernel(GemmEpilogue e) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= static_cast<int64_t>(e.rows) * units) return;
     const int r = static_cast<int>(i / units), j = 4 * static_cast<int>(i - static_cast<int64_t>(r) * units);
-    const f32x4_t g = gemm_out4(e.d[0], e.bias[0], e.n[0], e.rows, r, j);
-    const f32x4_t u = gemm_out4(e.d[1], e.bias[1], e.n[0], e.rows, r, j);
+    const f32x4_t g = gemm_out4(e.d[0], e.bias[0], e.ld[0], e.rows, r, j);
+    const f32x4_t u = gemm_out4(e.d[1], e.bias[1], e.ld[1], e.rows, r, j);
     *reinterpret_cast<f32x4_t*>(e.y[0] + static_cast<int64_t>(r) * e.n[0] + j) =
         f32x4_t{swiglu_of(g[0], u[0]), swiglu_of(g[1], u[1]), swiglu_of(g[2], u[2]), swiglu_of(g[3], u[3])};
 }
@@ -1218,7 +1218,7 @@ __global__ __launch_bounds__(256) void residual_epilogue_kernel(GemmEpilogue e) 
     if (i >= static_cast<int64_t>(e.rows) * units) return;
     const int r = static_cast<int>(i / units), j = 4 * static_cast<int>(i - static_cast<int64_t>(r) * units);
     const int64_t at = static_cast<int64_t>(r) * e.n[0] + j;
-    *reinterpret_cast<f32x4_t*>(e.y[0] + at) = gemm_out4(e.d[0], e.bias[0], e.n[0], e.rows, r, j) + ld4(e.residual + at);
+    *reinterpret_cast<f32x4_t*>(e.y[0] + at) = gemm_out4(e.d[0], e.bias[0], e.ld[0], e.rows, r, j) + ld4(e.residual + at);
 }
 
 int launch_split_rows(const float* x, int rows, int K, const float* gamma, float eps, float* normalized,

@@ -17,7 +17,7 @@ namespace skv {
 int launch_split_rows(const float* x, int rows, int K, const float* gamma, float eps, float* normalized,
                       uint16_t* parts, hipStream_t s, float* rope_cs = nullptr, int first = 0, int head_dim = 0);
 
-// Epilogues over GEMM outputs d[m] = [2 * rows][n[m]] fp32 (row r: the hi
+// Epilogues over GEMM outputs d[m] = [2 * rows][ld[m]] fp32 (row r: the hi
 // products of token r, row rows + r its lo products): out = d[r] + d[rows + r]
 // + bias, then
 //   qkv:      RoPE of q and k at position first + r (first < 0: none; the
@@ -29,6 +29,7 @@ struct GemmEpilogue {
     const float* bias[3];
     float* y[3];
     int n[3];
+    int ld[3];                // row stride of d[m] (n[m], or the packed GEMM's width)
     const float* residual;
     const float* rope_cs;
     int rows, head_dim, first;

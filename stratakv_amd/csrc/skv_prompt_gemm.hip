@@ -139,6 +139,13 @@ bool layout_ok(const void* w, int weight_dtype, int64_t stride_k, int64_t stride
            (stride_n * 2) % 16 == 0 && aligned16(w) && n % 8 == 0;
 }
 
+// Whether matrix m + 1's rows follow matrix m's in memory with the same
+// stride (a packed allocation): then both are one GEMM of their summed width.
+bool follows(const void* a, int n_a, int64_t stride_a, const void* b, int64_t stride_b) {
+    return stride_a == stride_b &&
+           static_cast<const char*>(b) == static_cast<const char*>(a) + 2 * static_cast<int64_t>(n_a) * stride_a;
+}
+
 // Plans every GEMM of the call (nothing launched yet).
 bool plan_all(Gemm* g, int count, int rows, int K) {
     for (int i = 0; i < count; ++i)
@@ -200,22 +207,40 @@ extern "C" int skv_fused_qkv_gemm_f32(const float* hidden, int rows, const float
     if (!ok) return set_error(SKV_ERR_UNSUPPORTED, "%s: layout not taken by the library GEMMs", fn);
     Workspace ws = carve(workspace, rows, K, n[0] + n[1] + n[2]);
     float* y[3] = {q, k, v};
+    // q, k and v rows packed one after another: one GEMM over all three, each
+    // matrix's outputs a column range of its [2 rows][q + k + v] result.
+    const bool packed = follows(wq, n[0], stride_n[0], wk, stride_n[1]) && follows(wk, n[1], stride_n[1], wv, stride_n[2]);
     Gemm g[3];
-    float* d = ws.out;
-    for (int m = 0; m < 3; ++m) {
-        g[m] = Gemm{w[m], stride_n[m], n[m], d, nullptr};
-        d += size_t{2} * rows * n[m];
+    int ngemm = 3;
+    const float* dm[3];
+    int ldm[3];
+    if (packed) {
+        ngemm = 1;
+        g[0] = Gemm{wq, stride_n[0], n[0] + n[1] + n[2], ws.out, nullptr};
+        for (int m = 0, off = 0; m < 3; off += n[m], ++m) {
+            dm[m] = ws.out + off;
+            ldm[m] = n[0] + n[1] + n[2];
+        }
+    } else {
+        float* d = ws.out;
+        for (int m = 0; m < 3; ++m) {
+            g[m] = Gemm{w[m], stride_n[m], n[m], d, nullptr};
+            dm[m] = d;
+            ldm[m] = n[m];
+            d += size_t{2} * rows * n[m];
+        }
     }
-    if (!plan_all(g, 3, rows, K)) return set_error(SKV_ERR_UNSUPPORTED, "%s: no hipBLASLt algorithm", fn);
+    if (!plan_all(g, ngemm, rows, K)) return set_error(SKV_ERR_UNSUPPORTED, "%s: no hipBLASLt algorithm", fn);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (int rc = launch_split_rows(hidden, rows, K, gamma, epsilon, normalized, ws.parts, s,
                                    rope ? ws.rope_cs : nullptr, first_position, head_dim))
         return rc;
-    if (int rc = run_gemms(fn, g, 3, ws.parts, ws.lib, s)) return rc;
+    if (int rc = run_gemms(fn, g, ngemm, ws.parts, ws.lib, s)) return rc;
     GemmEpilogue e{};
     const float* bias[3] = {bias_q, bias_k, bias_v};
     for (int m = 0; m < 3; ++m) {
-        e.d[m] = g[m].d;
+        e.d[m] = dm[m];
+        e.ld[m] = ldm[m];
         e.bias[m] = bias[m];
         e.y[m] = y[m];
         e.n[m] = n[m];
@@ -244,15 +269,20 @@ extern "C" int skv_fused_gate_up_swiglu_gemm_f32(const float* x, int rows, const
                     layout_ok(w_up, weight_dtype, stride_k, stride_n_up, K, out_dim);
     if (!ok) return set_error(SKV_ERR_UNSUPPORTED, "%s: layout not taken by the library GEMMs", fn);
     Workspace ws = carve(workspace, rows, K, 2 * out_dim);
+    // gate and up rows packed one after another: one GEMM of 2 out_dim outputs.
+    const bool packed = follows(w_gate, out_dim, stride_n_gate, w_up, stride_n_up);
     Gemm g[2] = {{w_gate, stride_n_gate, out_dim, ws.out, nullptr},
                  {w_up, stride_n_up, out_dim, ws.out + size_t{2} * rows * out_dim, nullptr}};
-    if (!plan_all(g, 2, rows, K)) return set_error(SKV_ERR_UNSUPPORTED, "%s: no hipBLASLt algorithm", fn);
+    if (packed) g[0].n = 2 * out_dim;
+    const int ngemm = packed ? 1 : 2;
+    if (!plan_all(g, ngemm, rows, K)) return set_error(SKV_ERR_UNSUPPORTED, "%s: no hipBLASLt algorithm", fn);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (int rc = launch_split_rows(x, rows, K, gamma, epsilon, normalized, ws.parts, s)) return rc;
-    if (int rc = run_gemms(fn, g, 2, ws.parts, ws.lib, s)) return rc;
+    if (int rc = run_gemms(fn, g, ngemm, ws.parts, ws.lib, s)) return rc;
     GemmEpilogue e{};
-    e.d[0] = g[0].d;
-    e.d[1] = g[1].d;
+    e.d[0] = ws.out;
+    e.d[1] = packed ? ws.out + out_dim : g[1].d;
+    e.ld[0] = e.ld[1] = packed ? 2 * out_dim : out_dim;
     e.bias[0] = bias_gate;
     e.bias[1] = bias_up;
     e.y[0] = act;
@@ -280,6 +310,7 @@ extern "C" int skv_linear_residual_gemm_f32(const float* x, int rows, const void
     if (int rc = run_gemms(fn, g, 1, ws.parts, ws.lib, s)) return rc;
     GemmEpilogue e{};
     e.d[0] = g[0].d;
+    e.ld[0] = out_dim;
     e.bias[0] = bias;
     e.y[0] = y;
     e.n[0] = out_dim;

@@ -45,26 +45,53 @@ def _run_all(gpu, entry, dW, ld, bp, dims, n, position, dx, dg, dctx, dact, dres
                                      dres.ptr, out["d"].ptr, *extra, None))
 
 
+class _At:
+    """A device address inside another buffer (kept alive by it)."""
+
+    def __init__(self, buf, offset):
+        self.buf, self.ptr = buf, buf.ptr + offset
+
+
+def _upload_weights(D, W, names, pad, packed):
+    """Device weights and row strides: each matrix in its own buffer, or
+    (packed) the matrices of each group of `names` as consecutive row blocks
+    of one buffer, as the Generator's loader places q/k/v and gate/up."""
+    dW, ld = {}, {}
+    groups = (("q", "k", "v"), ("g", "u")) if packed else ()
+    for group in groups:
+        stride = W[group[0]].shape[1] + max(pad.get(n, 0) for n in group)
+        rows = np.concatenate([_padded(W[n], stride - W[n].shape[1])[0] for n in group])
+        base = D.from_numpy(rows)
+        first = 0
+        for n in group:
+            dW[n], ld[n] = _At(base, 2 * first * stride), stride
+            first += W[n].shape[0]
+    for n in names:
+        if n not in dW:
+            buf, ld[n] = _padded(W[n], pad.get(n, 0))
+            dW[n] = D.from_numpy(buf)
+    return dW, ld
+
+
 @pytest.mark.parametrize("dims", [(2048, 32, 4, 64, 5632), (1024, 8, 2, 128, 1536)], ids=["tinyllama", "hd128"])
 @pytest.mark.parametrize("with_bias", [False, True])
-def test_gemm_projections_match_float64_and_mm(gpu, dims, with_bias):
+@pytest.mark.parametrize("packed", [False, True], ids=["separate", "packed"])
+def test_gemm_projections_match_float64_and_mm(gpu, dims, with_bias, packed):
     """Every output within 1e-4 of its matrix's rms of the float64 result (a
     dropped lo part errs by ~2e-3 relative, a wrong RoPE pair, token or half
     by O(1)), each within 5e-5 (|ref| + rms) of the matrix-core kernels'
     (fp32 sums in another order), and the normalised rows bit-identical to
     theirs.  Tokens 1 .. 1,024 (the 1,024-token chunk of
-    the prompt path), RoPE positions up to 16,381 and none, and weight rows
-    with a padded stride for o_proj and gate."""
+    the prompt path), RoPE positions up to 16,381 and none, weight rows with a
+    padded stride for o_proj and gate, and q/k/v and gate/up each packed in one
+    allocation (one GEMM each) or apart."""
     H, Hq, Hkv, hd, inter = dims
     rng = np.random.default_rng(7 * H + inter + with_bias)
     lib, D = gpu.lib(), gpu.DeviceBuffer
     shapes = (("q", Hq * hd, H), ("k", Hkv * hd, H), ("v", Hkv * hd, H), ("o", H, Hq * hd),
               ("g", inter, H), ("u", inter, H), ("d", H, inter))
     W = {n: _bf16_rows(rng, o, i, 0.03) for n, o, i in shapes}
-    dW, ld = {}, {}
-    for name, _, _ in shapes:
-        buf, ld[name] = _padded(W[name], 64 if name in "og" else 0)
-        dW[name] = D.from_numpy(buf)
+    dW, ld = _upload_weights(D, W, [n for n, _, _ in shapes], {"o": 64, "g": 64}, packed)
     B = {n: (rng.standard_normal(o).astype(np.float32) if with_bias else None) for n, o, _ in shapes}
     dB = {n: (D.from_numpy(B[n]) if B[n] is not None else None) for n, _, _ in shapes}
     bp = lambda n: dB[n].ptr if dB[n] is not None else None
