@@ -592,8 +592,8 @@ def run_cfg1(steps: int, warmup: int, with_cpu: bool):
                 "generate(1); weight_gbs = bf16 weight bytes read per decode token / decode time"))
         else:
             log(f"generate driver failed ({proc.returncode}): {proc.stderr.strip()[-300:]}")
-        # A long prompt: the prompt pass (prefill_into of 2,048 tokens in
-        # 1,024-token chunks, projections on the matrix cores) and the first token.
+        # A long prompt: the prompt pass (prefill_into of 2,048 tokens in one
+        # chunk, projections as library GEMMs) and the first token.
         proc = subprocess.run([gen_driver, "--prompt", "2048", "--new", "1", "--repeat", "3"], stdout=subprocess.PIPE,
                               stderr=subprocess.PIPE, text=True, timeout=600)
         if proc.returncode == 0:

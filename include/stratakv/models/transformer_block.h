@@ -75,9 +75,9 @@ public:
     // prefill_chunk_rows() tokens, as many as kPrefillChunk and the scratch
     // budget allow (never fewer than kPrefillMinChunk).  Long chunks give the
     // projections and the attention large grids.
-    static constexpr int kPrefillChunk = 1024;
+    static constexpr int kPrefillChunk = 2048;
     static constexpr int kPrefillMinChunk = 256;
-    static constexpr std::size_t kPrefillScratchBudget = std::size_t{96} << 20;  // bytes per block
+    static constexpr std::size_t kPrefillScratchBudget = std::size_t{128} << 20;  // bytes per block
     int prefill_chunk_rows() const noexcept;
     // Chunk length from which the projections run on the matrix cores.
     static constexpr int kPrefillMmRows = 32;

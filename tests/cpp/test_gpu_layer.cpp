@@ -354,14 +354,14 @@ void transformer_block_parity() {
     check(threw, "mismatched pool geometry is rejected");
 }
 
-// TransformerBlock::prefill_into: several tokens per call (a 1,100-token prompt
+// TransformerBlock::prefill_into: several tokens per call (a 2,100-token prompt
 // = two internal chunks, then a second 21-token chunk with aliased
 // input/output), then decode steps through forward_into on the cache the
 // prefill wrote.  Every output row against the float64 layer with causal
 // attention over the pools as the device holds them; the prefill's K/V rows
 // against the bf16 rounding of the float64 K/V.
 void prefill_parity() {
-    const int H = 512, I = 768, Hq = 8, Hkv = 2, hd = H / Hq, bs = 16, total = 80;
+    const int H = 512, I = 768, Hq = 8, Hkv = 2, hd = H / Hq, bs = 16, total = 140;
     std::mt19937 rng(77);
     std::normal_distribution<float> nd(0.0f, 1.0f);
     stratakv::models::TransformerBlock block(H, I, Hq, Hkv, total, bs);
@@ -427,11 +427,11 @@ void prefill_parity() {
                                             (1e-3 + 1e-3 * std::fabs(want[i])));
         }
     };
-    check(block.prefill_chunk_rows() == 1024, "prefill chunk of this layer: 1,024 tokens");
-    run(1100, true, false);  // prompt: 1,024 + 76 tokens inside prefill_into
+    check(block.prefill_chunk_rows() == 2048, "prefill chunk of this layer: 2,048 tokens");
+    run(2100, true, false);  // prompt: 2,048 + 52 tokens inside prefill_into
     run(21, true, true);     // a later chunk, input and output aliased
     run(2, false, false);    // decode on the prefilled cache
-    check(pt.get_state(3).sequence_length == 1123, "prefill + decode length");
+    check(pt.get_state(3).sequence_length == 2123, "prefill + decode length");
     check(worst <= 1.0, "prefill_into matches the float64 layer (worst error / bound = " + std::to_string(worst) + ")");
     check(worst_kv <= 1.0 / 64, "prefill K/V are the bf16 rounding of the rows (" + std::to_string(worst_kv) + ")");
     std::printf("prefill_into: worst error/bound %.3g, worst K/V rel diff %.3g\n", worst, worst_kv);
