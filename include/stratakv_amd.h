@@ -464,6 +464,24 @@ int skv_linear_residual_gemm_f32(const float* x, int rows, const void* weight, i
                                  int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
                                  const float* bias, const float* residual, float* y,
                                  void* workspace, size_t workspace_bytes, void* stream);
+/* The whole feed-forward half of the layer on the library GEMMs:
+ * y = x + down(swiglu(gate(n), up(n))) with n = rmsnorm(x, gamma) (written to
+ * `normalized`) and the projections' biases; y may alias x.  The SwiGLU
+ * epilogue writes the activations straight as the bf16 hi / lo operand of
+ * down_proj (no fp32 activation rows): the arithmetic of
+ * skv_fused_gate_up_swiglu_gemm_f32 followed by skv_linear_residual_gemm_f32
+ * (residual x), equal to it to fp32 rounding (hipBLASLt's kernels for skinny
+ * shapes may split K and add the parts in any order).  Workspace: skv_prompt_gemm_workspace_bytes(rows,
+ * max(hidden_dim, inter_dim), max(2 * inter_dim, hidden_dim)).  The same
+ * SKV_ERR_UNSUPPORTED rules as the separate calls.
+ * Replaces: src/models/transformer_block.cpp:310-332 (post-attention norm,
+ * gate/up, SwiGLU, down_proj and the residual); no counterpart of its own. */
+int skv_ffn_swiglu_gemm_f32(const float* x, int rows, const float* gamma, float epsilon,
+                            const void* w_gate, const void* w_up, const void* w_down, int weight_dtype,
+                            int64_t stride_k, int64_t stride_n_gate, int64_t stride_n_up,
+                            int64_t stride_n_down, const float* bias_gate, const float* bias_up,
+                            const float* bias_down, int hidden_dim, int inter_dim, float* y,
+                            float* normalized, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- model boundary: checkpoint tensors, embedding, token choice --------
  * Checkpoint decode on the device (the host only moves file bytes).  src holds

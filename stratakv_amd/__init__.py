@@ -142,6 +142,8 @@ _PROTOS = {
                                                  _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "skv_linear_residual_gemm_f32": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp,
                                             _vp, _vp, _sz, _vp]),
+    "skv_ffn_swiglu_gemm_f32": (_i32, [_vp, _i32, _vp, _f32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64,
+                                       _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "skv_rope_rows_f32": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
     "skv_write_i32": (_i32, [_vp, _c.POINTER(_c.c_int32), _i32, _vp]),
     "skv_convert_to_bf16": (_i32, [_vp, _i32, _sz, _vp, _vp, _vp]),

@@ -564,6 +564,8 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
             for (const auto& [in, outs] : {std::pair<int, int>{hidden, q_dim + 2 * kv_dim}, {hidden, 2 * inter},
                                            {q_dim, hidden}, {inter, hidden}})
                 gemm_bytes = std::max(gemm_bytes, skv_prompt_gemm_workspace_bytes(n, in, outs));
+            gemm_bytes = std::max(gemm_bytes, skv_prompt_gemm_workspace_bytes(n, std::max(hidden, inter),
+                                                                              std::max(2 * inter, hidden)));
             gemm_ws = prefill_gemm_workspace(gemm_bytes);
         }
         // Input RMSNorm, q/k/v projections and RoPE at p0 + row.
@@ -620,51 +622,63 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
             linear(wo, ctx, n, h, "prefill_into: o_proj");
             detail::check(skv_add_f32(h, x, n * hidden, s), "prefill_into: residual");
         }
-        // Post-attention RMSNorm, gate/up and SwiGLU.
-        auto gate_up = [&](auto entry, float* scratch) {
-            return entry(h, n, cfp(norm2_.gamma()), norm2_.epsilon(), gate_proj_.weight().raw_data(),
-                         up_proj_.weight().raw_data(), wdtype(gate_proj_), stride_k(gate_proj_), stride_n(gate_proj_),
-                         stride_n(up_proj_), bias_of(gate_proj_), bias_of(up_proj_), hidden, inter, act, scratch, s);
-        };
-        // The library-GEMM entry point in the shape of the others (workspace bound here).
-        auto gate_up_gemm_entry = [&](const float* xx, int rows, const float* g, float e, const void* a,
-                                      const void* b, int dt, int64_t sk, int64_t sa, int64_t sb, const float* ba,
-                                      const float* bb, int in, int out, float* y_, float* scratch, void* st) {
-            return skv_fused_gate_up_swiglu_gemm_f32(xx, rows, g, e, a, b, dt, sk, sa, sb, ba, bb, in, out, y_,
-                                                     scratch, gemm_ws, gemm_bytes, st);
-        };
-        if (!(ffn_same &&
-              ((lib && fused(gate_up(gate_up_gemm_entry, fp(*pf_normalized_)), "prefill_into: gate/up as library GEMMs")) ||
-               (mm && fused(gate_up(skv_fused_gate_up_swiglu_mm_f32, fp(*pf_normalized_)),
-                            "prefill_into: gate/up on the matrix cores")) ||
-               fused(gate_up(skv_fused_gate_up_swiglu_rows_f32, fp(*pf_normalized_)),
-                     "prefill_into: fused rmsnorm + gate/up + swiglu")))) {
-            float* hn = fp(*pf_normalized_);
-            float* up = fallback_buffer(pf_up_, static_cast<std::size_t>(inter));
-            detail::check(skv_rmsnorm_f32(h, hn, cfp(norm2_.gamma()), n, hidden, norm2_.epsilon(), s),
-                          "prefill_into: post-attention rmsnorm");
-            linear(gate_proj_, hn, n, act, "prefill_into: gate_proj");
-            linear(up_proj_, hn, n, up, "prefill_into: up_proj");
-            detail::check(skv_swiglu_f32(act, up, n * inter, s), "prefill_into: swiglu");
-        }
-        // down_proj + residual into the output rows.
-        if (!((lib && fused(skv_linear_residual_gemm_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
-                                                         stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
-                                                         bias_of(down_proj_), h, y, gemm_ws, gemm_bytes, s),
-                            "prefill_into: down_proj as a library GEMM")) ||
-              (mm && fused(skv_linear_residual_mm_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
-                                                      stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
-                                                      bias_of(down_proj_), h, y, s),
-                           "prefill_into: down_proj on the matrix cores")) ||
-              fused(skv_linear_residual_rows_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
-                                                 stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
-                                                 bias_of(down_proj_), h, y, s),
-                    "prefill_into: fused down_proj + residual"))) {
-            float* d = fallback_buffer(pf_down_, hidden_dim_);
-            linear(down_proj_, act, n, d, "prefill_into: down_proj");
-            detail::check(skv_add_f32(h, d, n * hidden, s), "prefill_into: residual");
-            detail::check(skv_memcpy_d2d(y, h, static_cast<std::size_t>(n) * hidden * sizeof(float), s),
-                          "prefill_into: output copy");
+        // The feed-forward half as one library-GEMM call (the SwiGLU output
+        // goes straight to down_proj as its split operand), else in two steps.
+        if (!(lib && ffn_same && stride_k(down_proj_) == stride_k(gate_proj_) &&
+              wdtype(down_proj_) == wdtype(gate_proj_) &&
+              fused(skv_ffn_swiglu_gemm_f32(h, n, cfp(norm2_.gamma()), norm2_.epsilon(), gate_proj_.weight().raw_data(),
+                                            up_proj_.weight().raw_data(), down_proj_.weight().raw_data(),
+                                            wdtype(gate_proj_), stride_k(gate_proj_), stride_n(gate_proj_),
+                                            stride_n(up_proj_), stride_n(down_proj_), bias_of(gate_proj_),
+                                            bias_of(up_proj_), bias_of(down_proj_), hidden, inter, y,
+                                            fp(*pf_normalized_), gemm_ws, gemm_bytes, s),
+                    "prefill_into: FFN as library GEMMs"))) {
+            // Post-attention RMSNorm, gate/up and SwiGLU.
+            auto gate_up = [&](auto entry, float* scratch) {
+                return entry(h, n, cfp(norm2_.gamma()), norm2_.epsilon(), gate_proj_.weight().raw_data(),
+                             up_proj_.weight().raw_data(), wdtype(gate_proj_), stride_k(gate_proj_), stride_n(gate_proj_),
+                             stride_n(up_proj_), bias_of(gate_proj_), bias_of(up_proj_), hidden, inter, act, scratch, s);
+            };
+            // The library-GEMM entry point in the shape of the others (workspace bound here).
+            auto gate_up_gemm_entry = [&](const float* xx, int rows, const float* g, float e, const void* a,
+                                          const void* b, int dt, int64_t sk, int64_t sa, int64_t sb, const float* ba,
+                                          const float* bb, int in, int out, float* y_, float* scratch, void* st) {
+                return skv_fused_gate_up_swiglu_gemm_f32(xx, rows, g, e, a, b, dt, sk, sa, sb, ba, bb, in, out, y_,
+                                                         scratch, gemm_ws, gemm_bytes, st);
+            };
+            if (!(ffn_same &&
+                  ((lib && fused(gate_up(gate_up_gemm_entry, fp(*pf_normalized_)), "prefill_into: gate/up as library GEMMs")) ||
+                   (mm && fused(gate_up(skv_fused_gate_up_swiglu_mm_f32, fp(*pf_normalized_)),
+                                "prefill_into: gate/up on the matrix cores")) ||
+                   fused(gate_up(skv_fused_gate_up_swiglu_rows_f32, fp(*pf_normalized_)),
+                         "prefill_into: fused rmsnorm + gate/up + swiglu")))) {
+                float* hn = fp(*pf_normalized_);
+                float* up = fallback_buffer(pf_up_, static_cast<std::size_t>(inter));
+                detail::check(skv_rmsnorm_f32(h, hn, cfp(norm2_.gamma()), n, hidden, norm2_.epsilon(), s),
+                              "prefill_into: post-attention rmsnorm");
+                linear(gate_proj_, hn, n, act, "prefill_into: gate_proj");
+                linear(up_proj_, hn, n, up, "prefill_into: up_proj");
+                detail::check(skv_swiglu_f32(act, up, n * inter, s), "prefill_into: swiglu");
+            }
+            // down_proj + residual into the output rows.
+            if (!((lib && fused(skv_linear_residual_gemm_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
+                                                             stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
+                                                             bias_of(down_proj_), h, y, gemm_ws, gemm_bytes, s),
+                                "prefill_into: down_proj as a library GEMM")) ||
+                  (mm && fused(skv_linear_residual_mm_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
+                                                          stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
+                                                          bias_of(down_proj_), h, y, s),
+                               "prefill_into: down_proj on the matrix cores")) ||
+                  fused(skv_linear_residual_rows_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
+                                                     stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
+                                                     bias_of(down_proj_), h, y, s),
+                        "prefill_into: fused down_proj + residual"))) {
+                float* d = fallback_buffer(pf_down_, hidden_dim_);
+                linear(down_proj_, act, n, d, "prefill_into: down_proj");
+                detail::check(skv_add_f32(h, d, n * hidden, s), "prefill_into: residual");
+                detail::check(skv_memcpy_d2d(y, h, static_cast<std::size_t>(n) * hidden * sizeof(float), s),
+                              "prefill_into: output copy");
+            }
         }
     }
 }

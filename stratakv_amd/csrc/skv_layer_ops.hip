@@ -1201,6 +1201,10 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(GemmEpilogue e) {
     *reinterpret_cast<f32x4_t*>(y + jb) = b;
 }
 
+// PARTS: the activations go out already split (e.parts, [2 rows][n] bf16,
+// split_rows_kernel's layout and rounding) as the next GEMM's input, instead
+// of as fp32 rows.
+template <bool PARTS>
 __global__ __launch_bounds__(256) void gate_up_epilogue_kernel(GemmEpilogue e) {
     const int units = e.n[0] / 4;
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -1208,8 +1212,16 @@ __global__ __launch_bounds__(256) void gate_up_epilogue_kernel(GemmEpilogue e) {
     const int r = static_cast<int>(i / units), j = 4 * static_cast<int>(i - static_cast<int64_t>(r) * units);
     const f32x4_t g = gemm_out4(e.d[0], e.bias[0], e.ld[0], e.rows, r, j);
     const f32x4_t u = gemm_out4(e.d[1], e.bias[1], e.ld[1], e.rows, r, j);
-    *reinterpret_cast<f32x4_t*>(e.y[0] + static_cast<int64_t>(r) * e.n[0] + j) =
-        f32x4_t{swiglu_of(g[0], u[0]), swiglu_of(g[1], u[1]), swiglu_of(g[2], u[2]), swiglu_of(g[3], u[3])};
+    const f32x4_t act = {swiglu_of(g[0], u[0]), swiglu_of(g[1], u[1]), swiglu_of(g[2], u[2]), swiglu_of(g[3], u[3])};
+    if constexpr (PARTS) {
+        uint2 h, l;
+        split_pair(act[0], act[1], h.x, l.x);
+        split_pair(act[2], act[3], h.y, l.y);
+        *reinterpret_cast<uint2*>(e.parts + static_cast<int64_t>(r) * e.n[0] + j) = h;
+        *reinterpret_cast<uint2*>(e.parts + (static_cast<int64_t>(e.rows) + r) * e.n[0] + j) = l;
+    } else {
+        *reinterpret_cast<f32x4_t*>(e.y[0] + static_cast<int64_t>(r) * e.n[0] + j) = act;
+    }
 }
 
 __global__ __launch_bounds__(256) void residual_epilogue_kernel(GemmEpilogue e) {
@@ -1245,7 +1257,8 @@ int launch_qkv_epilogue(const GemmEpilogue& e, hipStream_t s) {
 }
 
 int launch_gate_up_epilogue(const GemmEpilogue& e, hipStream_t s) {
-    gate_up_epilogue_kernel<<<epilogue_grid(e.rows, e.n[0] / 4), 256, 0, s>>>(e);
+    if (e.parts != nullptr) gate_up_epilogue_kernel<true><<<epilogue_grid(e.rows, e.n[0] / 4), 256, 0, s>>>(e);
+    else gate_up_epilogue_kernel<false><<<epilogue_grid(e.rows, e.n[0] / 4), 256, 0, s>>>(e);
     return check_launch("gate_up_epilogue_kernel");
 }
 

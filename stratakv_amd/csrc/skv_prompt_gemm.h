@@ -22,7 +22,7 @@ int launch_split_rows(const float* x, int rows, int K, const float* gamma, float
 // + bias, then
 //   qkv:      RoPE of q and k at position first + r (first < 0: none; the
 //             cos / sin from rope_cs, written by launch_split_rows) into y[m];
-//   gate/up:  act = swiglu(gate, up);
+//   gate/up:  act = swiglu(gate, up) (into y[0], or split into parts);
 //   residual: y = out + residual (y may alias residual).
 struct GemmEpilogue {
     const float* d[3];
@@ -32,6 +32,7 @@ struct GemmEpilogue {
     int ld[3];                // row stride of d[m] (n[m], or the packed GEMM's width)
     const float* residual;
     const float* rope_cs;
+    uint16_t* parts;          // gate/up: write the activations split for the next GEMM here (else y[0])
     int rows, head_dim, first;
 };
 int launch_qkv_epilogue(const GemmEpilogue& e, hipStream_t s);

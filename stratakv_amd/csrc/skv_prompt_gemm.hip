@@ -21,6 +21,7 @@
 
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -315,6 +316,61 @@ extern "C" int skv_linear_residual_gemm_f32(const float* x, int rows, const void
     e.y[0] = y;
     e.n[0] = out_dim;
     e.residual = residual;
+    e.rows = rows;
+    return launch_residual_epilogue(e, s);
+}
+
+extern "C" int skv_ffn_swiglu_gemm_f32(const float* x, int rows, const float* gamma, float epsilon,
+                                       const void* w_gate, const void* w_up, const void* w_down, int weight_dtype,
+                                       int64_t stride_k, int64_t stride_n_gate, int64_t stride_n_up,
+                                       int64_t stride_n_down, const float* bias_gate, const float* bias_up,
+                                       const float* bias_down, int hidden_dim, int inter_dim, float* y,
+                                       float* normalized, void* workspace, size_t workspace_bytes, void* stream) {
+    const char* fn = "skv_ffn_swiglu_gemm_f32";
+    SKV_REQUIRE(x && y && rows > 0 && hidden_dim > 0 && inter_dim > 0, "%s: invalid pointers or sizes", fn);
+    SKV_REQUIRE(gamma == nullptr || normalized != nullptr, "%s: normalized scratch required with gamma", fn);
+    const int H = hidden_dim, I = inter_dim;
+    const int kmax = std::max(H, I), outs = std::max(2 * I, H);
+    if (int rc = check_workspace(fn, workspace, workspace_bytes, rows, kmax, outs)) return rc;
+    const bool ok = H % 8 == 0 && H <= 8192 && I % 8 == 0 && I <= 8192 && aligned16(x) && aligned16(y) &&
+                    (gamma == nullptr || aligned16(normalized)) &&
+                    layout_ok(w_gate, weight_dtype, stride_k, stride_n_gate, H, I) &&
+                    layout_ok(w_up, weight_dtype, stride_k, stride_n_up, H, I) &&
+                    layout_ok(w_down, weight_dtype, stride_k, stride_n_down, I, H);
+    if (!ok) return set_error(SKV_ERR_UNSUPPORTED, "%s: layout not taken by the library GEMMs", fn);
+    Workspace ws = carve(workspace, rows, kmax, outs);
+    const bool packed = follows(w_gate, I, stride_n_gate, w_up, stride_n_up);
+    Gemm g[3] = {{w_gate, stride_n_gate, packed ? 2 * I : I, ws.out, nullptr},
+                 {w_up, stride_n_up, I, ws.out + size_t{2} * rows * I, nullptr},
+                 {w_down, stride_n_down, H, ws.out, nullptr}};
+    const int ngate = packed ? 1 : 2;
+    if (!plan_all(g, ngate, rows, H) || !plan_all(g + 2, 1, rows, I))
+        return set_error(SKV_ERR_UNSUPPORTED, "%s: no hipBLASLt algorithm", fn);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // rmsnorm + split of x; gate/up; SwiGLU straight into the split operand
+    // of down_proj (the activations never go to memory in fp32); down_proj;
+    // + bias + x.  The GEMM outputs reuse one region: each is consumed before
+    // the next GEMM writes it.
+    if (int rc = launch_split_rows(x, rows, H, gamma, epsilon, normalized, ws.parts, s)) return rc;
+    if (int rc = run_gemms(fn, g, ngate, ws.parts, ws.lib, s)) return rc;
+    GemmEpilogue a{};
+    a.d[0] = ws.out;
+    a.d[1] = packed ? ws.out + I : g[1].d;
+    a.ld[0] = a.ld[1] = packed ? 2 * I : I;
+    a.bias[0] = bias_gate;
+    a.bias[1] = bias_up;
+    a.n[0] = a.n[1] = I;
+    a.parts = ws.parts;
+    a.rows = rows;
+    if (int rc = launch_gate_up_epilogue(a, s)) return rc;
+    if (int rc = run_gemms(fn, g + 2, 1, ws.parts, ws.lib, s)) return rc;
+    GemmEpilogue e{};
+    e.d[0] = ws.out;
+    e.ld[0] = H;
+    e.bias[0] = bias_down;
+    e.y[0] = y;
+    e.n[0] = H;
+    e.residual = x;
     e.rows = rows;
     return launch_residual_epilogue(e, s);
 }

@@ -169,3 +169,60 @@ def test_gemm_projections_refuse_unsupported_shapes(gpu):
         assert rc == gpu.SKV_ERR_UNSUPPORTED, (K, out_dim, dt)
     gpu.synchronize()
     assert np.array_equal(y.download(np.float32, (3, 64)), np.full((3, 64), 7.0, np.float32))
+
+
+@pytest.mark.parametrize("dims", [(2048, 32, 4, 64, 5632), (1024, 8, 2, 128, 1536)], ids=["tinyllama", "hd128"])
+@pytest.mark.parametrize("with_bias", [False, True])
+@pytest.mark.parametrize("packed", [False, True], ids=["separate", "packed"])
+def test_ffn_gemm_matches_two_calls_and_float64(gpu, dims, with_bias, packed):
+    """skv_ffn_swiglu_gemm_f32 (rmsnorm, gate/up, SwiGLU written straight as
+    down_proj's split operand, down_proj, + x) in place (y = x): within 1e-4
+    of the rms of the float64 result, within 5e-5 (|ref| + rms) of
+    skv_fused_gate_up_swiglu_gemm_f32 followed by skv_linear_residual_gemm_f32
+    (the same operands; hipBLASLt may sum split K in another order), and the
+    normalised rows bit-identical."""
+    H, _, _, _, inter = dims
+    rng = np.random.default_rng(3 * H + inter + with_bias + 2 * packed)
+    lib, D = gpu.lib(), gpu.DeviceBuffer
+    W = {n: _bf16_rows(rng, o, i, 0.03) for n, o, i in (("g", inter, H), ("u", inter, H), ("d", H, inter))}
+    dW, ld = _upload_weights(D, W, ["g", "u", "d"], {}, False)
+    if packed:
+        base = D.from_numpy(np.concatenate([W["g"], W["u"]]))
+        dW["g"], dW["u"] = _At(base, 0), _At(base, 2 * inter * H)
+    B = {n: (rng.standard_normal(W[n].shape[0]).astype(np.float32) if with_bias else None) for n in "gud"}
+    dB = {n: (D.from_numpy(B[n]) if B[n] is not None else None) for n in "gud"}
+    bp = lambda n: dB[n].ptr if dB[n] is not None else None
+    eps = ctypes.c_float(1e-5)
+    max_rows = 1024
+    wsb = lib.skv_prompt_gemm_workspace_bytes(max_rows, max(H, inter), max(2 * inter, H))
+    ws = D(wsb)
+    w64 = {n: oracle.bf16_to_f32(W[n]).astype(np.float64) for n in "gud"}
+    b64 = {n: (B[n].astype(np.float64) if B[n] is not None else 0.0) for n in "gud"}
+    for n in (1, 37, 300, max_rows):
+        x = rng.standard_normal((n, H)).astype(np.float32)
+        gamma = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+        dx, dg = D.from_numpy(x), D.from_numpy(gamma)
+        # two calls: act through memory
+        act, xn, y2 = D(4 * n * inter), D(4 * n * H), D(4 * n * H)
+        gpu._check(lib.skv_fused_gate_up_swiglu_gemm_f32(dx.ptr, n, dg.ptr, eps, dW["g"].ptr, dW["u"].ptr,
+                                                         gpu.DTYPE_BF16, 1, H, H, bp("g"), bp("u"), H, inter, act.ptr,
+                                                         xn.ptr, ws.ptr, wsb, None))
+        gpu._check(lib.skv_linear_residual_gemm_f32(act.ptr, n, dW["d"].ptr, gpu.DTYPE_BF16, 1, inter, inter, H,
+                                                    bp("d"), dx.ptr, y2.ptr, ws.ptr, wsb, None))
+        # one call, in place
+        dy, xn1 = D.from_numpy(x), D(4 * n * H)
+        gpu._check(lib.skv_ffn_swiglu_gemm_f32(dy.ptr, n, dg.ptr, eps, dW["g"].ptr, dW["u"].ptr, dW["d"].ptr,
+                                               gpu.DTYPE_BF16, 1, H, H, inter, bp("g"), bp("u"), bp("d"), H, inter,
+                                               dy.ptr, xn1.ptr, ws.ptr, wsb, None))
+        gpu.synchronize()
+        one, two = dy.download(np.float32, (n, H)), y2.download(np.float32, (n, H))
+        assert np.array_equal(xn1.download(np.uint32, (n, H)), xn.download(np.uint32, (n, H))), n
+        x64 = x.astype(np.float64)
+        xn64 = x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + 1e-5) * gamma.astype(np.float64)
+        g, u = xn64 @ w64["g"].T + b64["g"], xn64 @ w64["u"].T + b64["u"]
+        ref = (g / (1.0 + np.exp(-g)) * u) @ w64["d"].T + b64["d"] + x64
+        rms = np.sqrt((ref ** 2).mean())
+        err = np.abs(one.astype(np.float64) - ref).max()
+        assert np.isfinite(one).all() and err <= 1e-4 * rms, (n, err)
+        dtwo = (np.abs(one.astype(np.float64) - two) / (np.abs(ref) + rms)).max()
+        assert dtwo <= 5e-5, (n, dtwo)
