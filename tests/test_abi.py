@@ -195,3 +195,10 @@ def test_library_gemm_projections_reject_invalid_arguments():
     assert res(-1, 2048, 2048) == skv.SKV_ERR_INVALID_ARGUMENT
     assert res(2, 2048, 2048, nbytes=0) == skv.SKV_ERR_INVALID_ARGUMENT
     assert res(2, 2048, 2052) == skv.SKV_ERR_UNSUPPORTED                            # out_dim not a multiple of 8
+    ffn = lambda rows, H, I, normalized=FAKE, nbytes=big: lib.skv_ffn_swiglu_gemm_f32(
+        FAKE, rows, FAKE, eps, FAKE, FAKE, FAKE, B, 1, H, H, I, None, None, None, H, I, FAKE, normalized, FAKE,
+        nbytes, None)
+    assert ffn(0, 2048, 5632) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert ffn(4, 2048, 5632, normalized=None) == skv.SKV_ERR_INVALID_ARGUMENT       # gamma without scratch
+    assert ffn(4, 2048, 5632, nbytes=wsb(4, 5632, 11264) - 1) == skv.SKV_ERR_INVALID_ARGUMENT
+    assert ffn(4, 2048, 5636) == skv.SKV_ERR_UNSUPPORTED                            # inter not a multiple of 8
