@@ -77,22 +77,25 @@ public:
     // projections and the attention large grids.
     static constexpr int kPrefillChunk = 2048;
     static constexpr int kPrefillMinChunk = 256;
-    static constexpr std::size_t kPrefillScratchBudget = std::size_t{128} << 20;  // bytes per block
+    static constexpr std::size_t kPrefillScratchBudget = std::size_t{1} << 30;  // bytes of fp32 rows per scratch
     int prefill_chunk_rows() const noexcept;
     // Chunk length from which the projections run on the matrix cores.
     static constexpr int kPrefillMmRows = 32;
     // Chunk length from which the projections run as hipBLASLt GEMMs
     // (skv_*_gemm_f32), equal to the matrix-core kernels to fp32 rounding.
     static constexpr int kPrefillGemmRows = 256;
-    // The GEMMs' workspace (skv_prompt_gemm_workspace_bytes for the chunk).
-    // Blocks may share one when they run one after another on one stream (a
-    // Generator's layers); a block with none allocates its own on first use.
-    struct PrefillGemmWorkspace {
-        std::optional<Tensor> buffer;
+    // prefill_into's scratch: the chunk's q, k, v, context, residual,
+    // activation and normalised rows, its metadata and the library GEMMs'
+    // workspace (skv_prompt_gemm_workspace_bytes).  Blocks of one shape that
+    // run one after another on one stream (a Generator's layers) may share
+    // one; a block with none allocates its own on first use.  Buffers are
+    // grown on demand and re-made when a block of another shape uses them.
+    struct PrefillScratch {
+        int rows = 0;
+        std::size_t dims[4] = {0, 0, 0, 0};   // hidden, q, kv, intermediate
+        std::optional<Tensor> queries, keys, values, context, residual, act, normalized, up, down, meta, gemm;
     };
-    void share_prefill_gemm_workspace(std::shared_ptr<PrefillGemmWorkspace> ws) noexcept {
-        pf_gemm_ = std::move(ws);
-    }
+    void share_prefill_scratch(std::shared_ptr<PrefillScratch> scratch) noexcept { pf_ = std::move(scratch); }
     void forward_into(const Tensor& hidden_states, Tensor& output, int seq_id,
                       memory::PageTable& page_table, memory::BlockPool& block_pool,
                       bool append_tokens = true);
@@ -162,15 +165,11 @@ private:
     std::optional<Tensor> up_workspace_;
     std::optional<Tensor> down_workspace_;
     std::optional<Tensor> decode_workspace_;  // skv_paged_attention_decode scratch
-    // prefill_into scratch, [rows][dim] for up to prefill_rows_ tokens
-    // (allocated on first use, grown to prefill_chunk_rows() at most;
-    // pf_up_ and pf_down_ only when the separate-kernel fallback runs).
+    // prefill_into scratch, [rows][dim] for up to pf_->rows tokens (allocated
+    // on first use, grown to prefill_chunk_rows() at most; up and down only
+    // when the separate-kernel fallback runs).
     void ensure_prefill_workspace(int rows);
-    int prefill_rows_ = 0;
-    std::optional<Tensor> pf_queries_, pf_keys_, pf_values_, pf_context_, pf_residual_, pf_act_;
-    std::optional<Tensor> pf_normalized_, pf_up_, pf_down_;
-    std::optional<Tensor> pf_meta_;  // 4 int32: position, chunk offsets {0, n}, context length
-    std::shared_ptr<PrefillGemmWorkspace> pf_gemm_;
+    std::shared_ptr<PrefillScratch> pf_;
     // The shared workspace grown to at least `bytes`; its 256-byte aligned start.
     void* prefill_gemm_workspace(std::size_t bytes);
 };

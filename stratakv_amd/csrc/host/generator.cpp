@@ -221,9 +221,9 @@ Generator::Generator(GeneratorConfig config, io::WeightMap weights)
     (void)kv_dim;
 
     for (auto& b : blocks_) b.to(Device::GPU);
-    // The layers run one after another on one stream: one prompt-GEMM workspace serves them all.
-    const auto gemm_ws = std::make_shared<models::TransformerBlock::PrefillGemmWorkspace>();
-    for (auto& b : blocks_) b.share_prefill_gemm_workspace(gemm_ws);
+    // The layers run one after another on one stream: one prefill scratch serves them all.
+    const auto scratch = std::make_shared<models::TransformerBlock::PrefillScratch>();
+    for (auto& b : blocks_) b.share_prefill_scratch(scratch);
     // STRATAKV_PARITY=1 (src/generation/generator.cpp:33-36): the reference
     // compares every layer with its CPU copy; this build has no CPU layers and
     // runs each block's attention check instead.

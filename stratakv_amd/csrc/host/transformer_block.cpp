@@ -429,30 +429,33 @@ int TransformerBlock::prefill_chunk_rows() const noexcept {
 }
 
 void TransformerBlock::ensure_prefill_workspace(int rows) {
-    if (rows <= prefill_rows_) return;
-    const std::size_t r = static_cast<std::size_t>(rows);
+    if (!pf_) pf_ = std::make_shared<PrefillScratch>();
     const std::size_t q_dim = attention_.num_heads() * attention_.head_dim();
     const std::size_t kv_dim = attention_.num_kv_heads() * attention_.head_dim();
     const std::size_t inter = gate_proj_.output_dim();
+    const std::size_t dims[4] = {hidden_dim_, q_dim, kv_dim, inter};
+    const bool same_shape = std::equal(dims, dims + 4, pf_->dims);
+    if (same_shape && rows <= pf_->rows) return;
+    const std::size_t r = static_cast<std::size_t>(same_shape ? rows : std::max(rows, pf_->rows));
     auto make = [&](std::optional<Tensor>& t, std::size_t dim) {
         t.emplace(std::vector<std::size_t>{r, dim}, DataType::FP32, Device::GPU);
     };
-    make(pf_queries_, q_dim);
-    make(pf_keys_, kv_dim);
-    make(pf_values_, kv_dim);
-    make(pf_context_, q_dim);
-    make(pf_residual_, hidden_dim_);
-    make(pf_act_, inter);
-    make(pf_normalized_, hidden_dim_);
-    pf_up_.reset();
-    pf_down_.reset();
-    if (!pf_meta_) pf_meta_.emplace(std::vector<std::size_t>{4}, DataType::FP32, Device::GPU);
-    prefill_rows_ = rows;
+    make(pf_->queries, q_dim);
+    make(pf_->keys, kv_dim);
+    make(pf_->values, kv_dim);
+    make(pf_->context, q_dim);
+    make(pf_->residual, hidden_dim_);
+    make(pf_->act, inter);
+    make(pf_->normalized, hidden_dim_);
+    pf_->up.reset();
+    pf_->down.reset();
+    if (!pf_->meta) pf_->meta.emplace(std::vector<std::size_t>{4}, DataType::FP32, Device::GPU);
+    pf_->rows = static_cast<int>(r);
+    std::copy(dims, dims + 4, pf_->dims);
 }
 
 void* TransformerBlock::prefill_gemm_workspace(std::size_t bytes) {
-    if (!pf_gemm_) pf_gemm_ = std::make_shared<PrefillGemmWorkspace>();
-    std::optional<Tensor>& b = pf_gemm_->buffer;
+    std::optional<Tensor>& b = pf_->gemm;
     if (!b || b->num_elements() * sizeof(float) < bytes)
         b.emplace(std::vector<std::size_t>{(bytes + sizeof(float) - 1) / sizeof(float)}, DataType::FP32,
                   Device::GPU);
@@ -496,7 +499,7 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
     const int q_dim = num_heads * head_dim;
     const int chunk = prefill_chunk_rows();
     ensure_prefill_workspace(std::min(tokens, chunk));
-    const std::size_t ws_rows = static_cast<std::size_t>(prefill_rows_);
+    const std::size_t ws_rows = static_cast<std::size_t>(pf_->rows);
     auto fallback_buffer = [&](std::optional<Tensor>& t, std::size_t dim) {
         if (!t) t.emplace(std::vector<std::size_t>{ws_rows, dim}, DataType::FP32, Device::GPU);
         return static_cast<float*>(t->raw_data());
@@ -530,13 +533,13 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                             stride_k(wq) == stride_k(wk) && stride_k(wq) == stride_k(wv);
     const bool ffn_same = wdtype(gate_proj_) == wdtype(up_proj_) && stride_k(gate_proj_) == stride_k(up_proj_);
     const int64_t qkv_strides[3] = {stride_n(wq), stride_n(wk), stride_n(wv)};
-    float* q = fp(*pf_queries_);
-    float* k = fp(*pf_keys_);
-    float* v = fp(*pf_values_);
-    float* ctx = fp(*pf_context_);
-    float* h = fp(*pf_residual_);
-    float* act = fp(*pf_act_);
-    auto* meta = static_cast<std::int32_t*>(pf_meta_->raw_data());
+    float* q = fp(*pf_->queries);
+    float* k = fp(*pf_->keys);
+    float* v = fp(*pf_->values);
+    float* ctx = fp(*pf_->context);
+    float* h = fp(*pf_->residual);
+    float* act = fp(*pf_->act);
+    auto* meta = static_cast<std::int32_t*>(pf_->meta->raw_data());
 
     for (int c0 = 0; c0 < tokens; c0 += chunk) {
         const int n = std::min(chunk, tokens - c0);
@@ -582,10 +585,10 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                                           kk, vv, scratch, gemm_ws, gemm_bytes, st);
         };
         if (!(same_dtype &&
-              ((lib && fused(qkv(qkv_gemm_entry, fp(*pf_normalized_)), "prefill_into: q/k/v as library GEMMs")) ||
-               (mm && fused(qkv(skv_fused_qkv_mm_f32, fp(*pf_normalized_)), "prefill_into: q/k/v on the matrix cores")) ||
-               fused(qkv(skv_fused_qkv_rows_f32, fp(*pf_normalized_)), "prefill_into: fused rmsnorm + q/k/v + rope")))) {
-            float* xn = fp(*pf_normalized_);
+              ((lib && fused(qkv(qkv_gemm_entry, fp(*pf_->normalized)), "prefill_into: q/k/v as library GEMMs")) ||
+               (mm && fused(qkv(skv_fused_qkv_mm_f32, fp(*pf_->normalized)), "prefill_into: q/k/v on the matrix cores")) ||
+               fused(qkv(skv_fused_qkv_rows_f32, fp(*pf_->normalized)), "prefill_into: fused rmsnorm + q/k/v + rope")))) {
+            float* xn = fp(*pf_->normalized);
             detail::check(skv_rmsnorm_f32(x, xn, cfp(norm1_.gamma()), n, hidden, norm1_.epsilon(), s),
                           "prefill_into: input rmsnorm");
             linear(wq, xn, n, q, "prefill_into: q_proj");
@@ -631,7 +634,7 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                                             wdtype(gate_proj_), stride_k(gate_proj_), stride_n(gate_proj_),
                                             stride_n(up_proj_), stride_n(down_proj_), bias_of(gate_proj_),
                                             bias_of(up_proj_), bias_of(down_proj_), hidden, inter, y,
-                                            fp(*pf_normalized_), gemm_ws, gemm_bytes, s),
+                                            fp(*pf_->normalized), gemm_ws, gemm_bytes, s),
                     "prefill_into: FFN as library GEMMs"))) {
             // Post-attention RMSNorm, gate/up and SwiGLU.
             auto gate_up = [&](auto entry, float* scratch) {
@@ -647,13 +650,13 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                                                          scratch, gemm_ws, gemm_bytes, st);
             };
             if (!(ffn_same &&
-                  ((lib && fused(gate_up(gate_up_gemm_entry, fp(*pf_normalized_)), "prefill_into: gate/up as library GEMMs")) ||
-                   (mm && fused(gate_up(skv_fused_gate_up_swiglu_mm_f32, fp(*pf_normalized_)),
+                  ((lib && fused(gate_up(gate_up_gemm_entry, fp(*pf_->normalized)), "prefill_into: gate/up as library GEMMs")) ||
+                   (mm && fused(gate_up(skv_fused_gate_up_swiglu_mm_f32, fp(*pf_->normalized)),
                                 "prefill_into: gate/up on the matrix cores")) ||
-                   fused(gate_up(skv_fused_gate_up_swiglu_rows_f32, fp(*pf_normalized_)),
+                   fused(gate_up(skv_fused_gate_up_swiglu_rows_f32, fp(*pf_->normalized)),
                          "prefill_into: fused rmsnorm + gate/up + swiglu")))) {
-                float* hn = fp(*pf_normalized_);
-                float* up = fallback_buffer(pf_up_, static_cast<std::size_t>(inter));
+                float* hn = fp(*pf_->normalized);
+                float* up = fallback_buffer(pf_->up, static_cast<std::size_t>(inter));
                 detail::check(skv_rmsnorm_f32(h, hn, cfp(norm2_.gamma()), n, hidden, norm2_.epsilon(), s),
                               "prefill_into: post-attention rmsnorm");
                 linear(gate_proj_, hn, n, act, "prefill_into: gate_proj");
@@ -673,7 +676,7 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                                                      stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
                                                      bias_of(down_proj_), h, y, s),
                         "prefill_into: fused down_proj + residual"))) {
-                float* d = fallback_buffer(pf_down_, hidden_dim_);
+                float* d = fallback_buffer(pf_->down, hidden_dim_);
                 linear(down_proj_, act, n, d, "prefill_into: down_proj");
                 detail::check(skv_add_f32(h, d, n * hidden, s), "prefill_into: residual");
                 detail::check(skv_memcpy_d2d(y, h, static_cast<std::size_t>(n) * hidden * sizeof(float), s),
