@@ -247,9 +247,37 @@ void sampler_host_rules(bool device) {
 
 }  // namespace
 
+// Tensor::rows_view: rows [first, first + count) of a contiguous matrix share
+// its storage (values, writes through the view, the transpose view of a
+// block) and outlive the matrix's own handle; out-of-range blocks throw.
+void tensor_rows_view() {
+    using stratakv::DataType;
+    using stratakv::Device;
+    using stratakv::Tensor;
+    stratakv::Tensor view({1}, DataType::FP32, Device::CPU);
+    {
+        Tensor m({6, 4}, DataType::BF16, Device::CPU);
+        for (std::size_t i = 0; i < 24; ++i) m[i] = static_cast<float>(i);
+        view = m.rows_view(2, 3);
+        check(view.shape() == std::vector<std::size_t>({3, 4}) && view.num_elements() == 12, "rows_view shape");
+        check(view.raw_data() == static_cast<const char*>(m.raw_data()) + 2 * 4 * 2, "rows_view shares storage");
+        view[5] = 100.0f;
+        check(static_cast<float>(m[13]) == 100.0f, "a write through rows_view lands in the matrix");
+        const Tensor t = m.rows_view(4, 2).transpose_2d();
+        check(t.shape() == std::vector<std::size_t>({4, 2}) && t.value_at(1) == 20.0f, "transpose of a row block");
+        check(throws<std::invalid_argument>([&] { (void)m.rows_view(4, 3); }), "rows_view past the last row throws");
+        check(throws<std::invalid_argument>([&] { (void)m.rows_view(0, 0); }), "an empty rows_view throws");
+        check(throws<std::invalid_argument>([&] { (void)t.rows_view(0, 1); }), "rows_view of a transpose view throws");
+    }
+    bool same = true;
+    for (std::size_t i = 0; i < 12; ++i) same = same && view.value_at(i) == (i == 5 ? 100.0f : static_cast<float>(8 + i));
+    check(same, "rows_view keeps the storage alive after the matrix handle is gone");
+}
+
 int main() {
     const bool device = device_memory_available();
     try {
+        tensor_rows_view();
         sampler_host_rules(device);
         if (device) {
             device_batch_trace();
