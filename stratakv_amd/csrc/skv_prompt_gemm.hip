@@ -134,6 +134,9 @@ int check_workspace(const char* fn, void* ws, size_t bytes, int rows, int K, int
     return SKV_OK;
 }
 
+// Biases are read 4 at a time by the epilogues.
+bool bias_ok(const float* b) { return b == nullptr || aligned16(b); }
+
 // The common layout rules; SKV_ERR_UNSUPPORTED when a shape is not taken.
 bool layout_ok(const void* w, int weight_dtype, int64_t stride_k, int64_t stride_n, int K, int n) {
     return w != nullptr && weight_dtype == SKV_DTYPE_BF16 && stride_k == 1 && stride_n >= K &&
@@ -203,7 +206,8 @@ extern "C" int skv_fused_qkv_gemm_f32(const float* hidden, int rows, const float
     const bool rope = first_position >= 0;
     const void* w[3] = {wq, wk, wv};
     bool ok = K % 8 == 0 && K <= 8192 && (!rope || head_dim % 8 == 0) && aligned16(hidden) && aligned16(q) &&
-              aligned16(k) && aligned16(v) && (gamma == nullptr || aligned16(normalized));
+              aligned16(k) && aligned16(v) && (gamma == nullptr || aligned16(normalized)) && bias_ok(bias_q) &&
+              bias_ok(bias_k) && bias_ok(bias_v);
     for (int m = 0; m < 3 && ok; ++m) ok = layout_ok(w[m], weight_dtype, stride_k, stride_n[m], K, n[m]);
     if (!ok) return set_error(SKV_ERR_UNSUPPORTED, "%s: layout not taken by the library GEMMs", fn);
     Workspace ws = carve(workspace, rows, K, n[0] + n[1] + n[2]);
@@ -265,7 +269,7 @@ extern "C" int skv_fused_gate_up_swiglu_gemm_f32(const float* x, int rows, const
     const int K = in_dim;
     if (int rc = check_workspace(fn, workspace, workspace_bytes, rows, K, 2 * out_dim)) return rc;
     const bool ok = K % 8 == 0 && K <= 8192 && aligned16(x) && aligned16(act) &&
-                    (gamma == nullptr || aligned16(normalized)) &&
+                    (gamma == nullptr || aligned16(normalized)) && bias_ok(bias_gate) && bias_ok(bias_up) &&
                     layout_ok(w_gate, weight_dtype, stride_k, stride_n_gate, K, out_dim) &&
                     layout_ok(w_up, weight_dtype, stride_k, stride_n_up, K, out_dim);
     if (!ok) return set_error(SKV_ERR_UNSUPPORTED, "%s: layout not taken by the library GEMMs", fn);
@@ -300,7 +304,7 @@ extern "C" int skv_linear_residual_gemm_f32(const float* x, int rows, const void
     SKV_REQUIRE(x && residual && y && rows > 0 && in_dim > 0 && out_dim > 0, "%s: invalid pointers or sizes", fn);
     const int K = in_dim;
     if (int rc = check_workspace(fn, workspace, workspace_bytes, rows, K, out_dim)) return rc;
-    const bool ok = K % 8 == 0 && K <= 8192 && aligned16(x) && aligned16(residual) && aligned16(y) &&
+    const bool ok = K % 8 == 0 && K <= 8192 && aligned16(x) && aligned16(residual) && aligned16(y) && bias_ok(bias) &&
                     layout_ok(weight, weight_dtype, stride_k, stride_n, K, out_dim);
     if (!ok) return set_error(SKV_ERR_UNSUPPORTED, "%s: layout not taken by the library GEMMs", fn);
     Workspace ws = carve(workspace, rows, K, out_dim);
@@ -333,7 +337,8 @@ extern "C" int skv_ffn_swiglu_gemm_f32(const float* x, int rows, const float* ga
     const int kmax = std::max(H, I), outs = std::max(2 * I, H);
     if (int rc = check_workspace(fn, workspace, workspace_bytes, rows, kmax, outs)) return rc;
     const bool ok = H % 8 == 0 && H <= 8192 && I % 8 == 0 && I <= 8192 && aligned16(x) && aligned16(y) &&
-                    (gamma == nullptr || aligned16(normalized)) &&
+                    (gamma == nullptr || aligned16(normalized)) && bias_ok(bias_gate) && bias_ok(bias_up) &&
+                    bias_ok(bias_down) &&
                     layout_ok(w_gate, weight_dtype, stride_k, stride_n_gate, H, I) &&
                     layout_ok(w_up, weight_dtype, stride_k, stride_n_up, H, I) &&
                     layout_ok(w_down, weight_dtype, stride_k, stride_n_down, I, H);

@@ -154,7 +154,8 @@ def test_gemm_residual_in_place_and_repeated_calls(gpu):
 
 def test_gemm_projections_refuse_unsupported_shapes(gpu):
     """fp32 weights, in_dim not a multiple of 8, an output count not a multiple
-    of 8: SKV_ERR_UNSUPPORTED and nothing written."""
+    of 8, a bias not 16-byte aligned: SKV_ERR_UNSUPPORTED and nothing
+    written."""
     lib, D = gpu.lib(), gpu.DeviceBuffer
     y = D.from_numpy(np.full((3, 64), 7.0, np.float32))
     res = D.from_numpy(np.zeros((3, 64), np.float32))
@@ -167,6 +168,13 @@ def test_gemm_projections_refuse_unsupported_shapes(gpu):
         rc = lib.skv_linear_residual_gemm_f32(x.ptr, 3, w.ptr, dt, 1, K, K, out_dim, None, res.ptr, y.ptr, ws.ptr,
                                               wsb, None)
         assert rc == gpu.SKV_ERR_UNSUPPORTED, (K, out_dim, dt)
+    K, bias = 1024, D(4 * 65)
+    w, x = D(64 * K * 2), D.from_numpy(np.ones((3, K), np.float32))
+    wsb = lib.skv_prompt_gemm_workspace_bytes(3, K, 64)
+    ws = D(wsb)
+    rc = lib.skv_linear_residual_gemm_f32(x.ptr, 3, w.ptr, gpu.DTYPE_BF16, 1, K, K, 64, bias.ptr + 4, res.ptr, y.ptr,
+                                          ws.ptr, wsb, None)
+    assert rc == gpu.SKV_ERR_UNSUPPORTED
     gpu.synchronize()
     assert np.array_equal(y.download(np.float32, (3, 64)), np.full((3, 64), 7.0, np.float32))
 
