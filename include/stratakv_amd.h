@@ -440,9 +440,10 @@ int skv_linear_residual_mm_f32(const float* x, int rows, const void* weight, int
  * weights are bf16 aligned output-major rows with a 16-byte row stride, in_dim
  * is a multiple of 8 up to 8,192, every output count is a multiple of 8,
  * head_dim is a multiple of 8 when rotating, the input, outputs, biases and
- * residual are 16-byte aligned and hipBLASLt offers an algorithm for each GEMM.  The
- * first call of a shape on a device asks hipBLASLt for its algorithm (kept
- * for the process); calls on one workspace must not overlap.
+ * residual are 16-byte aligned and hipBLASLt offers an algorithm for each
+ * GEMM.  The first call of a shape on a device times hipBLASLt's best-ranked
+ * algorithms on its operands (the host waits for that) and keeps the fastest
+ * for the process; calls on one workspace must not overlap.
  * Replaces: the same reference code as the rows variants
  * (src/models/transformer_block.cpp:300-332); no counterpart of its own. */
 size_t skv_prompt_gemm_workspace_bytes(int rows, int in_dim, int outputs);

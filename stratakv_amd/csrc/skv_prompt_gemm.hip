@@ -22,6 +22,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -33,12 +34,18 @@ constexpr size_t kLibWorkspace = size_t{32} << 20;   // hipBLASLt's own scratch,
 
 size_t align256(size_t b) { return (b + 255) & ~size_t{255}; }
 
-// One GEMM shape's descriptors and the algorithm hipBLASLt ranks first for it.
+// One GEMM shape's descriptors and algorithm.  hipBLASLt's heuristic ranks
+// up to kCandidates algorithms; the first call of the shape times each of
+// them on its own operands and keeps the fastest (at the prompt pass's
+// shapes its first choice was up to 26 % slower than the best one).
+constexpr int kCandidates = 10;
 struct Plan {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
     hipblasLtMatmulAlgo_t algo{};
-    size_t workspace = 0;
+    hipblasLtMatmulAlgo_t candidates[kCandidates];
+    int ncandidates = 0;
+    std::atomic<bool> chosen{false};   // algo final (set under the lock, read without it)
     bool ok = false;
 };
 
@@ -56,7 +63,7 @@ std::map<int, DeviceState> g_devices;
 
 // The plan of an m x n x k GEMM with lda, or nullptr when hipBLASLt has none
 // (or cannot start on this device).
-const Plan* plan_for(int m, int n, int k, int64_t lda) {
+Plan* plan_for(int m, int n, int k, int64_t lda) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lock(g_mutex);
@@ -84,14 +91,17 @@ const Plan* plan_for(int m, int n, int k, int64_t lda) {
               hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
                                                     &kLibWorkspace, sizeof(kLibWorkspace)) == HIPBLAS_STATUS_SUCCESS;
     if (ok) {
-        hipblasLtMatmulHeuristicResult_t best{};
-        int found = 0;
-        ok = hipblasLtMatmulAlgoGetHeuristic(ds.handle, p.desc, p.a, p.b, p.c, p.c, pref, 1, &best, &found) ==
-                 HIPBLAS_STATUS_SUCCESS &&
-             found > 0 && best.workspaceSize <= kLibWorkspace;
+        hipblasLtMatmulHeuristicResult_t found[kCandidates];
+        int nfound = 0;
+        ok = hipblasLtMatmulAlgoGetHeuristic(ds.handle, p.desc, p.a, p.b, p.c, p.c, pref, kCandidates, found,
+                                             &nfound) == HIPBLAS_STATUS_SUCCESS;
+        for (int i = 0; ok && i < nfound; ++i)
+            if (found[i].state == HIPBLAS_STATUS_SUCCESS && found[i].workspaceSize <= kLibWorkspace)
+                p.candidates[p.ncandidates++] = found[i].algo;
+        ok = ok && p.ncandidates > 0;
         if (ok) {
-            p.algo = best.algo;
-            p.workspace = best.workspaceSize;
+            p.algo = p.candidates[0];
+            p.chosen = p.ncandidates == 1;
         }
     }
     if (pref != nullptr) hipblasLtMatmulPreferenceDestroy(pref);
@@ -106,7 +116,7 @@ struct Gemm {
     int64_t ld;
     int n;
     float* d;
-    const Plan* plan;
+    Plan* plan;
 };
 
 // Workspace: [2 rows][K] bf16 parts, then [2 rows][outputs] fp32 GEMM
@@ -157,6 +167,42 @@ bool plan_all(Gemm* g, int count, int rows, int K) {
     return true;
 }
 
+// The first call of a shape: each candidate once to warm up, then twice
+// timed with events on the call's stream (the host waits for them), on the
+// call's own operands; the GEMM has beta = 0, so the runs only overwrite its
+// output, which the chosen algorithm then writes once more.  Under the lock,
+// so a shape is timed once per device.
+void choose_algorithm(hipblasLtHandle_t handle, Plan& p, const Gemm& g, const uint16_t* parts, void* lib,
+                      hipStream_t s) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (p.chosen) return;
+    const float alpha = 1.0f, beta = 0.0f;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float best = 0.0f;
+    int best_i = 0;
+    if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
+        for (int i = 0; i < p.ncandidates; ++i) {
+            auto run = [&] {
+                return hipblasLtMatmul(handle, p.desc, &alpha, g.w, p.a, parts, p.b, &beta, g.d, p.c, g.d, p.c,
+                                       &p.candidates[i], lib, kLibWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
+            };
+            float ms = 0.0f;
+            const bool ok = run() && hipEventRecord(e0, s) == hipSuccess && run() && run() &&
+                            hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+                            hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+            if (ok && (i == 0 || ms < best)) {
+                best = ms;
+                best_i = i;
+            }
+        }
+    }
+    if (e0 != nullptr) (void)hipEventDestroy(e0);
+    if (e1 != nullptr) (void)hipEventDestroy(e1);
+    (void)hipGetLastError();   // a candidate that failed to launch is not the call's error
+    p.algo = p.candidates[best_i];
+    p.chosen = true;
+}
+
 int run_gemms(const char* fn, const Gemm* g, int count, const uint16_t* parts, void* lib, hipStream_t s) {
     const float alpha = 1.0f, beta = 0.0f;
     int dev = 0;
@@ -167,7 +213,8 @@ int run_gemms(const char* fn, const Gemm* g, int count, const uint16_t* parts, v
         handle = g_devices[dev].handle;
     }
     for (int i = 0; i < count; ++i) {
-        const Plan& p = *g[i].plan;
+        Plan& p = *g[i].plan;
+        if (!p.chosen) choose_algorithm(handle, p, g[i], parts, lib, s);
         const hipblasStatus_t st = hipblasLtMatmul(handle, p.desc, &alpha, g[i].w, p.a, parts, p.b, &beta, g[i].d,
                                                    p.c, g[i].d, p.c, &p.algo, lib, kLibWorkspace, s);
         if (st != HIPBLAS_STATUS_SUCCESS) return set_error(SKV_ERR_HIP, "%s: hipblasLtMatmul failed (%d)", fn, st);
