@@ -44,6 +44,9 @@ sys.path.insert(0, ROOT)
 
 METRIC = "paged decode-attn achieved HBM GB/s (% of peak) + decode tokens/sec, 1 GPU"
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD public specification
+# Table sets cycled through by the timed steps of configs whose step reads less
+# than a few times the 256 MB last-level cache (cfg3: 8 x 285 MB).
+CACHE_ROTATION = 8
 
 
 def log(msg: str) -> None:
@@ -76,8 +79,13 @@ def workload(cfg: int):
         perm = rng.permutation(total).astype(np.int32)
         nb = -(-4097 // bs)
         tables = perm[:nb].reshape(1, nb)
+        # Timed steps cycle through disjoint tables (consecutive 257-id slices of
+        # the same permutation), so no step re-reads what the step before left
+        # in the 256 MB last-level cache.
+        rotation = [perm[i * nb:(i + 1) * nb].reshape(1, nb) for i in range(total // nb)]
         desc = ("cfg2: batch 1, 32 Q / 4 KV heads, head_dim 64, context 4097 (4096 + 1 appended), "
-                "table = first 257 ids of a seeded permutation of a 65536-block pool")
+                "table = first 257 ids of a seeded permutation of a 65536-block pool; timed steps "
+                "cycle through the permutation's 255 disjoint 257-id tables")
     elif cfg == 3:
         rng = np.random.default_rng(0x5EED0003)
         Hq, Hkv, hd, B = 32, 4, 64, 64
@@ -85,13 +93,18 @@ def workload(cfg: int):
         total = 1 << 20
         perm = rng.permutation(total).astype(np.int32)
         nbs = [-(-int(L) // bs) for L in lens]
-        tables = np.full((B, max(nbs)), -1, np.int32)
+        rotation = []
         pos = 0
-        for b, nb in enumerate(nbs):
-            tables[b, :nb] = perm[pos:pos + nb]
-            pos += nb
+        for _ in range(CACHE_ROTATION):
+            t = np.full((B, max(nbs)), -1, np.int32)
+            for b, nb in enumerate(nbs):
+                t[b, :nb] = perm[pos:pos + nb]
+                pos += nb
+            rotation.append(t)
+        tables = rotation[0]
         desc = ("cfg3: batch 64, TinyLlama geometry (32 Q / 4 KV heads, head_dim 64), contexts "
-                "U[512, 8192], tables = consecutive slices of a seeded permutation of a 2^20-block pool")
+                "U[512, 8192], tables = consecutive slices of a seeded permutation of a 2^20-block pool; "
+                f"timed steps cycle through {CACHE_ROTATION} disjoint table sets (the next slices)")
     elif cfg == 4:
         rng = np.random.default_rng(0x5EED0004)
         Hq, Hkv, hd, B = 32, 8, 128, 128
@@ -107,8 +120,11 @@ def workload(cfg: int):
         return churn_workload()
     else:
         raise SystemExit(f"bench.py: unknown --config {cfg} (configs: 1, 2, 3, 4, 5)")
-    return dict(cfg=cfg, Hq=Hq, Hkv=Hkv, hd=hd, B=B, bs=bs, lens=lens, tables=tables,
-                total=int(total), desc=desc, seed=0x5EED0000 + cfg)
+    w = dict(cfg=cfg, Hq=Hq, Hkv=Hkv, hd=hd, B=B, bs=bs, lens=lens, tables=tables,
+             total=int(total), desc=desc, seed=0x5EED0000 + cfg)
+    if cfg in (2, 3):
+        w["rotation"] = rotation
+    return w
 
 
 def contiguous_tables(w):
@@ -122,8 +138,10 @@ def contiguous_tables(w):
     for b, nb in enumerate(nbs):
         tables[b, :nb] = np.arange(pos, pos + nb, dtype=np.int32)
         pos += nb
-    return dict(w, tables=tables, total=int(pos),
-                desc=w["desc"] + "; tables replaced by consecutive ids in a pool of the blocks used")
+    w = dict(w, tables=tables, total=int(pos),
+             desc=w["desc"] + "; tables replaced by consecutive ids in a pool of the blocks used")
+    w.pop("rotation", None)
+    return w
 
 
 class LifoPool:
@@ -232,6 +250,13 @@ def setup_gpu(w):
     skv.fill_normal_bf16(d["k_new"], B * Hkv * hd, w["seed"] + 3, 0, h)
     skv.fill_normal_bf16(d["v_new"], B * Hkv * hd, w["seed"] + 4, 0, h)
     d["tables"] = skv.DeviceBuffer.from_numpy(w["tables"])
+    # Per-step tables: the rotation's table sets one after another in one buffer.
+    rot = w.get("rotation")
+    if rot is not None:
+        d["rot_buf"] = skv.DeviceBuffer.from_numpy(np.ascontiguousarray(np.stack(rot)))
+        d["rot_ptrs"] = [d["rot_buf"].ptr + i * rot[0].nbytes for i in range(len(rot))]
+    else:
+        d["rot_ptrs"] = [d["tables"].ptr]
     d["lens"] = skv.DeviceBuffer.from_numpy(w["lens"])
     d["positions"] = skv.DeviceBuffer.from_numpy(w["lens"] - 1)
     d["out"] = skv.DeviceBuffer(B * Hq * hd * 4)
@@ -282,16 +307,22 @@ def run_gpu(w, steps: int, warmup: int, fused: bool = True):
                           tables.ptr + CHURN_LONG * max_blocks * 4, max_blocks, zero_pos,
                           CHURN_NEW, CHURN_CHUNK, Hkv, hd, bs, stream=stream.handle)
         if not fused:
-            skv.kv_append(k_new, v_new, skv.DTYPE_BF16, k_pool, v_pool, total, tables, max_blocks,
+            t = rot_ptrs[main_counter[0] % len(rot_ptrs)]
+            skv.kv_append(k_new, v_new, skv.DTYPE_BF16, k_pool, v_pool, total, t, max_blocks,
                           positions, B, 1, Hkv, hd, bs, stream=stream.handle)
 
+    rot_ptrs = d["rot_ptrs"]
+    main_counter = [0]
+
     def main():
+        t = rot_ptrs[main_counter[0] % len(rot_ptrs)]
+        main_counter[0] += 1
         if fused:
             skv.paged_decode_append(q, skv.DTYPE_BF16, k_new, v_new, skv.DTYPE_BF16, k_pool, v_pool,
-                                    total, tables, max_blocks, lens, B, Hq, Hkv, hd, bs, scale, out,
+                                    total, t, max_blocks, lens, B, Hq, Hkv, hd, bs, scale, out,
                                     ws, wsb, stream=stream.handle)
         else:
-            skv.paged_decode(q, skv.DTYPE_BF16, k_pool, v_pool, total, tables, max_blocks, lens, B,
+            skv.paged_decode(q, skv.DTYPE_BF16, k_pool, v_pool, total, t, max_blocks, lens, B,
                              Hq, Hkv, hd, bs, scale, out, ws, wsb, stream=stream.handle)
 
     for _ in range(warmup):
@@ -407,39 +438,94 @@ def run_load_calibration(w, steps: int, warmup: int, rounds: int = 5):
 # ---------------------------------------------------------------------------
 # CPU baseline: the oracle (restatement of src/layers/attention.cpp:263-337)
 # ---------------------------------------------------------------------------
+def host_cpu():
+    """(logical CPUs of the host, CPUs this process may run on, CPU model)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return os.cpu_count() or 1, usable, model
+
+
+def cpu_threads_all() -> int:
+    """Threads for the all-cores leg: every CPU this process may run on, but
+    no more than OMP_NUM_THREADS when that is set (the GPU boxes set it to the
+    CPU share of one GPU, which is smaller than what the host reports)."""
+    _, usable, _ = host_cpu()
+    try:
+        cap = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        cap = 0
+    return max(1, min(usable, cap) if cap > 0 else usable)
+
+
+def cpu_sample_tables(w, chosen):
+    """The chosen sequences' rows of the config's own tables, with the block ids
+    renumbered by rank into a pool of just the blocks they use: the blocks
+    keep the order and interleaving they have in the config's pool (cfg4's
+    round-robin placement, cfg3's shuffled slices) without allocating the
+    config's whole pool on the host."""
+    rows = w["tables"][chosen]
+    nbs = [-(-int(L) // w["bs"]) for L in w["lens"][chosen]]
+    used = np.concatenate([rows[i, :nb] for i, nb in enumerate(nbs)])
+    order = np.unique(used)
+    tables = np.full((len(chosen), max(nbs)), -1, np.int32)
+    for i, nb in enumerate(nbs):
+        tables[i, :nb] = np.searchsorted(order, rows[i, :nb])
+    return tables, len(order)
+
+
 def cpu_baseline(w, budget_s: float = 12.0):
+    """The oracle's fp32 decode loops (restatement of
+    src/layers/attention.cpp:263-337) on this host over a seeded sample of the
+    config's sequences sized to about `budget_s` seconds on one thread, then
+    the same sample on every usable core."""
     import oracle
 
     rng = np.random.default_rng(w["seed"] + 99)
     B, Hq, Hkv, hd, bs = w["B"], w["Hq"], w["Hkv"], w["hd"], w["bs"]
     order = rng.permutation(B)
-    # Estimate: the scalar loop runs ~0.16 GMAC/s on one core at head_dim 128;
-    # take sequences until ~budget_s/2 of single-thread work.
-    macs_budget = 0.16e9 * budget_s / 2
+    # Values do not change the loop's time: tile a 4 Mi-element random bf16 block.
+    base = oracle.f32_to_bf16(rng.standard_normal(1 << 22, dtype=np.float32))
+    scale = 1.0 / math.sqrt(hd)
+
+    def sample(chosen):
+        chosen = sorted(chosen)
+        tables, tot = cpu_sample_tables(w, chosen)
+        kp = np.resize(base, (tot, bs, Hkv, hd))
+        vp = np.resize(base[::-1], (tot, bs, Hkv, hd))
+        q = oracle.bf16_to_f32(np.resize(base[1::2], (len(chosen), Hq, hd)))
+        return chosen, tables, tot, kp, vp, q
+
+    # The host's rate: one sequence on one thread (multiply-adds of q.k and P.V
+    # per key, query head and dimension per second); then take sequences up to
+    # ~budget_s of single-thread work.
+    _, tb, _, kp, vp, q = sample([int(order[0])])
+    t0 = time.perf_counter()
+    oracle.paged_decode(q, kp, vp, tb, w["lens"][[int(order[0])]].astype(np.int32), Hkv, bs, scale, threads=1)
+    rate = int(w["lens"][order[0]]) * Hq * hd * 2 / max(time.perf_counter() - t0, 1e-6)
     chosen, macs = [], 0
     for b in order:
         chosen.append(int(b))
         macs += int(w["lens"][b]) * Hq * hd * 2
-        if macs >= macs_budget:
+        if macs >= rate * budget_s:
             break
+    chosen, tables, tot, kp, vp, q = sample(chosen)
     lens = w["lens"][chosen].astype(np.int32)
-    nbs = [-(-int(L) // bs) for L in lens]
-    tot = sum(nbs)
-    tables = np.full((len(chosen), max(nbs)), -1, np.int32)
-    pos = 0
-    for i, nb in enumerate(nbs):
-        tables[i, :nb] = np.arange(pos, pos + nb)
-        pos += nb
-    # Values do not change the loop's time: tile a 4 Mi-element random bf16 block.
-    base = oracle.f32_to_bf16(rng.standard_normal(1 << 22, dtype=np.float32))
-    kp = np.resize(base, (tot, bs, Hkv, hd))
-    vp = np.resize(base[::-1], (tot, bs, Hkv, hd))
-    q = oracle.bf16_to_f32(oracle.f32_to_bf16(rng.standard_normal((len(chosen), Hq, hd), dtype=np.float32)))
-    scale = 1.0 / math.sqrt(hd)
     sample_bytes = int((2 * lens.astype(np.int64) * Hkv * hd * 2).sum())
+    nproc, usable, model = host_cpu()
     results = {}
-    threads_all = min(os.cpu_count() or 1, 16)
-    for threads in (1, threads_all):
+    threads_all = cpu_threads_all()
+    for threads in sorted({1, threads_all}):
         t0 = time.perf_counter()
         oracle.paged_decode(q, kp, vp, tables, lens, Hkv, bs, scale, threads=threads)
         dt = time.perf_counter() - t0
@@ -450,14 +536,17 @@ def cpu_baseline(w, budget_s: float = 12.0):
     for threads, dt in results.items():
         gbs = sample_bytes / dt / 1e9
         out[threads] = dict(value=round(gbs, 4), unit="GB/s", cores=threads, kind="port",
+                            nproc=nproc, cpus_usable=usable, cpu_model=model,
                             tokens_per_s=round(B / (full_kv / (gbs * 1e9)), 6),
                             sample=(f"oracle two-pass fp32 attention (restatement of "
                                     f"src/layers/attention.cpp:263-337, gcc -O3 -mavx2 -mfma) over "
                                     f"{len(chosen)} of {B} sequences ({int(lens.sum())} tokens, "
-                                    f"{sample_bytes / 1e6:.1f} MB of bf16 K/V) in {dt:.2f} s; "
-                                    f"GB/s on the same algorithmic bytes, tokens/s scaled by bytes "
-                                    f"to the full batch; the reference itself caches FP32, so its "
-                                    f"real traffic is twice these bytes"))
+                                    f"{sample_bytes / 1e6:.1f} MB of bf16 K/V) through their rows of "
+                                    f"the config's own block tables (ids renumbered by rank into a "
+                                    f"pool of the {tot} blocks they use) in {dt:.2f} s on {threads} "
+                                    f"thread(s); GB/s on the same algorithmic bytes, tokens/s scaled "
+                                    f"by bytes to the full batch; the reference itself caches FP32, "
+                                    f"so its real traffic is twice these bytes"))
     return out[1], out[threads_all]
 
 
@@ -904,7 +993,14 @@ def main() -> int:
     step_s = g["ms_per_step"] / 1e3
     value = (dec_bytes + tok_bytes + churn_bytes) / step_s / 1e9
     main_bytes = dec_bytes + (tok_bytes if fused else 0)
-    achieved = main_bytes / (g["main_ms"] / 1e3) / 1e9
+    # The roofline's time: the timed region's own time per step when the step
+    # is the decode call alone (fused append + decode, configs 2-4); with work
+    # before the call (cfg5's churn, or --separate) the call's mean time from
+    # the second, per-step-event pass.
+    call_only = fused and "churn" not in w
+    roof_s = step_s if call_only else g["main_ms"] / 1e3
+    achieved = main_bytes / roof_s / 1e9
+    per_call = main_bytes / (g["main_ms"] / 1e3) / 1e9
     key = f"cfg{args.config}" + ("" if fused else "_separate")
     traffic = profile_traffic(key)
     line = {
@@ -947,6 +1043,9 @@ def main() -> int:
             "traffic": traffic,
             "algorithmic_bytes": main_bytes,
             "flops": flops,
+            "time_source": ("timed region, ms_per_step" if call_only else
+                            "mean decode-call time of a second pass with events around each call"),
+            "achieved_per_call_events": round(per_call, 2),
         },
     }
     if not args.no_cpu_baseline:

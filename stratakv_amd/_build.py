@@ -112,19 +112,13 @@ def build_cpp_tests() -> list[str]:
 
 def build_bench() -> list[str]:
     """Compile the C++ benchmark drivers (stratakv_amd/csrc/bench/*.cpp) into
-    build/bin/bench_<name>; they use only the library's public headers.  The
-    stand-alone kernel benchmarks (bench/*.hip: memory-access patterns of the
-    library's kernels, no library code) are built with hipcc for gfx950."""
+    build/bin/bench_<name>; they use only the library's public headers."""
     os.makedirs(BIN, exist_ok=True)
     outs, cmds = [], []
     for src in sorted(glob.glob(os.path.join(CSRC, "bench", "*.cpp"))):
         exe = os.path.join(BIN, "bench_" + os.path.splitext(os.path.basename(src))[0])
         cmds.append([CXX, "-O2", "-std=c++17", "-Wall", f"-I{INCLUDE}", src, f"-L{PKG}", "-lstratakv_amd",
                      f"-Wl,-rpath,{PKG}", "-o", exe])
-        outs.append(exe)
-    for src in sorted(glob.glob(os.path.join(CSRC, "bench", "*.hip"))):
-        exe = os.path.join(BIN, "bench_" + os.path.splitext(os.path.basename(src))[0])
-        cmds.append([HIPCC, *HIP_FLAGS, src, "-o", exe])
         outs.append(exe)
     _run_all(cmds)
     return outs

@@ -79,8 +79,6 @@ def test_fp32_rounding_edge_patterns(gpu):
     gk, gv, rk, rv = _run(gpu, k_new, v_new, 4, bs, Hkv, hd, tables, [17, 5], 1)
     _bits_equal(gk, rk, "K")
     _bits_equal(gv, rv, "V")
-    if oracle.ref_available():  # cross-check the oracle rule with the reference itself
-        np.testing.assert_array_equal(oracle.f32_to_bf16(row), oracle.ref_bf16_rne(row))
 
 
 def test_chunk_append_prefill_blocks(gpu):
