@@ -690,9 +690,15 @@ def run_cfg1(steps: int, warmup: int, with_cpu: bool):
             ms = g["prefill_and_first_token_ms"]
             line["prompt_2048"] = {
                 "ms": ms, "prompt_tokens_per_s": round(2048 / (ms / 1e3), 1),
+                "first_call_ms": g.get("first_call_ms"),
+                "unseen_2047_first_ms": g.get("unseen_length_first_ms"),
+                "unseen_2047_second_ms": g.get("unseen_length_second_ms"),
                 "note": ("Generator::generate(prompt of 2,048 ids, 1 new token): embedding, prefill_into of 22 "
                          "TinyLlama-shaped layers (q/k/v, o, gate/up, down as hipBLASLt bf16 GEMMs over the inputs "
-                         "split into bf16 hi + lo, causal prefill attention), lm_head and the first greedy token")}
+                         "split into bf16 hi + lo, causal prefill attention), lm_head and the first greedy token; "
+                         "first_call_ms: the process's first such call (opens the GEMM library, creates the "
+                         "hipBLASLt handle, asks its heuristic for each shape); unseen_2047_*: a 2,047-token "
+                         "prompt never run before, its first call (new GEMM shapes) and its second")}
         else:
             log(f"long-prompt driver failed ({proc.returncode}): {proc.stderr.strip()[-300:]}")
     if with_cpu:

@@ -67,7 +67,9 @@ public:
     // fewer than kPrefillMmRows tokens give every projection row the bits
     // forward_into gives for that token; longer ones (bf16 weights) run the
     // projections on the matrix cores (from kPrefillGemmRows tokens as
-    // hipBLASLt GEMMs), equal to fp32 rounding.  The attention
+    // hipBLASLt GEMMs): their inputs keep ~16 significant bits (hi + lo bf16
+    // parts, a relative error up to ~2^-16 each), so those rows agree with
+    // forward_into within that bound, not bit for bit.  The attention
     // of the chunk runs the prefill kernel instead of the decode kernel.
     void prefill_into(const Tensor& hidden_states, Tensor& output, int seq_id,
                       memory::PageTable& page_table, memory::BlockPool& block_pool);
@@ -77,12 +79,15 @@ public:
     // projections and the attention large grids.
     static constexpr int kPrefillChunk = 2048;
     static constexpr int kPrefillMinChunk = 256;
-    static constexpr std::size_t kPrefillScratchBudget = std::size_t{1} << 30;  // bytes of fp32 rows per scratch
+    // Bytes of prefill scratch: the fp32 rows of a chunk plus the library
+    // GEMMs' workspace for the projections they take.
+    static constexpr std::size_t kPrefillScratchBudget = std::size_t{1} << 30;
     int prefill_chunk_rows() const noexcept;
     // Chunk length from which the projections run on the matrix cores.
     static constexpr int kPrefillMmRows = 32;
     // Chunk length from which the projections run as hipBLASLt GEMMs
-    // (skv_*_gemm_f32), equal to the matrix-core kernels to fp32 rounding.
+    // (skv_*_gemm_f32, libstratakv_amd_gemm.so, when it can be opened): the
+    // same hi + lo split as the matrix-core kernels, different summation order.
     static constexpr int kPrefillGemmRows = 256;
     // prefill_into's scratch: the chunk's q, k, v, context, residual,
     // activation and normalised rows, its metadata and the library GEMMs'
@@ -172,6 +177,15 @@ private:
     std::shared_ptr<PrefillScratch> pf_;
     // The shared workspace grown to at least `bytes`; its 256-byte aligned start.
     void* prefill_gemm_workspace(std::size_t bytes);
+    // Which projections of a chunk of `rows` tokens go to the library GEMMs
+    // (libstratakv_amd_gemm.so opened, rows >= kPrefillGemmRows, and the
+    // layout rules the entry points check on the weights: bf16, in_dim a
+    // multiple of 8 up to 8,192), and the workspace those take.
+    struct PrefillGemmUse {
+        bool qkv = false, o = false, ffn = false, gate_up = false, down = false;
+        std::size_t bytes = 0;
+    };
+    PrefillGemmUse prefill_gemm_use(int rows) const noexcept;
 };
 
 }  // namespace models

@@ -398,8 +398,9 @@ int skv_linear_residual_rows_f32(const float* x, int rows, const void* weight, i
  * (rows * in_dim floats, as in the rows variants).  Each input value v is
  * split into bf16 parts hi = bf16(v) and lo = bf16(v - hi), and each output
  * is W hi + W lo with fp32 accumulation: every product is exact and v keeps
- * ~16 significant bits, so the results agree with the one-token entry points
- * to fp32 rounding but are not bit-identical to them.  RoPE, bias, SwiGLU
+ * ~16 significant bits (the lo part is itself rounded to bf16: a relative
+ * error up to ~2^-16 per input, against fp32's 2^-24), so the results agree
+ * with the one-token entry points within that bound, not bit for bit.  RoPE, bias, SwiGLU
  * and the residual are applied as in the rows variants (y may alias
  * residual).  SKV_ERR_UNSUPPORTED (nothing launched) unless the weights are
  * bf16 aligned output-major rows, in_dim is a multiple of 128 from 512 to
@@ -425,64 +426,10 @@ int skv_linear_residual_mm_f32(const float* x, int rows, const void* weight, int
                                const float* bias, const float* residual, float* y,
                                void* stream);
 
-/* The same three projections as the *_mm variants with the products on
- * hipBLASLt (bf16 x bf16 GEMMs, fp32 accumulation), for long prompts.  A
- * prologue kernel normalises the rows (with gamma, into `normalized`, the bits
- * of skv_rmsnorm_f32) and splits every input value v into hi = bf16(v) and
- * lo = bf16(v - hi), stacked as 2 * rows GEMM columns; one GEMM per weight
- * matrix computes W hi and W lo; an epilogue kernel adds the two halves and
- * applies bias, RoPE, SwiGLU or the residual as the *_mm variants do (y may
- * alias residual).  Results equal the *_mm variants' to fp32 rounding.
- * `workspace` (256-byte aligned) holds the split inputs, the GEMM outputs and
- * the library's own scratch: at least skv_prompt_gemm_workspace_bytes(rows,
- * in_dim, outputs per token: q + k + v, gate + up, or out_dim) bytes, else
- * SKV_ERR_INVALID_ARGUMENT.  SKV_ERR_UNSUPPORTED (nothing launched) unless the
- * weights are bf16 aligned output-major rows with a 16-byte row stride, in_dim
- * is a multiple of 8 up to 8,192, every output count is a multiple of 8,
- * head_dim is a multiple of 8 when rotating, the input, outputs, biases and
- * residual are 16-byte aligned and hipBLASLt offers an algorithm for each
- * GEMM.  The first call of a shape on a device times hipBLASLt's best-ranked
- * algorithms on its operands (the host waits for that) and keeps the fastest
- * for the process; calls on one workspace must not overlap.
- * Replaces: the same reference code as the rows variants
- * (src/models/transformer_block.cpp:300-332); no counterpart of its own. */
-size_t skv_prompt_gemm_workspace_bytes(int rows, int in_dim, int outputs);
-int skv_fused_qkv_gemm_f32(const float* hidden, int rows, const float* gamma, float epsilon,
-                           const void* wq, const void* wk, const void* wv, int weight_dtype,
-                           int64_t stride_k, const int64_t stride_n[3], const float* bias_q,
-                           const float* bias_k, const float* bias_v, int hidden_dim,
-                           int num_heads, int num_kv_heads, int head_dim, int first_position,
-                           float* q, float* k, float* v, float* normalized, void* workspace,
-                           size_t workspace_bytes, void* stream);
-int skv_fused_gate_up_swiglu_gemm_f32(const float* x, int rows, const float* gamma, float epsilon,
-                                      const void* w_gate, const void* w_up, int weight_dtype,
-                                      int64_t stride_k, int64_t stride_n_gate,
-                                      int64_t stride_n_up, const float* bias_gate,
-                                      const float* bias_up, int in_dim, int out_dim,
-                                      float* act, float* normalized, void* workspace,
-                                      size_t workspace_bytes, void* stream);
-int skv_linear_residual_gemm_f32(const float* x, int rows, const void* weight, int weight_dtype,
-                                 int64_t stride_k, int64_t stride_n, int in_dim, int out_dim,
-                                 const float* bias, const float* residual, float* y,
-                                 void* workspace, size_t workspace_bytes, void* stream);
-/* The whole feed-forward half of the layer on the library GEMMs:
- * y = x + down(swiglu(gate(n), up(n))) with n = rmsnorm(x, gamma) (written to
- * `normalized`) and the projections' biases; y may alias x.  The SwiGLU
- * epilogue writes the activations straight as the bf16 hi / lo operand of
- * down_proj (no fp32 activation rows): the arithmetic of
- * skv_fused_gate_up_swiglu_gemm_f32 followed by skv_linear_residual_gemm_f32
- * (residual x), equal to it to fp32 rounding (hipBLASLt's kernels for skinny
- * shapes may split K and add the parts in any order).  Workspace: skv_prompt_gemm_workspace_bytes(rows,
- * max(hidden_dim, inter_dim), max(2 * inter_dim, hidden_dim)).  The same
- * SKV_ERR_UNSUPPORTED rules as the separate calls.
- * Replaces: src/models/transformer_block.cpp:310-332 (post-attention norm,
- * gate/up, SwiGLU, down_proj and the residual); no counterpart of its own. */
-int skv_ffn_swiglu_gemm_f32(const float* x, int rows, const float* gamma, float epsilon,
-                            const void* w_gate, const void* w_up, const void* w_down, int weight_dtype,
-                            int64_t stride_k, int64_t stride_n_gate, int64_t stride_n_up,
-                            int64_t stride_n_down, const float* bias_gate, const float* bias_up,
-                            const float* bias_down, int hidden_dim, int inter_dim, float* y,
-                            float* normalized, void* workspace, size_t workspace_bytes, void* stream);
+/* The same projections with their products as hipBLASLt GEMMs, for long
+ * prompts (skv_*_gemm_f32), are declared in stratakv_amd_gemm.h and exported
+ * by libstratakv_amd_gemm.so, the only library of this build that links
+ * hipBLASLt. */
 
 /* ---- model boundary: checkpoint tensors, embedding, token choice --------
  * Checkpoint decode on the device (the host only moves file bytes).  src holds

@@ -18,6 +18,8 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libstratakv_amd.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "stratakv_amd.h")
+GEMM_LIB_PATH = os.path.join(_HERE, "libstratakv_amd_gemm.so")
+GEMM_HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "stratakv_amd_gemm.h")
 
 SKV_OK = 0
 SKV_ERR_INVALID_ARGUMENT = 1
@@ -134,16 +136,6 @@ _PROTOS = {
                                                _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
     "skv_linear_residual_mm_f32": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp,
                                           _vp, _vp]),
-    "skv_prompt_gemm_workspace_bytes": (_sz, [_i32, _i32, _i32]),
-    "skv_fused_qkv_gemm_f32": (_i32, [_vp, _i32, _vp, _f32, _vp, _vp, _vp, _i32, _i64,
-                                      _c.POINTER(_c.c_int64), _vp, _vp, _vp, _i32, _i32, _i32, _i32,
-                                      _i32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
-    "skv_fused_gate_up_swiglu_gemm_f32": (_i32, [_vp, _i32, _vp, _f32, _vp, _vp, _i32, _i64, _i64,
-                                                 _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
-    "skv_linear_residual_gemm_f32": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp,
-                                            _vp, _vp, _sz, _vp]),
-    "skv_ffn_swiglu_gemm_f32": (_i32, [_vp, _i32, _vp, _f32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64,
-                                       _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "skv_rope_rows_f32": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
     "skv_write_i32": (_i32, [_vp, _c.POINTER(_c.c_int32), _i32, _vp]),
     "skv_convert_to_bf16": (_i32, [_vp, _i32, _sz, _vp, _vp, _vp]),
@@ -157,7 +149,23 @@ _PROTOS = {
     "skv_sample_f32": (_i32, [_vp, _i32, _f32, _i32, _f32, _c.c_double, _vp, _i32, _vp, _vp]),
 }
 
+# libstratakv_amd_gemm.so (include/stratakv_amd_gemm.h): the hipBLASLt
+# projections of long prompt chunks, the only library linking hipBLASLt.
+_GEMM_PROTOS = {
+    "skv_prompt_gemm_workspace_bytes": (_sz, [_i32, _i32, _i32]),
+    "skv_fused_qkv_gemm_f32": (_i32, [_vp, _i32, _vp, _f32, _vp, _vp, _vp, _i32, _i64,
+                                      _c.POINTER(_c.c_int64), _vp, _vp, _vp, _i32, _i32, _i32, _i32,
+                                      _i32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "skv_fused_gate_up_swiglu_gemm_f32": (_i32, [_vp, _i32, _vp, _f32, _vp, _vp, _i32, _i64, _i64,
+                                                 _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "skv_linear_residual_gemm_f32": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp,
+                                            _vp, _vp, _sz, _vp]),
+    "skv_ffn_swiglu_gemm_f32": (_i32, [_vp, _i32, _vp, _f32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64,
+                                       _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
+}
+
 _lib = None
+_gemm_lib = None
 
 
 def header_symbols(path: str = HEADER_PATH) -> list[str]:
@@ -180,6 +188,24 @@ def lib() -> ctypes.CDLL:
             fn.argtypes = args
         _lib = handle
     return _lib
+
+
+def gemm_lib() -> ctypes.CDLL:
+    """Load libstratakv_amd_gemm.so (after libstratakv_amd.so, which it
+    depends on and which holds skv_last_error; raises if either is missing)."""
+    global _gemm_lib
+    if _gemm_lib is None:
+        lib()
+        path = os.path.join(os.path.dirname(LIB_PATH), os.path.basename(GEMM_LIB_PATH))
+        if not os.path.exists(path):
+            raise ImportError(f"{path} is missing: run __graft_entry__.build() first")
+        handle = ctypes.CDLL(path)
+        for name, (res, args) in _GEMM_PROTOS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _gemm_lib = handle
+    return _gemm_lib
 
 
 def _check(rc: int) -> None:

@@ -5,6 +5,9 @@ Everything is compiled in-tree so the built files travel with the source tree:
 * ``stratakv_amd/libstratakv_amd.so`` -- the gfx950 HIP kernels, the C ABI
   (``include/stratakv_amd.h``) and the C++17 host layer (``include/stratakv/``),
   built with ``hipcc --offload-arch=gfx950``.
+* ``stratakv_amd/libstratakv_amd_gemm.so`` -- the hipBLASLt projections of long
+  prompt chunks (``include/stratakv_amd_gemm.h``), the only library that links
+  hipBLASLt; it links the one above, whose host layer opens it on demand.
 * ``build/bin/test_*`` -- the C++ test programs under ``tests/cpp``;
   ``build/bin/bench_*`` -- the C++ benchmark drivers under ``stratakv_amd/csrc/bench``.
 * ``oracle/liboracle.so`` and, when the StrataKV sources are present,
@@ -26,6 +29,7 @@ PKG = os.path.join(ROOT, "stratakv_amd")
 CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(PKG, "libstratakv_amd.so")
+GEMM_LIB = os.path.join(PKG, "libstratakv_amd_gemm.so")
 BIN = os.path.join(ROOT, "build", "bin")
 ORACLE = os.path.join(ROOT, "oracle")
 REFERENCE = os.environ.get("STRATAKV_REFERENCE", "/root/reference")
@@ -87,10 +91,17 @@ def build_library() -> str:
         extra = FILE_FLAGS.get(os.path.basename(src), [])
         cmds.append([HIPCC, *HIP_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj])
         objs.append(obj)
+    gemm_src = os.path.join(CSRC, "gemm", "skv_prompt_gemm.hip")
+    gemm_obj = os.path.join(OBJ, "gemm_" + os.path.basename(gemm_src) + ".o")
+    cmds.append([HIPCC, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", gemm_src, "-o", gemm_obj])
     _run_all(cmds)
-    # hipBLASLt: the GEMMs of the prompt-pass projections (skv_prompt_gemm.hip).
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", *objs, "-lhipblaslt", "-o", LIB + ".tmp"])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", *objs, "-Wl,-soname,libstratakv_amd.so", "-o", LIB + ".tmp"])
     os.replace(LIB + ".tmp", LIB)
+    # The prompt-pass GEMMs on hipBLASLt, in their own library (found beside
+    # libstratakv_amd.so through $ORIGIN).
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", gemm_obj, f"-L{PKG}", "-lstratakv_amd", "-lhipblaslt",
+          "-Wl,-rpath,$ORIGIN", "-Wl,-soname,libstratakv_amd_gemm.so", "-o", GEMM_LIB + ".tmp"])
+    os.replace(GEMM_LIB + ".tmp", GEMM_LIB)
     return LIB
 
 

@@ -10,6 +10,9 @@
 // --prompt N: N prompt tokens (the 16 below, then ids from a fixed 32-bit LCG)
 // instead of 16, to time the prompt pass on long prompts.  --eager: every decode
 // step launched one kernel at a time (Generator::set_graph_replay(false)).
+// Also reported: the process's first generation (first_call_ms) and, for a
+// prompt one token shorter than any run before, its first and second
+// generation of one token (unseen_length_*_ms).
 #include <algorithm>
 #include <chrono>
 #include <cstdint>
@@ -115,7 +118,8 @@ int main(int argc, char** argv) {
             x = x * 1664525u + 1013904223u;
             prompt.push_back(static_cast<int>((x >> 8) % kVocab));
         }
-        std::vector<int> out = gen.generate(prompt, n_new);  // warmup
+        std::vector<int> out = gen.generate(prompt, n_new);  // warmup: the process's first generation
+        const double first_call_ms = gen.last_generation_ms();
         std::vector<double> full, one;
         bool replayed = false;
         for (int r = 0; r < repeat; ++r) {
@@ -125,17 +129,30 @@ int main(int argc, char** argv) {
             (void)gen.generate(prompt, 1);
             one.push_back(gen.last_generation_ms());
         }
+        // A prompt length this process has not run (one token shorter), with
+        // one new token: its first call (new shapes for the library GEMMs of
+        // a long prompt) and its second.
+        double unseen_first_ms = 0.0, unseen_second_ms = 0.0;
+        if (prompt.size() > 1) {
+            const std::vector<int> shorter(prompt.begin(), prompt.end() - 1);
+            (void)gen.generate(shorter, 1);
+            unseen_first_ms = gen.last_generation_ms();
+            (void)gen.generate(shorter, 1);
+            unseen_second_ms = gen.last_generation_ms();
+        }
         const double ms = median(full), ms1 = median(one);
         const double per_token = (ms - ms1) / std::max(1, n_new - 1);
         std::printf("{\"layers\": %zu, \"prompt\": %zu, \"new_tokens\": %zu, \"gen_ms\": %.4f, "
                     "\"tokens_per_s\": %.2f, \"prefill_and_first_token_ms\": %.4f, \"decode_ms_per_token\": %.5f, "
                     "\"decode_tokens_per_s\": %.2f, \"init_ms\": %.2f, \"load_ms\": %.2f, "
                     "\"load_payload_bytes\": %zu, \"load_decode_ms\": %.2f, \"checkpoint\": %s, \"repeat\": %d, "
-                    "\"graph_replay\": %s}\n",
+                    "\"graph_replay\": %s, \"first_call_ms\": %.4f, \"unseen_length_first_ms\": %.4f, "
+                    "\"unseen_length_second_ms\": %.4f}\n",
                     kLayers, prompt.size(), out.size() - prompt.size(), ms,
                     (out.size() - prompt.size()) / (ms / 1e3), ms1, per_token, 1e3 / per_token,
                     gen.initialization_ms(), load_ms, bd.payload_bytes, bd.tensor_decode_ms,
-                    checkpoint.empty() ? "false" : "true", repeat, replayed ? "true" : "false");
+                    checkpoint.empty() ? "false" : "true", repeat, replayed ? "true" : "false", first_call_ms,
+                    unseen_first_ms, unseen_second_ms);
         return 0;
     } catch (const std::exception& e) {
         std::fprintf(stderr, "bench_generate: %s\n", e.what());

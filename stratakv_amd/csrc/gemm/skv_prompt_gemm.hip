@@ -1,29 +1,40 @@
 // skv_prompt_gemm.hip -- the projections of long prompt chunks with their
 // products on hipBLASLt: bf16 weights x bf16 parts of the fp32 inputs, fp32
 // accumulation.  The library GEMMs run the multiply-adds; the kernels around
-// them (skv_layer_ops.hip) split the inputs and apply the layer's epilogue.
+// them (skv_layer_ops.hip, in libstratakv_amd.so) split the inputs and apply
+// the layer's epilogue.  Built as its own shared object,
+// libstratakv_amd_gemm.so, the only part of the build that links hipBLASLt:
+// the append / decode library loads without it, and its host layer opens this
+// one on demand (host/prompt_gemm_api.cpp).
 //
 // Why hi and lo parts: the activations are fp32 and the weights bf16 (the
 // reference multiplies fp32 activations by bf16 weights in fp32,
 // src/cuda/gemm_cuda.cu:445-560).  Each input v becomes hi = bf16(v) and
-// lo = bf16(v - hi); W hi + W lo keeps ~16 significant bits of v and every
-// product is exact, so the result is the fp32 projection up to fp32 rounding.
-// The two parts are stacked as 2 * rows GEMM columns, so each weight matrix
-// is one GEMM of twice the tokens instead of two.
+// lo = bf16(v - hi); both parts are rounded to bf16, so hi + lo keeps ~16
+// significant bits of v (relative error up to ~2^-16, against fp32's 2^-24),
+// and every product of a part with a bf16 weight is exact in fp32.  The two
+// parts are stacked as 2 * rows GEMM columns, so each weight matrix is one
+// GEMM of twice the tokens instead of two.
 //
 // Layout, column-major as hipBLASLt sees it: a weight matrix of N
 // output-major rows with row stride ld is the K x N matrix W^T (op T, lda =
 // ld); the parts are K x 2 rows (op N, ldb = K); the output is N x 2 rows
 // (ldc = N), i.e. [2 * rows][N] row-major with token r's hi products in row r
 // and its lo products in row rows + r.
+//
+// Algorithm choice: hipBLASLt's heuristic ranks the algorithms of a shape;
+// every call takes its first choice.  The choice depends only on the shape,
+// the device and the library version, never on timing, so two processes on
+// the same device and library compute the same bits.
 #include "skv_common.h"
 #include "skv_prompt_gemm.h"
+#include "stratakv_amd_gemm.h"
 
 #include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
-#include <atomic>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <tuple>
 
@@ -34,28 +45,31 @@ constexpr size_t kLibWorkspace = size_t{32} << 20;   // hipBLASLt's own scratch,
 
 size_t align256(size_t b) { return (b + 255) & ~size_t{255}; }
 
-// One GEMM shape's descriptors and algorithm.  hipBLASLt's heuristic ranks
-// up to kCandidates algorithms; the first call of the shape times each of
-// them on its own operands and keeps the fastest (at the prompt pass's
-// shapes its first choice was up to 26 % slower than the best one).
-constexpr int kCandidates = 10;
+// One GEMM shape's descriptors and hipBLASLt's first-ranked algorithm for it.
 struct Plan {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
     hipblasLtMatmulAlgo_t algo{};
-    hipblasLtMatmulAlgo_t candidates[kCandidates];
-    int ncandidates = 0;
-    std::atomic<bool> chosen{false};   // algo final (set under the lock, read without it)
     bool ok = false;
+    ~Plan() {
+        if (a != nullptr) hipblasLtMatrixLayoutDestroy(a);
+        if (b != nullptr) hipblasLtMatrixLayoutDestroy(b);
+        if (c != nullptr) hipblasLtMatrixLayoutDestroy(c);
+        if (desc != nullptr) hipblasLtMatmulDescDestroy(desc);
+    }
 };
+using PlanPtr = std::shared_ptr<const Plan>;
 
 // Per device: the library handle (created on first use, kept for the process)
-// and the plans of the shapes seen.  Plans are never erased, so a pointer to
-// one stays valid after the lock is released.
+// and the plans of the shapes seen.  The plan of a shape holds the token count
+// (each new prompt-tail length is a new shape), so the cache is bounded: past
+// kMaxPlans shapes it starts afresh.  Callers hold shared pointers, so a plan
+// in use outlives its removal from the cache.
+constexpr size_t kMaxPlans = 256;
 struct DeviceState {
     hipblasLtHandle_t handle = nullptr;
     bool failed = false;
-    std::map<std::tuple<int, int, int, int64_t>, Plan> plans;
+    std::map<std::tuple<int, int, int, int64_t>, PlanPtr> plans;
 };
 
 std::mutex g_mutex;
@@ -63,7 +77,7 @@ std::map<int, DeviceState> g_devices;
 
 // The plan of an m x n x k GEMM with lda, or nullptr when hipBLASLt has none
 // (or cannot start on this device).
-Plan* plan_for(int m, int n, int k, int64_t lda) {
+PlanPtr plan_for(int m, int n, int k, int64_t lda) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lock(g_mutex);
@@ -75,38 +89,41 @@ Plan* plan_for(int m, int n, int k, int64_t lda) {
     if (ds.failed) return nullptr;
     const auto key = std::make_tuple(m, n, k, lda);
     auto it = ds.plans.find(key);
-    if (it != ds.plans.end()) return it->second.ok ? &it->second : nullptr;
-    Plan& p = ds.plans[key];
+    if (it != ds.plans.end()) return it->second->ok ? it->second : nullptr;
+    if (ds.plans.size() >= kMaxPlans) ds.plans.clear();
+    auto p = std::make_shared<Plan>();
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
     hipblasLtMatmulPreference_t pref = nullptr;
-    bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) ==
+    bool ok = hipblasLtMatmulDescCreate(&p->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) ==
                   HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) ==
+              hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) ==
                   HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, k, m, lda) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, k, n, k) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&p.c, HIP_R_32F, m, n, m) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p->a, HIP_R_16BF, k, m, lda) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p->b, HIP_R_16BF, k, n, k) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p->c, HIP_R_32F, m, n, m) == HIPBLAS_STATUS_SUCCESS &&
               hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
               hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
                                                     &kLibWorkspace, sizeof(kLibWorkspace)) == HIPBLAS_STATUS_SUCCESS;
     if (ok) {
-        hipblasLtMatmulHeuristicResult_t found[kCandidates];
+        // The first algorithm of the heuristic's ranking that fits the workspace.
+        constexpr int kRanked = 4;
+        hipblasLtMatmulHeuristicResult_t found[kRanked];
         int nfound = 0;
-        ok = hipblasLtMatmulAlgoGetHeuristic(ds.handle, p.desc, p.a, p.b, p.c, p.c, pref, kCandidates, found,
+        ok = hipblasLtMatmulAlgoGetHeuristic(ds.handle, p->desc, p->a, p->b, p->c, p->c, pref, kRanked, found,
                                              &nfound) == HIPBLAS_STATUS_SUCCESS;
-        for (int i = 0; ok && i < nfound; ++i)
-            if (found[i].state == HIPBLAS_STATUS_SUCCESS && found[i].workspaceSize <= kLibWorkspace)
-                p.candidates[p.ncandidates++] = found[i].algo;
-        ok = ok && p.ncandidates > 0;
-        if (ok) {
-            p.algo = p.candidates[0];
-            p.chosen = p.ncandidates == 1;
-        }
+        bool have = false;
+        for (int i = 0; ok && !have && i < nfound; ++i)
+            if (found[i].state == HIPBLAS_STATUS_SUCCESS && found[i].workspaceSize <= kLibWorkspace) {
+                p->algo = found[i].algo;
+                have = true;
+            }
+        ok = ok && have;
     }
     if (pref != nullptr) hipblasLtMatmulPreferenceDestroy(pref);
-    p.ok = ok;
-    return ok ? &p : nullptr;
+    p->ok = ok;
+    ds.plans.emplace(key, p);
+    return ok ? p : nullptr;
 }
 
 // The plans of every weight matrix of one call, looked up before anything is
@@ -116,7 +133,7 @@ struct Gemm {
     int64_t ld;
     int n;
     float* d;
-    Plan* plan;
+    PlanPtr plan;
 };
 
 // Workspace: [2 rows][K] bf16 parts, then [2 rows][outputs] fp32 GEMM
@@ -167,42 +184,6 @@ bool plan_all(Gemm* g, int count, int rows, int K) {
     return true;
 }
 
-// The first call of a shape: each candidate once to warm up, then twice
-// timed with events on the call's stream (the host waits for them), on the
-// call's own operands; the GEMM has beta = 0, so the runs only overwrite its
-// output, which the chosen algorithm then writes once more.  Under the lock,
-// so a shape is timed once per device.
-void choose_algorithm(hipblasLtHandle_t handle, Plan& p, const Gemm& g, const uint16_t* parts, void* lib,
-                      hipStream_t s) {
-    std::lock_guard<std::mutex> lock(g_mutex);
-    if (p.chosen) return;
-    const float alpha = 1.0f, beta = 0.0f;
-    hipEvent_t e0 = nullptr, e1 = nullptr;
-    float best = 0.0f;
-    int best_i = 0;
-    if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
-        for (int i = 0; i < p.ncandidates; ++i) {
-            auto run = [&] {
-                return hipblasLtMatmul(handle, p.desc, &alpha, g.w, p.a, parts, p.b, &beta, g.d, p.c, g.d, p.c,
-                                       &p.candidates[i], lib, kLibWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
-            };
-            float ms = 0.0f;
-            const bool ok = run() && hipEventRecord(e0, s) == hipSuccess && run() && run() &&
-                            hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
-                            hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
-            if (ok && (i == 0 || ms < best)) {
-                best = ms;
-                best_i = i;
-            }
-        }
-    }
-    if (e0 != nullptr) (void)hipEventDestroy(e0);
-    if (e1 != nullptr) (void)hipEventDestroy(e1);
-    (void)hipGetLastError();   // a candidate that failed to launch is not the call's error
-    p.algo = p.candidates[best_i];
-    p.chosen = true;
-}
-
 int run_gemms(const char* fn, const Gemm* g, int count, const uint16_t* parts, void* lib, hipStream_t s) {
     const float alpha = 1.0f, beta = 0.0f;
     int dev = 0;
@@ -213,8 +194,7 @@ int run_gemms(const char* fn, const Gemm* g, int count, const uint16_t* parts, v
         handle = g_devices[dev].handle;
     }
     for (int i = 0; i < count; ++i) {
-        Plan& p = *g[i].plan;
-        if (!p.chosen) choose_algorithm(handle, p, g[i], parts, lib, s);
+        const Plan& p = *g[i].plan;
         const hipblasStatus_t st = hipblasLtMatmul(handle, p.desc, &alpha, g[i].w, p.a, parts, p.b, &beta, g[i].d,
                                                    p.c, g[i].d, p.c, &p.algo, lib, kLibWorkspace, s);
         if (st != HIPBLAS_STATUS_SUCCESS) return set_error(SKV_ERR_HIP, "%s: hipblasLtMatmul failed (%d)", fn, st);

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "abi_check.h"
+#include "prompt_gemm_api.h"
 
 namespace stratakv {
 namespace models {
@@ -418,14 +419,50 @@ void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output,
     }
 }
 
+TransformerBlock::PrefillGemmUse TransformerBlock::prefill_gemm_use(int rows) const noexcept {
+    PrefillGemmUse use;
+    const detail::PromptGemmApi* api = rows >= kPrefillGemmRows ? detail::prompt_gemm_api() : nullptr;
+    if (api == nullptr) return use;
+    auto takes = [](const layers::Linear& l) {
+        return l.weight().dtype() == DataType::BF16 && l.weight().strides()[0] == 1 && l.input_dim() % 8 == 0 &&
+               l.input_dim() <= 8192;
+    };
+    const layers::Linear& wq = attention_.query_projection();
+    const layers::Linear& wk = attention_.key_projection();
+    const layers::Linear& wv = attention_.value_projection();
+    const int hidden = static_cast<int>(hidden_dim_);
+    const int inter = static_cast<int>(gate_proj_.output_dim());
+    const int q_dim = static_cast<int>(attention_.num_heads() * attention_.head_dim());
+    const int kv_dim = static_cast<int>(attention_.num_kv_heads() * attention_.head_dim());
+    use.qkv = takes(wq) && takes(wk) && takes(wv);
+    use.o = takes(attention_.output_projection());
+    use.gate_up = takes(gate_proj_) && takes(up_proj_);
+    use.down = takes(down_proj_);
+    use.ffn = use.gate_up && use.down;
+    auto need = [&](bool on, int in, int outs) {
+        if (on) use.bytes = std::max(use.bytes, api->workspace_bytes(rows, in, outs));
+    };
+    need(use.qkv, hidden, q_dim + 2 * kv_dim);
+    need(use.o, q_dim, hidden);
+    // The feed-forward call's workspace also serves gate/up and down_proj as
+    // separate calls, should it refuse the chunk.
+    need(use.ffn, std::max(hidden, inter), std::max(2 * inter, hidden));
+    need(use.gate_up, hidden, 2 * inter);
+    need(use.down, inter, hidden);
+    return use;
+}
+
 int TransformerBlock::prefill_chunk_rows() const noexcept {
-    // fp32 scratch per token: q, k, v, context, residual, act, normalised input.
+    // fp32 scratch per token: q, k, v, context, residual, act, normalised
+    // input; plus the library GEMMs' workspace of the chunk.
     const std::size_t q_dim = attention_.num_heads() * attention_.head_dim();
     const std::size_t kv_dim = attention_.num_kv_heads() * attention_.head_dim();
     const std::size_t row_bytes = 4 * (2 * q_dim + 2 * kv_dim + 2 * hidden_dim_ + gate_proj_.output_dim());
-    const std::size_t fit = kPrefillScratchBudget / std::max<std::size_t>(row_bytes, 1);
-    const std::size_t rows = std::min<std::size_t>(kPrefillChunk, fit) / 64 * 64;
-    return static_cast<int>(std::max<std::size_t>(kPrefillMinChunk, rows));
+    int rows = kPrefillChunk;
+    while (rows > kPrefillMinChunk &&
+           row_bytes * static_cast<std::size_t>(rows) + prefill_gemm_use(rows).bytes > kPrefillScratchBudget)
+        rows -= 64;
+    return std::max(rows, kPrefillMinChunk);
 }
 
 void TransformerBlock::ensure_prefill_workspace(int rows) {
@@ -555,22 +592,15 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
         // (or when it does not take the shape) the rows kernels, else the
         // separate kernels.
         const bool mm = n >= kPrefillMmRows;
-        // From kPrefillGemmRows tokens every projection runs as library GEMMs
-        // (one workspace sized for the widest): the 2,048-token prompt of the
-        // TinyLlama shape took 14.8 ms so against 15.2 ms with q/k/v and
-        // o_proj on the matrix-core kernels and 17.2 ms with all four there.
-        const bool lib = n >= kPrefillGemmRows;
-        std::size_t gemm_bytes = 0;
-        void* gemm_ws = nullptr;
-        if (lib) {
-            const int kv_dim = num_kv_heads * head_dim;
-            for (const auto& [in, outs] : {std::pair<int, int>{hidden, q_dim + 2 * kv_dim}, {hidden, 2 * inter},
-                                           {q_dim, hidden}, {inter, hidden}})
-                gemm_bytes = std::max(gemm_bytes, skv_prompt_gemm_workspace_bytes(n, in, outs));
-            gemm_bytes = std::max(gemm_bytes, skv_prompt_gemm_workspace_bytes(n, std::max(hidden, inter),
-                                                                              std::max(2 * inter, hidden)));
-            gemm_ws = prefill_gemm_workspace(gemm_bytes);
-        }
+        // From kPrefillGemmRows tokens the projections whose weights the
+        // library GEMMs take run there (one workspace sized for the widest of
+        // those): the 2,048-token prompt of the TinyLlama shape took 14.8 ms
+        // so against 15.2 ms with q/k/v and o_proj on the matrix-core kernels
+        // and 17.2 ms with all four there.
+        const PrefillGemmUse use = prefill_gemm_use(n);
+        const detail::PromptGemmApi* api = use.bytes > 0 ? detail::prompt_gemm_api() : nullptr;
+        const std::size_t gemm_bytes = use.bytes;
+        void* gemm_ws = api != nullptr ? prefill_gemm_workspace(gemm_bytes) : nullptr;
         // Input RMSNorm, q/k/v projections and RoPE at p0 + row.
         auto qkv = [&](auto entry, float* scratch) {
             return entry(x, n, cfp(norm1_.gamma()), norm1_.epsilon(), wq.weight().raw_data(), wk.weight().raw_data(),
@@ -581,11 +611,11 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                                   const void* c, int dt, int64_t sk, const int64_t* sn, const float* ba,
                                   const float* bb, const float* bc, int hd_, int nh, int nkv, int hdim, int pos,
                                   float* qq, float* kk, float* vv, float* scratch, void* st) {
-            return skv_fused_qkv_gemm_f32(xx, rows, g, e, a, b, c, dt, sk, sn, ba, bb, bc, hd_, nh, nkv, hdim, pos, qq,
-                                          kk, vv, scratch, gemm_ws, gemm_bytes, st);
+            return api->fused_qkv(xx, rows, g, e, a, b, c, dt, sk, sn, ba, bb, bc, hd_, nh, nkv, hdim, pos, qq, kk, vv,
+                                  scratch, gemm_ws, gemm_bytes, st);
         };
         if (!(same_dtype &&
-              ((lib && fused(qkv(qkv_gemm_entry, fp(*pf_->normalized)), "prefill_into: q/k/v as library GEMMs")) ||
+              ((use.qkv && fused(qkv(qkv_gemm_entry, fp(*pf_->normalized)), "prefill_into: q/k/v as library GEMMs")) ||
                (mm && fused(qkv(skv_fused_qkv_mm_f32, fp(*pf_->normalized)), "prefill_into: q/k/v on the matrix cores")) ||
                fused(qkv(skv_fused_qkv_rows_f32, fp(*pf_->normalized)), "prefill_into: fused rmsnorm + q/k/v + rope")))) {
             float* xn = fp(*pf_->normalized);
@@ -612,9 +642,9 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                       "prefill_into: paged prefill attention");
 
         // o_proj + residual (reads x before y is written: aliasing-safe).
-        if (!((lib && fused(skv_linear_residual_gemm_f32(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
-                                                         stride_n(wo), q_dim, hidden, bias_of(wo), x, h, gemm_ws,
-                                                         gemm_bytes, s),
+        if (!((use.o && fused(api->linear_residual(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
+                                                   stride_n(wo), q_dim, hidden, bias_of(wo), x, h, gemm_ws,
+                                                   gemm_bytes, s),
                             "prefill_into: o_proj as a library GEMM")) ||
               (mm && fused(skv_linear_residual_mm_f32(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),
                                                       stride_n(wo), q_dim, hidden, bias_of(wo), x, h, s),
@@ -627,14 +657,14 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
         }
         // The feed-forward half as one library-GEMM call (the SwiGLU output
         // goes straight to down_proj as its split operand), else in two steps.
-        if (!(lib && ffn_same && stride_k(down_proj_) == stride_k(gate_proj_) &&
+        if (!(use.ffn && ffn_same && stride_k(down_proj_) == stride_k(gate_proj_) &&
               wdtype(down_proj_) == wdtype(gate_proj_) &&
-              fused(skv_ffn_swiglu_gemm_f32(h, n, cfp(norm2_.gamma()), norm2_.epsilon(), gate_proj_.weight().raw_data(),
-                                            up_proj_.weight().raw_data(), down_proj_.weight().raw_data(),
-                                            wdtype(gate_proj_), stride_k(gate_proj_), stride_n(gate_proj_),
-                                            stride_n(up_proj_), stride_n(down_proj_), bias_of(gate_proj_),
-                                            bias_of(up_proj_), bias_of(down_proj_), hidden, inter, y,
-                                            fp(*pf_->normalized), gemm_ws, gemm_bytes, s),
+              fused(api->ffn_swiglu(h, n, cfp(norm2_.gamma()), norm2_.epsilon(), gate_proj_.weight().raw_data(),
+                                    up_proj_.weight().raw_data(), down_proj_.weight().raw_data(), wdtype(gate_proj_),
+                                    stride_k(gate_proj_), stride_n(gate_proj_), stride_n(up_proj_),
+                                    stride_n(down_proj_), bias_of(gate_proj_), bias_of(up_proj_),
+                                    bias_of(down_proj_), hidden, inter, y, fp(*pf_->normalized), gemm_ws,
+                                    gemm_bytes, s),
                     "prefill_into: FFN as library GEMMs"))) {
             // Post-attention RMSNorm, gate/up and SwiGLU.
             auto gate_up = [&](auto entry, float* scratch) {
@@ -646,11 +676,12 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
             auto gate_up_gemm_entry = [&](const float* xx, int rows, const float* g, float e, const void* a,
                                           const void* b, int dt, int64_t sk, int64_t sa, int64_t sb, const float* ba,
                                           const float* bb, int in, int out, float* y_, float* scratch, void* st) {
-                return skv_fused_gate_up_swiglu_gemm_f32(xx, rows, g, e, a, b, dt, sk, sa, sb, ba, bb, in, out, y_,
-                                                         scratch, gemm_ws, gemm_bytes, st);
+                return api->fused_gate_up_swiglu(xx, rows, g, e, a, b, dt, sk, sa, sb, ba, bb, in, out, y_, scratch,
+                                                 gemm_ws, gemm_bytes, st);
             };
             if (!(ffn_same &&
-                  ((lib && fused(gate_up(gate_up_gemm_entry, fp(*pf_->normalized)), "prefill_into: gate/up as library GEMMs")) ||
+                  ((use.gate_up && fused(gate_up(gate_up_gemm_entry, fp(*pf_->normalized)),
+                                         "prefill_into: gate/up as library GEMMs")) ||
                    (mm && fused(gate_up(skv_fused_gate_up_swiglu_mm_f32, fp(*pf_->normalized)),
                                 "prefill_into: gate/up on the matrix cores")) ||
                    fused(gate_up(skv_fused_gate_up_swiglu_rows_f32, fp(*pf_->normalized)),
@@ -664,9 +695,9 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                 detail::check(skv_swiglu_f32(act, up, n * inter, s), "prefill_into: swiglu");
             }
             // down_proj + residual into the output rows.
-            if (!((lib && fused(skv_linear_residual_gemm_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
-                                                             stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
-                                                             bias_of(down_proj_), h, y, gemm_ws, gemm_bytes, s),
+            if (!((use.down && fused(api->linear_residual(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
+                                                          stride_k(down_proj_), stride_n(down_proj_), inter, hidden,
+                                                          bias_of(down_proj_), h, y, gemm_ws, gemm_bytes, s),
                                 "prefill_into: down_proj as a library GEMM")) ||
                   (mm && fused(skv_linear_residual_mm_f32(act, n, down_proj_.weight().raw_data(), wdtype(down_proj_),
                                                           stride_k(down_proj_), stride_n(down_proj_), inter, hidden,

@@ -120,11 +120,6 @@ int skv_linear_f32(const float*, int, const void*, int, int64_t, int64_t, int, i
 int skv_linear_residual_f32(const float*, const void*, int, int64_t, int64_t, int, int, const float*, const float*, float*, void*) { return fail("skv_linear_residual_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
 int skv_linear_residual_mm_f32(const float*, int, const void*, int, int64_t, int64_t, int, int, const float*, const float*, float*, void*) { return fail("skv_linear_residual_mm_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
-size_t skv_prompt_gemm_workspace_bytes(int, int, int) { return 0; }
-int skv_fused_qkv_gemm_f32(const float*, int, const float*, float, const void*, const void*, const void*, int, int64_t, const int64_t*, const float*, const float*, const float*, int, int, int, int, int, float*, float*, float*, float*, void*, size_t, void*) { return fail("skv_fused_qkv_gemm_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
-int skv_fused_gate_up_swiglu_gemm_f32(const float*, int, const float*, float, const void*, const void*, int, int64_t, int64_t, int64_t, const float*, const float*, int, int, float*, float*, void*, size_t, void*) { return fail("skv_fused_gate_up_swiglu_gemm_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
-int skv_linear_residual_gemm_f32(const float*, int, const void*, int, int64_t, int64_t, int, int, const float*, const float*, float*, void*, size_t, void*) { return fail("skv_linear_residual_gemm_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
-int skv_ffn_swiglu_gemm_f32(const float*, int, const float*, float, const void*, const void*, const void*, int, int64_t, int64_t, int64_t, int64_t, const float*, const float*, const float*, int, int, float*, float*, void*, size_t, void*) { return fail("skv_ffn_swiglu_gemm_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
 int skv_linear_residual_rows_f32(const float*, int, const void*, int, int64_t, int64_t, int, int, const float*, const float*, float*, void*) { return fail("skv_linear_residual_rows_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 

@@ -4,6 +4,8 @@ reference's invalid_argument semantics (src/cuda/gemm_cuda.cu:920-928) before
 touching a device.  No kernel runs here."""
 import ctypes
 import math
+import shutil
+import subprocess
 
 import pytest
 
@@ -17,6 +19,30 @@ def test_library_exports_every_header_symbol():
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, f"declared but not exported: {missing}"
     assert skv.lib().skv_abi_version() >= 1
+
+
+def test_gemm_library_exports_every_header_symbol():
+    names = skv.header_symbols(skv.GEMM_HEADER_PATH)
+    assert len(names) == 5
+    assert not set(names) & set(skv.header_symbols()), "declared in both headers"
+    glib = skv.gemm_lib()
+    missing = [n for n in names if not hasattr(glib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def _needed(path):
+    out = subprocess.run(["readelf", "-d", path], stdout=subprocess.PIPE, text=True, check=True).stdout
+    return [line.split("[")[1].split("]")[0] for line in out.splitlines() if "(NEEDED)" in line]
+
+
+@pytest.mark.skipif(shutil.which("readelf") is None, reason="readelf not installed")
+def test_only_the_gemm_library_links_hipblaslt():
+    """libstratakv_amd.so (append, decode, layer kernels, host layer) loads
+    without hipBLASLt; libstratakv_amd_gemm.so links it and the main library."""
+    main = _needed(skv.LIB_PATH)
+    assert not [n for n in main if "hipblaslt" in n], main
+    gemm = _needed(skv.GEMM_LIB_PATH)
+    assert any("hipblaslt" in n for n in gemm) and "libstratakv_amd.so" in gemm, gemm
 
 
 def test_workspace_sizes_are_positive_and_bounded():
@@ -165,7 +191,7 @@ def test_library_gemm_projections_reject_invalid_arguments():
     (nothing launched, hipBLASLt not asked) for fp32 weights, in_dim not a
     multiple of 8, an output count not a multiple of 8, a rotated head_dim not
     a multiple of 8."""
-    lib = skv.lib()
+    lib = skv.gemm_lib()
     eps = ctypes.c_float(1e-5)
     wsb = lib.skv_prompt_gemm_workspace_bytes
     # [2 rows][K] bf16 parts, [2 rows][outputs] fp32 and a RoPE table of 4 rows (outputs / 3) bytes, each

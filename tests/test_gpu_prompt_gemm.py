@@ -27,7 +27,7 @@ def _padded(W, pad):
 def _run_all(gpu, entry, dW, ld, bp, dims, n, position, dx, dg, dctx, dact, dres, out, normalized, ws, wsb):
     """The four projections of a layer through the gemm (entry = "gemm") or mm
     (entry = "mm") entry points."""
-    lib = gpu.lib()
+    lib = gpu.gemm_lib() if entry == "gemm" else gpu.lib()
     H, Hq, Hkv, hd, inter = dims
     eps = ctypes.c_float(1e-5)
     strides = (ctypes.c_int64 * 3)(ld["q"], ld["k"], ld["v"])
@@ -87,7 +87,7 @@ def test_gemm_projections_match_float64_and_mm(gpu, dims, with_bias, packed):
     allocation (one GEMM each) or apart."""
     H, Hq, Hkv, hd, inter = dims
     rng = np.random.default_rng(7 * H + inter + with_bias)
-    lib, D = gpu.lib(), gpu.DeviceBuffer
+    lib, D = gpu.gemm_lib(), gpu.DeviceBuffer
     shapes = (("q", Hq * hd, H), ("k", Hkv * hd, H), ("v", Hkv * hd, H), ("o", H, Hq * hd),
               ("g", inter, H), ("u", inter, H), ("d", H, inter))
     W = {n: _bf16_rows(rng, o, i, 0.03) for n, o, i in shapes}
@@ -132,7 +132,7 @@ def test_gemm_residual_in_place_and_repeated_calls(gpu):
     """y aliasing the residual, and one workspace reused by calls of other
     sizes one after another (the second smaller): each result as the float64
     restatement."""
-    lib, D = gpu.lib(), gpu.DeviceBuffer
+    lib, D = gpu.gemm_lib(), gpu.DeviceBuffer
     rng = np.random.default_rng(11)
     K, N = 1024, 512
     W = _bf16_rows(rng, N, K, 0.03)
@@ -156,7 +156,7 @@ def test_gemm_projections_refuse_unsupported_shapes(gpu):
     """fp32 weights, in_dim not a multiple of 8, an output count not a multiple
     of 8, a bias not 16-byte aligned: SKV_ERR_UNSUPPORTED and nothing
     written."""
-    lib, D = gpu.lib(), gpu.DeviceBuffer
+    lib, D = gpu.gemm_lib(), gpu.DeviceBuffer
     y = D.from_numpy(np.full((3, 64), 7.0, np.float32))
     res = D.from_numpy(np.zeros((3, 64), np.float32))
     for K, out_dim, dt in ((1024, 64, gpu.DTYPE_FP32), (1020, 64, gpu.DTYPE_BF16), (1024, 60, gpu.DTYPE_BF16)):
@@ -191,7 +191,7 @@ def test_ffn_gemm_matches_two_calls_and_float64(gpu, dims, with_bias, packed):
     normalised rows bit-identical."""
     H, _, _, _, inter = dims
     rng = np.random.default_rng(3 * H + inter + with_bias + 2 * packed)
-    lib, D = gpu.lib(), gpu.DeviceBuffer
+    lib, D = gpu.gemm_lib(), gpu.DeviceBuffer
     W = {n: _bf16_rows(rng, o, i, 0.03) for n, o, i in (("g", inter, H), ("u", inter, H), ("d", H, inter))}
     dW, ld = _upload_weights(D, W, ["g", "u", "d"], {}, False)
     if packed:
@@ -234,3 +234,62 @@ def test_ffn_gemm_matches_two_calls_and_float64(gpu, dims, with_bias, packed):
         assert np.isfinite(one).all() and err <= 1e-4 * rms, (n, err)
         dtwo = (np.abs(one.astype(np.float64) - two) / (np.abs(ref) + rms)).max()
         assert dtwo <= 5e-5, (n, dtwo)
+
+
+def _digest_of_prompt_gemms():
+    """SHA-256 of the outputs of a packed q/k/v GEMM call and a feed-forward
+    GEMM call over seeded inputs (TinyLlama shapes, 256 and 2,048 tokens): the
+    bits a process computes, for the cross-process comparison below."""
+    import hashlib
+
+    import stratakv_amd as skv
+
+    skv.require_gpu()
+    glib, D = skv.gemm_lib(), skv.DeviceBuffer
+    H, Hq, Hkv, hd, inter = 2048, 32, 4, 64, 5632
+    rng = np.random.default_rng(20261202)
+    shapes = (("q", Hq * hd, H), ("k", Hkv * hd, H), ("v", Hkv * hd, H), ("g", inter, H), ("u", inter, H),
+              ("d", H, inter))
+    W = {n: _bf16_rows(rng, o, i, 0.03) for n, o, i in shapes}
+    dW, ld = _upload_weights(D, W, [n for n, _, _ in shapes], {}, True)
+    eps = ctypes.c_float(1e-5)
+    strides = (ctypes.c_int64 * 3)(ld["q"], ld["k"], ld["v"])
+    h = hashlib.sha256()
+    for n in (256, 2048):
+        wsb = max(glib.skv_prompt_gemm_workspace_bytes(n, H, (Hq + 2 * Hkv) * hd),
+                  glib.skv_prompt_gemm_workspace_bytes(n, inter, 2 * inter))
+        ws = D(wsb)
+        dx = D.from_numpy(rng.standard_normal((n, H)).astype(np.float32))
+        dg = D.from_numpy((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+        q, k, v, xn, y = D(4 * n * Hq * hd), D(4 * n * Hkv * hd), D(4 * n * Hkv * hd), D(4 * n * H), D(4 * n * H)
+        skv._check(glib.skv_fused_qkv_gemm_f32(dx.ptr, n, dg.ptr, eps, dW["q"].ptr, dW["k"].ptr, dW["v"].ptr,
+                                               skv.DTYPE_BF16, 1, strides, None, None, None, H, Hq, Hkv, hd, 3,
+                                               q.ptr, k.ptr, v.ptr, xn.ptr, ws.ptr, wsb, None))
+        skv._check(glib.skv_ffn_swiglu_gemm_f32(dx.ptr, n, dg.ptr, eps, dW["g"].ptr, dW["u"].ptr, dW["d"].ptr,
+                                                skv.DTYPE_BF16, 1, ld["g"], ld["u"], ld["d"], None, None, None, H,
+                                                inter, y.ptr, xn.ptr, ws.ptr, wsb, None))
+        skv.synchronize()
+        for buf, m in ((q, Hq * hd), (k, Hkv * hd), (v, Hkv * hd), (y, H)):
+            h.update(buf.download(np.uint32, (n, m)).tobytes())
+    return h.hexdigest()
+
+
+def test_gemm_results_are_the_same_in_two_processes(gpu):
+    """Each GEMM runs hipBLASLt's first-ranked algorithm for its shape, chosen
+    by the library's heuristic and never by timing, so two fresh processes
+    compute the same bits (and so does this one)."""
+    import os
+    import subprocess
+    import sys
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    code = (f"import sys; sys.path.insert(0, {here!r}); sys.path.insert(0, {os.path.dirname(here)!r}); "
+            "import test_gpu_prompt_gemm as t; print(t._digest_of_prompt_gemms())")
+    digests = []
+    for _ in range(2):
+        proc = subprocess.run([sys.executable, "-c", code], stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                              text=True, timeout=110)
+        assert proc.returncode == 0, proc.stderr[-2000:]
+        digests.append(proc.stdout.strip().splitlines()[-1])
+    digests.append(_digest_of_prompt_gemms())
+    assert digests[0] == digests[1] == digests[2], digests
