@@ -68,7 +68,8 @@ struct DecodeParams {
     int NH;                // query heads per segment: G or 1
     int ranges;            // block ranges; the grid is ranges * Hseg wavefronts
     int min_per;           // minimum blocks per range
-    int32_t* plan;         // [3 + B + 1]: total, per, used ranges, P[0..B]
+    int paired;            // 1: two workgroups per CU, the second half of the grid the younger wavefront of each SIMD
+    int32_t* plan;         // [5 + B + 1]: total, per, used ranges, half, per_b, P[0..B]
     float* ws_ml;          // [2 * ranges * Hseg][NH][2]  (reference max in log2 units, sum)
     float* ws_acc;         // [2 * ranges * Hseg][NH][HD] (unnormalised P.V)
     // Fused append (MFMA kernel only): the new token of sequence b, at position
@@ -103,16 +104,32 @@ __device__ __forceinline__ int seq_blocks(const DecodeParams& p, int b) {
 // Work split ("stream-K" over blocks).  Every workgroup builds P[b] = blocks of
 // the sequences before b in LDS (a wave scan over the batch), so no planner
 // launch is needed.  The flattened (sequence, block) space [0, P[B]) is cut
-// into `used` ranges of `per` blocks; wavefront w serves range w / Hseg for
-// head group w % Hseg, so the Hseg wavefronts reading the head slices of the
-// same 16-token blocks run side by side.  A segment = (sequence, head group):
-// it is final when one range holds all of it; otherwise each range touching it
+// into `used` ranges; wavefront w serves range w / Hseg for head group
+// w % Hseg, so the Hseg wavefronts reading the head slices of the same
+// 16-token blocks run side by side.  A segment = (sequence, head group): it is
+// final when one range holds all of it; otherwise each range touching it
 // leaves a partial in slot (2 * range + tail) * Hseg + group, tail = 1 when
 // the segment starts strictly inside the range (then it is the range's last
 // segment), 0 otherwise (the range's first segment).
+//
+// Ranges [0, half) hold `per` blocks and ranges [half, used) `per_b`.  The
+// split is even (half = used, per_b = per) unless the grid is paired: two
+// workgroups per CU, two wavefronts per SIMD, where the second half of the
+// grid is dispatched after the first and runs as the younger wavefront of
+// every SIMD.  The SIMD issues for the older wavefront first, so with equal
+// ranges the younger ones finished ~9 % later (per-wavefront timestamps, cfg3
+// on MI355X); paired grids give the first half kPairShare / (kPairShare - 1)
+// times the blocks of the second.
 // ---------------------------------------------------------------------------
+constexpr int kPairShare = 24;
+
 struct WorkSplit {
-    int total, per, used;
+    int total, per, used, half, per_b;
+    __device__ int lo(int r) const { return r <= half ? r * per : half * per + (r - half) * per_b; }
+    __device__ int range_of(int pos) const {
+        const int edge = half * per;
+        return pos < edge ? pos / per : half + (pos - edge) / per_b;
+    }
 };
 
 __device__ WorkSplit build_split(const DecodeParams& p, int* P_s, bool stream_k) {
@@ -144,16 +161,32 @@ __device__ WorkSplit build_split(const DecodeParams& p, int* P_s, bool stream_k)
         if (lane == 0) P_s[0] = 0;
     }
     __syncthreads();
-    WorkSplit ws{P_s[p.B], 0, 0};
+    WorkSplit ws{P_s[p.B], 0, 0, 0, 0};
     if (!stream_k) return ws;  // one workgroup per segment: no ranges
     ws.per = std::max(p.min_per, ws.total > 0 ? cdiv(ws.total, p.ranges) : 1);
     ws.used = ws.total > 0 ? cdiv(ws.total, ws.per) : 0;
+    ws.half = ws.used;
+    ws.per_b = ws.per;
+    if (p.paired && ws.total > 0) {
+        const int H = p.ranges / 2;
+        const int pb = static_cast<int>(static_cast<int64_t>(ws.total) * (kPairShare - 1) /
+                                        (static_cast<int64_t>(2) * kPairShare * H));
+        const int pa = pb > 0 ? cdiv(ws.total - H * pb, H) : 0;
+        if (pb >= p.min_per && pa >= pb) {
+            ws.per = pa;
+            ws.per_b = pb;
+            ws.half = H;
+            ws.used = H + cdiv(std::max(0, ws.total - H * pa), pb);
+        }
+    }
     if (blockIdx.x == 0 && lane < 64 && p.plan != nullptr) {  // publish for the merge kernel
-        for (int i = lane; i <= p.B; i += 64) p.plan[3 + i] = P_s[i];
+        for (int i = lane; i <= p.B; i += 64) p.plan[5 + i] = P_s[i];
         if (lane == 0) {
             p.plan[0] = ws.total;
             p.plan[1] = ws.per;
             p.plan[2] = ws.used;
+            p.plan[3] = ws.half;
+            p.plan[4] = ws.per_b;
         }
     }
     return ws;
@@ -279,11 +312,10 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
 
     const WorkSplit split = build_split(p, P_s, !SPLIT);
     if (!SPLIT && range >= split.used) return;
-    const int per = split.per;
     const int64_t row_stride = static_cast<int64_t>(Hkv) * HD;
     const int block_bytes = static_cast<int>(BS * row_stride * 2);
-    int range_lo = range * per;
-    int range_hi = range_lo + per;
+    int range_lo = SPLIT ? 0 : split.lo(range);
+    int range_hi = SPLIT ? 0 : split.lo(range + 1);
     int b = 0;
     if constexpr (SPLIT) {
         // Wavefront wv: blocks [wv * NBUF, wv * NBUF + NBUF) of the segment.
@@ -632,8 +664,8 @@ __global__ __launch_bounds__(64 * WPW) void block_stream_checksum_kernel(DecodeP
     if (range >= split.used) return;
     const int64_t row_stride = static_cast<int64_t>(Hkv) * HD;
     const int block_bytes = static_cast<int>(BS * row_stride * 2);
-    const int range_lo = range * split.per;
-    const int end = std::min(range_lo + split.per, split.total);
+    const int range_lo = split.lo(range);
+    const int end = std::min(split.lo(range + 1), split.total);
     int pos = range_lo;
     int b = find_seq(P_s, p.B, pos);
     const int lane_off_b = static_cast<int>((r * row_stride + static_cast<int64_t>(kvh) * HD + c * 8) * 2);
@@ -721,10 +753,9 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
     const int range = w / Hq;
     const WorkSplit split = build_split(p, P_s, true);
     if (range >= split.used) return;
-    const int per = split.per;
     const int64_t row_elems = static_cast<int64_t>(p.Hkv) * HD;
-    const int range_lo = range * per;
-    const int range_hi = range_lo + per;
+    const int range_lo = split.lo(range);
+    const int range_hi = split.lo(range + 1);
     int pos = range_lo;
     const int end = std::min(range_hi, split.total);
     int b = find_seq(P_s, p.B, pos);
@@ -830,17 +861,18 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
 // Merge of the segments cut by range boundaries:
 //   out = sum_r acc_r 2^(m_r - M) / sum_r l_r 2^(m_r - M),  M = max_r m_r,
 // over the n ranges r that touch the segment, per query head.  One 256-thread
-// workgroup per (segment, 64 output columns).  With at most 8 partials (long
-// batches) the segment's first workgroup merges all its columns in one round
-// of loads and the others exit.  With more (short batches, one long
-// sequence), thread (c, pg) = (t % 64, t / 64) of every workgroup takes
-// partials pg, pg + 4, ... of column c, 8 at a time with all their loads in
-// flight, and keeps its own (max, sum, acc) triple, rescaled per batch; the 4
-// partial groups are combined the same way through LDS.  Segments held by one
-// range, and sequences without context, were written by the attention kernel;
-// with a single range the merge is not launched at all.
+// workgroup per (segment, chunk of merge_cw output columns).  With at most
+// kMergeFew partials (kMergeFew / 2 when a thread covers 4 columns; long and
+// medium batches) every thread loads all the partials of its columns in one
+// round.  With more (short batches, one long sequence), thread (c, pg) =
+// (t % 64, t / 64) takes partials pg, pg + 4, ... of column c, 8 at a time
+// with all their loads in flight, and keeps its own (max, sum, acc) triple,
+// rescaled per batch; the 4 partial groups are combined the same way through
+// LDS.  Segments held by one range, and sequences without context, were
+// written by the attention kernel; with a single range the merge is not
+// launched at all.
 // ---------------------------------------------------------------------------
-constexpr int kMergeFew = 8;   // partials merged by one workgroup per segment
+constexpr int kMergeFew = 16;   // partials merged in one round of loads
 
 // NP partials (exactly), NC columns per thread: every load is unconditional,
 // so all 3 * NP * NC of them are in flight together (a conditional load makes
@@ -894,7 +926,21 @@ __device__ __forceinline__ void merge_few_n(const DecodeParams& p, int grp, int 
         case 5: merge_few<NC, 5>(p, grp, r0, first_tail, out0, c0, c1); break;
         case 6: merge_few<NC, 6>(p, grp, r0, first_tail, out0, c0, c1); break;
         case 7: merge_few<NC, 7>(p, grp, r0, first_tail, out0, c0, c1); break;
-        default: merge_few<NC, 8>(p, grp, r0, first_tail, out0, c0, c1); break;
+        case 8: merge_few<NC, 8>(p, grp, r0, first_tail, out0, c0, c1); break;
+        default:
+            if constexpr (NC <= 2) {
+                switch (n) {
+                    case 9: merge_few<NC, 9>(p, grp, r0, first_tail, out0, c0, c1); break;
+                    case 10: merge_few<NC, 10>(p, grp, r0, first_tail, out0, c0, c1); break;
+                    case 11: merge_few<NC, 11>(p, grp, r0, first_tail, out0, c0, c1); break;
+                    case 12: merge_few<NC, 12>(p, grp, r0, first_tail, out0, c0, c1); break;
+                    case 13: merge_few<NC, 13>(p, grp, r0, first_tail, out0, c0, c1); break;
+                    case 14: merge_few<NC, 14>(p, grp, r0, first_tail, out0, c0, c1); break;
+                    case 15: merge_few<NC, 15>(p, grp, r0, first_tail, out0, c0, c1); break;
+                    default: merge_few<NC, 16>(p, grp, r0, first_tail, out0, c0, c1); break;
+                }
+            }
+            break;
     }
 }
 
@@ -911,18 +957,23 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
     const int c0 = chunk * cw, c1 = min(cols, c0 + cw);
     const int b = s / p.Hseg;
     const int grp = s - b * p.Hseg;
-    const int per = p.plan[1];
-    const int32_t* P = p.plan + 3;
+    WorkSplit split;
+    split.total = p.plan[0];
+    split.per = p.plan[1];
+    split.used = p.plan[2];
+    split.half = p.plan[3];
+    split.per_b = p.plan[4];
+    const int32_t* P = p.plan + 5;
     const int lo = P[b], hi = P[b + 1];
     float* out0 = p.out + (static_cast<int64_t>(b) * p.Hq + grp * NH) * HD;
     if (lo == hi) return;  // no context: zeroed by the attention kernel
-    const int r0 = lo / per, r1 = (hi - 1) / per;
+    const int r0 = split.range_of(lo), r1 = split.range_of(hi - 1);
     if (r0 == r1) return;
     const int n = r1 - r0 + 1;
-    const bool first_tail = lo > r0 * per;
-    if (n <= kMergeFew && cw <= 1024) {
-        // Few partials (long batches): thread t takes columns c0 + t,
-        // c0 + t + 256, ... with all n partials of each loaded at once.
+    const bool first_tail = lo > split.lo(r0);
+    if ((n <= kMergeFew && cw <= 512) || (n <= kMergeFew / 2 && cw <= 1024)) {
+        // Few partials (long and medium batches): thread t takes columns
+        // c0 + t, c0 + t + 256, ... with all n partials of each loaded at once.
         if (cw <= 256) merge_few_n<1>(p, grp, r0, n, first_tail, out0, c0, c1);
         else if (cw <= 512) merge_few_n<2>(p, grp, r0, n, first_tail, out0, c0, c1);
         else merge_few_n<4>(p, grp, r0, n, first_tail, out0, c0, c1);
@@ -1008,7 +1059,7 @@ WorkspaceLayout workspace_layout(int B, int Hq, int Hkv, int HD, int slots = kMa
     WorkspaceLayout w{};
     const int G = Hq / std::max(Hkv, 1);
     const size_t head_slots = 2 * static_cast<size_t>(slots) * std::max(G, 1);
-    const size_t plan_ints = 3 + static_cast<size_t>(std::min(B, kMaxBatchPerLaunch)) + 1;
+    const size_t plan_ints = 5 + static_cast<size_t>(std::min(B, kMaxBatchPerLaunch)) + 1;
     w.plan_off = 0;
     w.ml_off = align256(sizeof(int32_t) * plan_ints);
     w.acc_off = w.ml_off + align256(sizeof(float) * 2 * head_slots);
@@ -1042,6 +1093,18 @@ int resident_waves(K kernel, int wpw, size_t lds, int max_per_simd) {
     return waves;
 }
 
+// Whether a grid of `ranges` ranges is paired (see WorkSplit): the full
+// persistent grid at two wavefronts per SIMD, i.e. two workgroups on every
+// CU, with an even number of ranges so that the second half of the ranges is
+// the second half of the workgroups.
+bool paired_grid(const DecodeParams& p, int waves, int max_per_simd) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return false;
+    return max_per_simd == 2 && waves == cus * 4 * max_per_simd && p.ranges * p.Hseg == waves && p.ranges % 2 == 0;
+}
+
 // Block ranges of the persistent grid: as many as `waves` resident wavefronts
 // hold (Hseg per range), no more than the largest possible work needs (small
 // batches and short contexts launch a small grid) and no more than the
@@ -1057,7 +1120,9 @@ int decode_ranges(const DecodeParams& p, int waves) {
 template <typename K>
 int launch_pair(K kern, int wpw, int max_per_simd, DecodeParams p, hipStream_t s, const char* name) {
     const size_t lds = sizeof(int) * (static_cast<size_t>(p.B) + 1);  // the block prefix
-    p.ranges = decode_ranges(p, resident_waves(kern, wpw, lds, max_per_simd));
+    const int waves = resident_waves(kern, wpw, lds, max_per_simd);
+    p.ranges = decode_ranges(p, waves);
+    p.paired = paired_grid(p, waves, max_per_simd) ? 1 : 0;
     const unsigned groups = static_cast<unsigned>(p.ranges) * (p.Hseg / wpw);
     kern<<<groups, 64 * wpw, lds, s>>>(p);
     if (int rc = check_launch(name)) return rc;
@@ -1124,7 +1189,9 @@ int launch_checksum_shape(DecodeParams p, uint32_t* sums, hipStream_t s) {
     constexpr int PER_SIMD = mfma_waves_per_simd(HD, G);
     const size_t lds = sizeof(int) * (static_cast<size_t>(p.B) + 1);
     auto go = [&](auto decode_kern, auto sum_kern, int wpw) {
-        p.ranges = decode_ranges(p, resident_waves(decode_kern, wpw, lds, PER_SIMD));
+        const int waves = resident_waves(decode_kern, wpw, lds, PER_SIMD);
+        p.ranges = decode_ranges(p, waves);
+        p.paired = paired_grid(p, waves, PER_SIMD) ? 1 : 0;
         const unsigned groups = static_cast<unsigned>(p.ranges) * (p.Hseg / wpw);
         sum_kern<<<groups, 64 * wpw, lds, s>>>(p, sums);
         return check_launch("block_stream_checksum_kernel");
