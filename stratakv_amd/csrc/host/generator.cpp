@@ -233,9 +233,10 @@ Generator::Generator(GeneratorConfig config, io::WeightMap weights)
         for (auto& b : blocks_) b.set_parity_diagnostic(true);
     }
     // STRATAKV_GRAPH_REPLAY=0: every decode step launched one kernel at a time
-    // (as set_graph_replay(false)).  For profiling: rocprofv3's kernel tracing
-    // (ROCm 7.2) ended the process with a segmentation fault inside
-    // hipGraphLaunch, so kernel traces are taken with replay off.
+    // (as set_graph_replay(false)).  For profiling: under rocprofv3's kernel
+    // tracing (ROCm 7.2) a replayed step ended the process with a host-side
+    // read of a runtime-owned device address inside hipGraphLaunch, in frames
+    // outside this library, so kernel traces are taken with replay off.
     if (const char* v = std::getenv("STRATAKV_GRAPH_REPLAY"); v != nullptr && std::strcmp(v, "0") == 0)
         graph_replay_ = false;
     hidden_.emplace(std::vector<std::size_t>{1, h}, DataType::FP32, Device::GPU);
