@@ -34,6 +34,9 @@
 #include "stratakv/models/transformer_block.h"
 
 namespace stratakv {
+namespace detail {
+class ParityModel;
+}
 namespace generation {
 
 struct GeneratorConfig {
@@ -88,6 +91,11 @@ public:
     std::vector<int> last_block_table(std::size_t layer) const {
         return layer < last_tables_.size() ? last_tables_[layer] : std::vector<int>{};
     }
+    // Layer `layer`'s block and KV pool (read-only; no counterpart in the
+    // reference, whose pools are private).  generate puts every block it
+    // wrote back as it was, so a pool holds the same bytes before and after.
+    const models::TransformerBlock& block(std::size_t layer) const { return blocks_.at(layer); }
+    const memory::BlockPool& block_pool(std::size_t layer) const { return pools_.at(layer); }
     // Reseed the sampler's uniform stream (the reference seeds it from
     // std::random_device, as the constructor here does).
     void seed_sampler(std::uint32_t seed) { sampler_ = Sampler(config_.sampler, seed); }
@@ -114,6 +122,8 @@ public:
 private:
     void validate_prompt(const std::vector<int>& prompt, std::size_t extra) const;
     void begin_sequence(std::size_t tokens);
+    void save_kv_blocks(std::size_t blocks);
+    int copy_kv_chunks(std::size_t from, std::size_t to) noexcept;
     void end_sequence() noexcept;
     // One decode step: embedding of ids_[in_index], all layers, final norm,
     // lm_head into `logits` (device [vocab]); data errors go to *flags.
@@ -131,6 +141,17 @@ private:
     // layer's weights do not allow the fused kernels.
     bool prepare_step_graph(std::size_t tokens);
     void release_step_graph() noexcept;
+    // STRATAKV_PARITY=1: the host model's pass over `rows` tokens at positions
+    // first, first + 1, ... (ids host_ids_[first ..]), each layer's output
+    // against the GPU's (gpu[layer] holds the rows), printed per position and
+    // layer; with first == 0 also the embedding and layer 0's ops against
+    // `l0` (row 0 of layer 0's scratch).
+    void parity_pass(int first, std::size_t rows, const std::vector<float>& gpu_embedding,
+                     const std::vector<std::vector<float>>& gpu, const models::TransformerBlock::ParityRow* l0);
+    // The final norm and logits of the host model's last hidden row against
+    // the GPU's (normed_ and logits_), at `position`.
+    void parity_final(int position);
+    std::vector<float> parity_download(const float* device, std::size_t count);
 
     GeneratorConfig config_;
     void* stream_ = nullptr;
@@ -151,11 +172,22 @@ private:
     std::size_t flags_capacity_ = 0;
     std::int32_t* host_ids_ = nullptr;       // page-locked copies of the chosen ids
     std::vector<void*> step_events_;         // ring of kLookahead + 1 events
-    // Free lists saved by begin_sequence and put back by end_sequence (the
-    // reference's SequenceGuard restores whole pool copies), and the tables
-    // of the last sequence.
+    // Free lists saved by begin_sequence and put back by end_sequence, and
+    // the tables of the last sequence.
     std::vector<std::vector<int>> saved_free_lists_;
     std::vector<std::vector<int>> last_tables_;
+    // The K/V blocks a generation may write (the next blocks each pool hands
+    // out), saved by begin_sequence and put back by end_sequence, so the pools
+    // hold the same bytes before and after generate, as after the reference's
+    // SequenceGuard restores its pool copies (src/generation/generator.cpp:
+    // 347-371).
+    void* kv_saved_ = nullptr;              // device [chunks][kv_chunk_bytes_]
+    void** kv_chunk_ptrs_ = nullptr;        // device [2][chunks]: pool block addresses, then their saved copies
+    void** kv_chunk_host_ = nullptr;        // page-locked staging of kv_chunk_ptrs_
+    std::size_t kv_chunks_capacity_ = 0;
+    std::size_t kv_chunks_ = 0;             // chunks saved by the current sequence
+    std::size_t kv_half_ = 0;               // offset of the saved copies' half of kv_chunk_ptrs_
+    std::size_t kv_chunk_bytes_ = 0;
     double last_generation_ms_ = 0.0;
     double initialization_ms_ = 0.0;
     // Graph replay of the greedy decode step.
@@ -167,6 +199,9 @@ private:
     std::int32_t* step_state_ = nullptr;      // device [position, context length, step flag word]
     float* rope_table_ = nullptr;             // device cos/sin pairs of positions [0, rope_positions_)
     int rope_positions_ = 0;
+    // STRATAKV_PARITY=1 (graph replay then stays off).
+    std::unique_ptr<detail::ParityModel> parity_;
+    std::vector<double> parity_last_;   // the host model's last hidden row
 };
 
 }  // namespace generation

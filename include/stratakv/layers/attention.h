@@ -16,6 +16,9 @@
 #include "stratakv/memory/page_table.h"
 
 namespace stratakv {
+namespace models {
+class TransformerBlock;
+}
 namespace layers {
 
 class PagedAttention {
@@ -34,6 +37,10 @@ public:
     // The reference's CPU path; not provided by this build (throws).
     Tensor forward(const Tensor& hidden_states, int seq_id, memory::PageTable& page_table,
                    memory::BlockPool& block_pool, bool append_tokens = true);
+    // Distinct pool blocks the last attention read (src/layers/attention.cpp:
+    // 230-232, 291-296, where only the CPU forward counts them).  Here
+    // TransformerBlock::forward_into and prefill_into set it: the blocks of
+    // the sequence's context.  Replayed graph steps (forward_into_at) leave it.
     std::size_t last_blocks_visited() const noexcept { return last_blocks_visited_; }
 
     Linear& query_projection() noexcept { return q_proj_; }
@@ -64,6 +71,7 @@ private:
     Linear v_proj_;
     Linear out_proj_;
     std::size_t last_blocks_visited_ = 0;
+    friend class models::TransformerBlock;   // sets last_blocks_visited_
 };
 
 }  // namespace layers

@@ -43,13 +43,19 @@ public:
     ~TransformerBlock() = default;
 
     void to(Device device);
-    // The reference's parity diagnostic: on sequence 0's first token,
-    // forward_into compares the paged attention output with a host
-    // double-precision restatement over the K/V read back from the pool and
-    // prints "[PARITY L0] paged_attention: max_diff = ..." to stderr (the
-    // reference also reports its other ops against its CPU path, which this
-    // build does not have).
-    void set_parity_diagnostic(bool enabled) noexcept { parity_diagnostic_ = enabled; }
+    // For the STRATAKV_PARITY diagnostic (the reference's per-op report of
+    // layer 0, src/models/transformer_block.cpp:405-595): row `row` of the
+    // values the last forward_into (row 0) or prefill_into chunk left in this
+    // block's scratch, copied to the host after the stream drains -- q and k
+    // after RoPE, v, the attention context, the residual stream after
+    // o_proj, and the SwiGLU activations.  The fused kernels write no other
+    // intermediate (the normalised rows, q and k before RoPE, gate and up
+    // stay in registers).  A prefill scratch shared by several blocks holds
+    // the last block's rows.  No counterpart in the reference.
+    struct ParityRow {
+        std::vector<float> q, k, v, context, residual, act;
+    };
+    ParityRow parity_row(int row) const;
     // Stream for the device work of forward_into (a hipStream_t; nullptr =
     // the default stream).
     void set_stream(void* stream) noexcept { stream_ = stream; }
@@ -154,9 +160,7 @@ private:
     layers::Linear gate_proj_;
     layers::Linear up_proj_;
     layers::Linear down_proj_;
-    bool parity_diagnostic_ = false;
-    void parity_check_attention(const Tensor& queries, const Tensor& context, const memory::SequenceState& state,
-                                const memory::BlockPool& pool) const;
+    bool last_pass_prefill_ = false;   // which scratch parity_row reads
     void* stream_ = nullptr;
     // Persistent GPU scratchpads, allocated by to(Device::GPU) and reused by
     // every forward_into; a block serves one request at a time.

@@ -510,6 +510,16 @@ int skv_gather_blocks(const uint16_t* pool, int64_t total_blocks,
                       const int32_t* table, int num_blocks,
                       int64_t block_elems, uint16_t* dst, void* stream);
 
+/* Copy `count` chunks of `chunk_bytes` bytes (a multiple of 16; every pointer
+ * 16-byte aligned, no chunk overlapping another's destination): chunk i from
+ * src[i] to dst[i].  src and dst are device arrays of `count` device pointers;
+ * count up to 65,535.  One launch.  The Generator saves the K/V blocks a
+ * generation will write with it and puts them back afterwards.
+ * Replaces: the deep copies of every pool that the reference's SequenceGuard
+ * makes and restores (src/generation/generator.cpp:347-371, the BlockPool
+ * copy constructor src/memory/block_pool.cpp:118-145). */
+int skv_copy_chunks(const void* const* src, void* const* dst, int count, size_t chunk_bytes, void* stream);
+
 /* ---- HIP graphs of recorded launches ----------------------------------------
  * For a sequence of launches replayed many times with the same arguments (the
  * greedy decode step of Generator, whose per-token values live in device

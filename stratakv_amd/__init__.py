@@ -100,6 +100,7 @@ _PROTOS = {
     "skv_paged_attention_decode": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32,
                                           _i32, _f32, _vp, _sz, _vp]),
     "skv_gather_blocks": (_i32, [_vp, _i64, _vp, _i32, _i64, _vp, _vp]),
+    "skv_copy_chunks": (_i32, [_vp, _vp, _i32, _sz, _vp]),
     "skv_paged_block_checksum": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32,
                                         _vp, _vp]),
     "skv_stream_read_checksum": (_i32, [_vp, _i64, _vp, _vp]),

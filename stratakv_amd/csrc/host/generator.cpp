@@ -25,6 +25,7 @@
 #include <utility>
 
 #include "abi_check.h"
+#include "parity_model.h"
 
 namespace stratakv {
 namespace generation {
@@ -224,13 +225,16 @@ Generator::Generator(GeneratorConfig config, io::WeightMap weights)
     // The layers run one after another on one stream: one prefill scratch serves them all.
     const auto scratch = std::make_shared<models::TransformerBlock::PrefillScratch>();
     for (auto& b : blocks_) b.share_prefill_scratch(scratch);
-    // STRATAKV_PARITY=1 (src/generation/generator.cpp:33-36): the reference
-    // compares every layer with its CPU copy; this build has no CPU layers and
-    // runs each block's attention check instead.
+    // STRATAKV_PARITY=1 (src/generation/generator.cpp:33-36, 485-490): every
+    // layer of every position is compared with a host model of the layer
+    // (parity_model.h); steps run one kernel at a time so each layer's output
+    // can be read.
     if (const char* v = std::getenv("STRATAKV_PARITY"); v != nullptr && std::strcmp(v, "1") == 0) {
-        std::fprintf(stderr, "[PARITY] per-layer CPU comparison is not available in this build; "
-                             "checking each layer's paged attention on the first token\n");
-        for (auto& b : blocks_) b.set_parity_diagnostic(true);
+        parity_ = std::make_unique<detail::ParityModel>(blocks_, *final_norm_, *lm_head_, *embeddings_);
+        graph_replay_ = false;
+        std::fprintf(stderr, "[PARITY] host model of %zu layers (double precision, bf16 K/V cache as the pools "
+                             "hold it); decode steps launched one kernel at a time\n",
+                     parity_->num_layers());
     }
     // STRATAKV_GRAPH_REPLAY=0: every decode step launched one kernel at a time
     // (as set_graph_replay(false)).  For profiling: under rocprofv3's kernel
@@ -239,6 +243,7 @@ Generator::Generator(GeneratorConfig config, io::WeightMap weights)
     // outside this library, so kernel traces are taken with replay off.
     if (const char* v = std::getenv("STRATAKV_GRAPH_REPLAY"); v != nullptr && std::strcmp(v, "0") == 0)
         graph_replay_ = false;
+    if (parity_) graph_replay_ = false;
     hidden_.emplace(std::vector<std::size_t>{1, h}, DataType::FP32, Device::GPU);
     normed_.emplace(std::vector<std::size_t>{1, h}, DataType::FP32, Device::GPU);
     logits_.emplace(std::vector<std::size_t>{1, config_.vocab_size}, DataType::FP32, Device::GPU);
@@ -259,10 +264,13 @@ Generator::~Generator() {
     if (step_state_) (void)skv_free(step_state_);
     if (rope_table_) (void)skv_free(rope_table_);
     if (capture_stream_) (void)skv_stream_destroy(capture_stream_);
+    if (kv_saved_) (void)skv_free(kv_saved_);
+    if (kv_chunk_ptrs_) (void)skv_free(kv_chunk_ptrs_);
+    if (kv_chunk_host_) (void)skv_host_free(kv_chunk_host_);
 }
 
 void Generator::set_graph_replay(bool enabled) {
-    graph_replay_ = enabled;
+    graph_replay_ = enabled && !parity_;
     if (!enabled) {
         (void)skv_stream_synchronize(stream_);
         release_step_graph();
@@ -424,8 +432,10 @@ void Generator::begin_sequence(std::size_t tokens) {
         flags_ = static_cast<std::int32_t*>(d);
         flags_capacity_ = 2 * tokens + 2;
     }
+    if (parity_) parity_->reset();
     saved_free_lists_.resize(pools_.size());
     for (std::size_t l = 0; l < pools_.size(); ++l) saved_free_lists_[l] = pools_[l].free_list();
+    save_kv_blocks(blocks);
     std::size_t done = 0;
     try {
         for (; done < pages_.size(); ++done) {
@@ -439,12 +449,89 @@ void Generator::begin_sequence(std::size_t tokens) {
     }
 }
 
+// The blocks each layer's pool will hand out for `blocks` blocks of one
+// sequence (the top of its free stack, in pop order), K and V, copied aside.
+void Generator::save_kv_blocks(std::size_t blocks) {
+    kv_chunks_ = 0;
+    if (pools_.empty() || blocks == 0) return;
+    const std::size_t elems = pools_.front().block_elements();
+    const std::size_t n = 2 * pools_.size() * blocks;
+    kv_chunk_bytes_ = elems * sizeof(std::uint16_t);
+    if (n > kv_chunks_capacity_) {
+        if (kv_saved_) (void)skv_free(kv_saved_);
+        if (kv_chunk_ptrs_) (void)skv_free(kv_chunk_ptrs_);
+        if (kv_chunk_host_) (void)skv_host_free(kv_chunk_host_);
+        kv_saved_ = nullptr;
+        kv_chunk_ptrs_ = nullptr;
+        kv_chunk_host_ = nullptr;
+        kv_chunks_capacity_ = 0;
+        void* d = nullptr;
+        detail::check(skv_malloc(&d, n * kv_chunk_bytes_), "Generator: K/V save");
+        kv_saved_ = d;
+        detail::check(skv_malloc(&d, 2 * n * sizeof(void*)), "Generator: K/V save");
+        kv_chunk_ptrs_ = static_cast<void**>(d);
+        detail::check(skv_host_alloc(&d, 2 * n * sizeof(void*)), "Generator: K/V save");
+        kv_chunk_host_ = static_cast<void**>(d);
+        kv_chunks_capacity_ = n;
+    }
+    std::size_t c = 0;
+    for (std::size_t l = 0; l < pools_.size(); ++l) {
+        const std::vector<int>& free = saved_free_lists_[l];
+        for (std::size_t j = 0; j < blocks && j < free.size(); ++j) {
+            const std::size_t id = static_cast<std::size_t>(free[free.size() - 1 - j]);
+            for (std::uint16_t* pool : {pools_[l].key_cache(), pools_[l].value_cache()}) {
+                kv_chunk_host_[c] = pool + id * elems;
+                kv_chunk_host_[n + c] = static_cast<char*>(kv_saved_) + c * kv_chunk_bytes_;
+                ++c;
+            }
+        }
+    }
+    // c <= n: the halves keep their n-entry offsets.
+    for (std::size_t i = c; i < n; ++i) kv_chunk_host_[i] = kv_chunk_host_[n + i] = nullptr;
+    detail::check(skv_memcpy_h2d_async(kv_chunk_ptrs_, kv_chunk_host_, 2 * n * sizeof(void*), stream_),
+                  "Generator: K/V save");
+    kv_half_ = n;
+    kv_chunks_ = c;
+    const int rc = copy_kv_chunks(0, n);
+    if (rc == SKV_ERR_UNSUPPORTED) {
+        for (std::size_t i = 0; i < c; ++i)
+            detail::check(skv_memcpy_d2d(kv_chunk_host_[n + i], kv_chunk_host_[i], kv_chunk_bytes_, stream_),
+                          "Generator: K/V save");
+    } else if (rc != SKV_OK) {
+        kv_chunks_ = 0;
+        detail::check(rc, "Generator: K/V save");
+    }
+}
+
+// The kv_chunks_ chunks from the addresses at offset `from` of kv_chunk_ptrs_
+// to those at offset `to`, in launches of at most 65,535 chunks;
+// SKV_ERR_UNSUPPORTED when the chunk size is not a multiple of 16 bytes.
+int Generator::copy_kv_chunks(std::size_t from, std::size_t to) noexcept {
+    if (kv_chunk_bytes_ % 16 != 0) return SKV_ERR_UNSUPPORTED;
+    constexpr std::size_t kMaxChunks = 65535;
+    for (std::size_t i = 0; i < kv_chunks_; i += kMaxChunks) {
+        const int count = static_cast<int>(std::min(kMaxChunks, kv_chunks_ - i));
+        if (int rc = skv_copy_chunks(const_cast<const void* const*>(kv_chunk_ptrs_ + from + i),
+                                     kv_chunk_ptrs_ + to + i, count, kv_chunk_bytes_, stream_))
+            return rc;
+    }
+    return SKV_OK;
+}
+
 // Frees sequence 0 in every layer and puts each pool's free list back as it
 // was before begin_sequence, so consecutive generations use the same block
 // ids in the same order, as after the reference's SequenceGuard restore
 // (src/generation/generator.cpp:347-371, 639).
 void Generator::end_sequence() noexcept {
     (void)skv_stream_synchronize(stream_);
+    // The saved K/V blocks back into the pools, complete before generate returns.
+    if (kv_chunks_ > 0) {
+        if (copy_kv_chunks(kv_half_, 0) != SKV_OK)
+            for (std::size_t i = 0; i < kv_chunks_; ++i)
+                (void)skv_memcpy_d2d(kv_chunk_host_[i], kv_chunk_host_[kv_half_ + i], kv_chunk_bytes_, stream_);
+        (void)skv_stream_synchronize(stream_);
+        kv_chunks_ = 0;
+    }
     last_tables_.assign(pages_.size(), {});
     for (std::size_t l = 0; l < pages_.size(); ++l) {
         try {
@@ -465,9 +552,19 @@ void Generator::step(int in_index, float* logits, std::int32_t* flags) {
     auto* x = static_cast<float*>(hidden_->raw_data());
     detail::check(skv_embedding_f32(embeddings_->raw_data(), dtype, vocab, h, ids_, in_index, x, flags, stream_),
                   "Generator: embedding");
-    for (std::size_t l = 0; l < blocks_.size(); ++l)
+    std::vector<float> gpu_embedding;
+    std::vector<std::vector<float>> gpu_layers;
+    std::optional<models::TransformerBlock::ParityRow> l0;
+    if (parity_ && in_index == 0) gpu_embedding = parity_download(x, config_.hidden_dim);
+    for (std::size_t l = 0; l < blocks_.size(); ++l) {
         blocks_[l].forward_into(*hidden_, *hidden_, 0, pages_[l], pools_[l], true);
+        if (parity_) {
+            if (l == 0 && in_index == 0) l0 = blocks_[0].parity_row(0);
+            gpu_layers.push_back(parity_download(x, config_.hidden_dim));
+        }
+    }
     if (logits != nullptr) logits_of(x, logits);
+    if (parity_) parity_pass(in_index, 1, gpu_embedding, gpu_layers, l0 ? &*l0 : nullptr);
 }
 
 void Generator::prompt_pass(std::size_t P, float* logits, std::int32_t* flags) {
@@ -483,9 +580,92 @@ void Generator::prompt_pass(std::size_t P, float* logits, std::int32_t* flags) {
                                              static_cast<int>(std::min(kEmbedRows, P - i)),
                                              rows + i * config_.hidden_dim, flags, stream_),
                       "Generator: embedding");
-    for (std::size_t l = 0; l < blocks_.size(); ++l)
+    std::vector<float> gpu_embedding;
+    std::vector<std::vector<float>> gpu_layers;
+    std::optional<models::TransformerBlock::ParityRow> l0;
+    if (parity_) gpu_embedding = parity_download(rows, config_.hidden_dim);
+    for (std::size_t l = 0; l < blocks_.size(); ++l) {
         blocks_[l].prefill_into(*prompt_rows_, *prompt_rows_, 0, pages_[l], pools_[l]);
+        if (parity_) {
+            // Layer 0's scratch holds row 0's ops when the prompt was one chunk.
+            if (l == 0 && P <= static_cast<std::size_t>(blocks_[0].prefill_chunk_rows()))
+                l0 = blocks_[0].parity_row(0);
+            gpu_layers.push_back(parity_download(rows, P * config_.hidden_dim));
+        }
+    }
     logits_of(rows + (P - 1) * config_.hidden_dim, logits);
+    if (parity_) parity_pass(0, P, gpu_embedding, gpu_layers, l0 ? &*l0 : nullptr);
+}
+
+std::vector<float> Generator::parity_download(const float* device, std::size_t count) {
+    std::vector<float> v(count);
+    detail::check(skv_stream_synchronize(stream_), "Generator: parity");
+    detail::check(skv_memcpy_d2h(v.data(), device, count * sizeof(float), nullptr), "Generator: parity");
+    return v;
+}
+
+namespace {
+
+// One op of layer 0 in the reference's report format
+// (src/models/transformer_block.cpp:63-80).
+void parity_op(const char* name, const std::vector<float>& gpu, const std::vector<double>& cpu) {
+    if (gpu.empty() || cpu.empty()) return;
+    auto at = [](const auto& v, std::size_t i) { return i < v.size() ? static_cast<double>(v[i]) : 0.0; };
+    std::fprintf(stderr,
+                 "[PARITY L0] %s: max_diff = %.9g, gpu_sample[0..2] = [%.9g, %.9g, %.9g], "
+                 "cpu_sample[0..2] = [%.9g, %.9g, %.9g]\n",
+                 name, detail::max_abs_diff(gpu, cpu), at(gpu, 0), at(gpu, 1), at(gpu, 2), at(cpu, 0), at(cpu, 1),
+                 at(cpu, 2));
+}
+
+}  // namespace
+
+void Generator::parity_pass(int first, std::size_t rows, const std::vector<float>& gpu_embedding,
+                            const std::vector<std::vector<float>>& gpu,
+                            const models::TransformerBlock::ParityRow* l0) {
+    const std::size_t H = config_.hidden_dim;
+    for (std::size_t r = 0; r < rows; ++r) {
+        const int position = first + static_cast<int>(r);
+        std::vector<double> x = parity_->embedding(host_ids_[position]);
+        if (position == 0) parity_op("embedding", gpu_embedding, x);
+        for (std::size_t l = 0; l < parity_->num_layers(); ++l) {
+            detail::HostLayerOps ops;
+            const bool report_ops = position == 0 && l == 0 && l0 != nullptr;
+            x = parity_->layer(l, x, report_ops ? &ops : nullptr);
+            if (report_ops) {
+                // The values the fused kernels leave in memory (parity_row).
+                parity_op("rope_q", l0->q, ops.q_rot);
+                parity_op("rope_k", l0->k, ops.k_rot);
+                parity_op("v_proj", l0->v, ops.v);
+                parity_op("paged_attention", l0->context, ops.context);
+                parity_op("out_proj + residual", l0->residual, ops.residual);
+                parity_op("swiglu", l0->act, ops.act);
+            }
+            const std::vector<float> g(gpu[l].begin() + static_cast<std::ptrdiff_t>(r * H),
+                                       gpu[l].begin() + static_cast<std::ptrdiff_t>((r + 1) * H));
+            std::fprintf(stderr, "[PARITY pos=%d layer=%zu] max_diff = %.9g\n", position, l,
+                         detail::max_abs_diff(g, x));
+        }
+        parity_last_ = std::move(x);
+    }
+}
+
+void Generator::parity_final(int position) {
+    const std::vector<double> norm = parity_->final_norm(parity_last_);
+    const std::vector<double> cpu = parity_->logits(norm);
+    const std::vector<float> gpu_norm = parity_download(static_cast<const float*>(normed_->raw_data()),
+                                                        config_.hidden_dim);
+    const std::vector<float> gpu = parity_download(static_cast<const float*>(logits_->raw_data()),
+                                                   config_.vocab_size);
+    std::fprintf(stderr, "[PARITY pos=%d] final_norm max_diff = %.9g\n", position,
+                 detail::max_abs_diff(gpu_norm, norm));
+    std::size_t ga = 0, ca = 0;
+    for (std::size_t i = 0; i < gpu.size() && i < cpu.size(); ++i) {
+        if (gpu[i] > gpu[ga]) ga = i;
+        if (cpu[i] > cpu[ca]) ca = i;
+    }
+    std::fprintf(stderr, "[PARITY FINAL] lm_head logits: max_diff = %.9g, gpu_argmax = %zu, cpu_argmax = %zu\n",
+                 detail::max_abs_diff(gpu, cpu), ga, ca);
 }
 
 void Generator::logits_of(const float* x, float* logits) {
@@ -543,6 +723,9 @@ std::vector<int> Generator::generate(const std::vector<int>& prompt, int max_new
         const int vocab = static_cast<int>(config_.vocab_size);
         if (P >= 2) prompt_pass(P, logits, flags_);
         else step(0, logits, flags_);
+        // The logits the first generated token is chosen from (the
+        // reference reports them at its first step, src/generation/generator.cpp:741-769).
+        if (parity_) parity_final(static_cast<int>(P) - 1);
         // Decode steps replayed from a graph where that gives the same launches.
         const bool replay = max_new_tokens >= 2 && graph_eligible(required) && prepare_step_graph(required);
         last_replayed_ = replay;

@@ -97,64 +97,37 @@ Tensor TransformerBlock::forward(const Tensor& hidden_states, int seq_id, memory
         "the hidden states to Device::GPU");
 }
 
-// The reference's STRATAKV parity diagnostic (src/models/transformer_block.cpp:
-// 63-80, 405-526) compares every op of sequence 0's first token with its CPU
-// path.  This build has no CPU forward, so it checks the op it replaces: the
-// paged attention output against a double-precision two-pass softmax over
-// the K/V read back from the pool, printed in the reference's report format.
-void TransformerBlock::parity_check_attention(const Tensor& queries, const Tensor& context,
-                                              const memory::SequenceState& state,
-                                              const memory::BlockPool& pool) const {
-    detail::check(skv_stream_synchronize(stream_), "parity diagnostic");
-    const int Hq = static_cast<int>(attention_.num_heads()), Hkv = static_cast<int>(attention_.num_kv_heads());
-    const int hd = static_cast<int>(attention_.head_dim()), bs = pool.block_size();
-    const int L = state.sequence_length;
-    std::vector<float> q(static_cast<std::size_t>(Hq) * hd), gpu(q.size());
-    detail::check(skv_memcpy_d2h(q.data(), queries.raw_data(), q.size() * sizeof(float), nullptr), "parity diagnostic");
-    detail::check(skv_memcpy_d2h(gpu.data(), context.raw_data(), gpu.size() * sizeof(float), nullptr),
-                  "parity diagnostic");
-    const std::size_t blk = pool.block_elements();
-    const std::size_t nb = static_cast<std::size_t>((L + bs - 1) / bs);
-    std::vector<std::uint16_t> k(nb * blk), v(nb * blk);
-    for (std::size_t i = 0; i < nb; ++i) {
-        const std::size_t off = static_cast<std::size_t>(state.physical_blocks[i]) * blk;
-        detail::check(skv_memcpy_d2h(k.data() + i * blk, pool.key_cache() + off, blk * 2, nullptr), "parity diagnostic");
-        detail::check(skv_memcpy_d2h(v.data() + i * blk, pool.value_cache() + off, blk * 2, nullptr), "parity diagnostic");
-    }
-    auto widen = [](std::uint16_t b) {
-        const std::uint32_t bits = static_cast<std::uint32_t>(b) << 16;
-        float f;
-        std::memcpy(&f, &bits, sizeof f);
-        return static_cast<double>(f);
+TransformerBlock::ParityRow TransformerBlock::parity_row(int row) const {
+    detail::check(skv_stream_synchronize(stream_), "parity_row");
+    const std::size_t q_dim = attention_.num_heads() * attention_.head_dim();
+    const std::size_t kv_dim = attention_.num_kv_heads() * attention_.head_dim();
+    const std::size_t inter = gate_proj_.output_dim();
+    auto copy = [&](const std::optional<Tensor>& t, std::size_t dim) {
+        std::vector<float> v;
+        if (!t || row < 0 || static_cast<std::size_t>(row) * dim + dim > t->num_elements()) return v;
+        v.resize(dim);
+        detail::check(skv_memcpy_d2h(v.data(), static_cast<const float*>(t->raw_data()) + row * dim,
+                                     dim * sizeof(float), nullptr),
+                      "parity_row");
+        return v;
     };
-    auto row = [&](int t, int kvh) { return (static_cast<std::size_t>(t) * Hkv + kvh) * hd; };  // within the gathered blocks
-    const double scale = 1.0 / std::sqrt(static_cast<double>(hd));
-    std::vector<float> cpu(gpu.size());
-    std::vector<double> sc(static_cast<std::size_t>(L));
-    for (int h = 0; h < Hq; ++h) {
-        const int kvh = h / (Hq / Hkv);
-        double mx = -INFINITY;
-        for (int t = 0; t < L; ++t) {
-            double d = 0.0;
-            for (int e = 0; e < hd; ++e) d += q[static_cast<std::size_t>(h) * hd + e] * widen(k[row(t, kvh) + e]);
-            sc[t] = d * scale;
-            mx = std::max(mx, sc[t]);
-        }
-        double den = 0.0;
-        for (int t = 0; t < L; ++t) den += (sc[t] = std::exp(sc[t] - mx));
-        for (int e = 0; e < hd; ++e) {
-            double o = 0.0;
-            for (int t = 0; t < L; ++t) o += sc[t] / den * widen(v[row(t, kvh) + e]);
-            cpu[static_cast<std::size_t>(h) * hd + e] = static_cast<float>(o);
-        }
+    ParityRow r;
+    if (last_pass_prefill_ && pf_) {
+        r.q = copy(pf_->queries, q_dim);
+        r.k = copy(pf_->keys, kv_dim);
+        r.v = copy(pf_->values, kv_dim);
+        r.context = copy(pf_->context, q_dim);
+        r.residual = copy(pf_->residual, hidden_dim_);
+        r.act = copy(pf_->act, inter);
+    } else if (row == 0) {
+        r.q = copy(query_workspace_, q_dim);
+        r.k = copy(key_workspace_, kv_dim);
+        r.v = copy(value_workspace_, kv_dim);
+        r.context = copy(context_workspace_, q_dim);
+        r.residual = copy(down_workspace_, hidden_dim_);   // h = input + o_proj
+        r.act = copy(gate_workspace_, inter);              // swiglu(gate, up)
     }
-    float max_diff = 0.0f;
-    for (std::size_t i = 0; i < gpu.size(); ++i) max_diff = std::max(max_diff, std::fabs(gpu[i] - cpu[i]));
-    std::fprintf(stderr,
-                 "[PARITY L0] paged_attention: max_diff = %.9g, gpu_sample[0..2] = [%.9g, %.9g, %.9g], "
-                 "cpu_sample[0..2] = [%.9g, %.9g, %.9g]\n",
-                 max_diff, gpu[0], gpu.size() > 1 ? gpu[1] : 0.0f, gpu.size() > 2 ? gpu[2] : 0.0f, cpu[0],
-                 cpu.size() > 1 ? cpu[1] : 0.0f, cpu.size() > 2 ? cpu[2] : 0.0f);
+    return r;
 }
 
 // forward_into's device work with the position, context length and block
@@ -163,6 +136,7 @@ void TransformerBlock::parity_check_attention(const Tensor& queries, const Tenso
 bool TransformerBlock::forward_into_at(const Tensor& hidden_states, Tensor& output, const std::int32_t* step,
                                        const float* rope_cos_sin, int rope_positions, const int* device_table,
                                        int table_capacity, memory::BlockPool& block_pool) {
+    last_pass_prefill_ = false;
     if (hidden_states.ndim() != 2 || hidden_states.shape()[0] != 1 || hidden_states.shape()[1] != hidden_dim_ ||
         output.shape() != hidden_states.shape() || output.device() != Device::GPU ||
         hidden_states.device() != Device::GPU || hidden_states.dtype() != DataType::FP32 ||
@@ -252,6 +226,7 @@ bool TransformerBlock::forward_into_at(const Tensor& hidden_states, Tensor& outp
 void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output, int seq_id,
                                     memory::PageTable& page_table, memory::BlockPool& block_pool,
                                     bool append_tokens) {
+    last_pass_prefill_ = false;
     // Validation in the order and with the messages of
     // src/models/transformer_block.cpp:338-394.
     if (hidden_states.ndim() != 2 || hidden_states.shape()[1] != hidden_dim_ ||
@@ -378,8 +353,9 @@ void TransformerBlock::forward_into(const Tensor& hidden_states, Tensor& output,
                       1.0f / std::sqrt(static_cast<float>(head_dim)), ws.raw_data(),
                       ws.num_elements() * ws.element_size(), s),
                   "forward_into: KV append + paged attention");
-    if (parity_diagnostic_ && seq_id == 0 && append_tokens && logical_position == 0)
-        parity_check_attention(queries, context, state, block_pool);
+    // The blocks that attention read: every block of the context.
+    attention_.last_blocks_visited_ = std::min<std::size_t>(
+        state.physical_blocks.size(), static_cast<std::size_t>((context_len + block_size - 1) / block_size));
 
     // o_proj + residual: reads hidden_states before output is written
     // (aliasing-safe).  down holds h = hidden + attention output.
@@ -578,6 +554,7 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
     float* act = fp(*pf_->act);
     auto* meta = static_cast<std::int32_t*>(pf_->meta->raw_data());
 
+    last_pass_prefill_ = true;
     for (int c0 = 0; c0 < tokens; c0 += chunk) {
         const int n = std::min(chunk, tokens - c0);
         const float* x = cfp(hidden_states) + static_cast<std::size_t>(c0) * hidden;
@@ -640,6 +617,7 @@ void TransformerBlock::prefill_into(const Tensor& hidden_states, Tensor& output,
                                         num_heads, num_kv_heads, head_dim, block_size,
                                         1.0f / std::sqrt(static_cast<float>(head_dim)), ctx, s),
                       "prefill_into: paged prefill attention");
+        attention_.last_blocks_visited_ = static_cast<std::size_t>(nblocks);
 
         // o_proj + residual (reads x before y is written: aliasing-safe).
         if (!((use.o && fused(api->linear_residual(ctx, n, wo.weight().raw_data(), wdtype(wo), stride_k(wo),

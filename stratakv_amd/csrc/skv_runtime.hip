@@ -94,6 +94,17 @@ __global__ void gather_blocks_kernel(const uint16_t* __restrict__ pool, int64_t 
         out[e] = ok ? in[e] : uint16_t(0);
 }
 
+// Chunk i: bytes [0, chunk_bytes) of src[i] to dst[i] (16-byte aligned, a
+// multiple of 16 bytes); one workgroup per chunk (the y dimension) and slice.
+__global__ __launch_bounds__(256) void copy_chunks_kernel(const void* const* __restrict__ src,
+                                                          void* const* __restrict__ dst, int64_t chunk16) {
+    const uint4* in = static_cast<const uint4*>(src[blockIdx.y]);
+    uint4* out = static_cast<uint4*>(dst[blockIdx.y]);
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < chunk16;
+         e += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        out[e] = in[e];
+}
+
 // Up to kWriteI32Max int32 values carried in the kernel arguments (copied at
 // launch, so the caller's host array is free as soon as the call returns).
 constexpr int kWriteI32Max = 16;
@@ -370,6 +381,18 @@ int skv_gather_blocks(const uint16_t* pool, int64_t total_blocks, const int32_t*
     gather_blocks_kernel<<<dim3(gx, num_blocks), 256, 0, static_cast<hipStream_t>(stream)>>>(
         pool, total_blocks, table, num_blocks, block_elems, dst);
     return check_launch("gather_blocks_kernel");
+}
+
+int skv_copy_chunks(const void* const* src, void* const* dst, int count, size_t chunk_bytes, void* stream) {
+    if (count == 0) return SKV_OK;
+    SKV_REQUIRE(src && dst, "skv_copy_chunks: NULL pointer array");
+    SKV_REQUIRE(count > 0 && count <= 65535 && chunk_bytes > 0 && chunk_bytes % 16 == 0,
+                "skv_copy_chunks: invalid sizes (count=%d, chunk_bytes=%zu)", count, chunk_bytes);
+    const int64_t chunk16 = static_cast<int64_t>(chunk_bytes / 16);
+    const unsigned gx = static_cast<unsigned>(std::min<int64_t>(cdiv<int64_t>(chunk16, 256), 64));
+    copy_chunks_kernel<<<dim3(gx, static_cast<unsigned>(count)), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        src, dst, chunk16);
+    return check_launch("copy_chunks_kernel");
 }
 
 int skv_graph_begin_capture(void* stream) {

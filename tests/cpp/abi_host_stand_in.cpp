@@ -36,6 +36,7 @@ extern "C" {
 int skv_argmax_at_f32(const float*, int, int32_t*, const int32_t*, int32_t*, const int32_t*, void*) { return fail("skv_argmax_at_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
 int skv_add_f32(float*, const float*, int, void*) { return fail("skv_add_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
+int skv_fill_normal_bf16(uint16_t*, size_t, uint64_t, uint64_t, void*) { return fail("skv_fill_normal_bf16: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
 int skv_check_finite(const void*, int, size_t, int32_t*, void*) { return fail("skv_check_finite: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
@@ -130,6 +131,14 @@ int skv_malloc(void** ptr, size_t bytes) {
 }
 
 int skv_memcpy_d2d(void* dst, const void* src, size_t bytes, void*) { return copy(dst, src, bytes); }
+
+int skv_copy_chunks(const void* const* src, void* const* dst, int count, size_t chunk_bytes, void*) {
+    if (count == 0) return SKV_OK;
+    if (!src || !dst || count < 0 || chunk_bytes % 16 != 0) return fail("skv_copy_chunks: invalid arguments");
+    for (int i = 0; i < count; ++i)
+        if (int rc = copy(dst[i], src[i], chunk_bytes)) return rc;
+    return SKV_OK;
+}
 
 int skv_memcpy_d2h(void* dst, const void* src, size_t bytes, void*) { return copy(dst, src, bytes); }
 

@@ -165,6 +165,7 @@ struct GenArgs {
     long long seed = -1;  // >= 0: Generator::seed_sampler
     int first_max = -1;   // >= 0: max_new of the first call (later calls use MAX_NEW)
     bool eager = false;   // Generator::set_graph_replay(false)
+    bool check_pools = false;   // fill the pools with a pattern, report whether generate leaves them unchanged
     std::vector<int> tokens;
 };
 
@@ -185,6 +186,7 @@ GenArgs parse_gen(int first, int argc, char** argv) {
         else if (s == "--seed") a.seed = std::stoll(argv[++i]);
         else if (s == "--first-max") a.first_max = std::stoi(argv[++i]);
         else if (s == "--eager") a.eager = true;
+        else if (s == "--check-pools") a.check_pools = true;
     }
     for (; i < argc; ++i) a.tokens.push_back(std::stoi(argv[i]));
     return a;
@@ -219,6 +221,35 @@ int cmd_generate(int argc, char** argv) {
         generation::Generator gen(cfg, std::move(l.weights));
         if (a.seed >= 0) gen.seed_sampler(static_cast<std::uint32_t>(a.seed));
         if (a.eager) gen.set_graph_replay(false);
+        // FNV-1a over every layer's K and V pool bytes.
+        auto pools_hash = [&]() {
+            std::uint64_t hsh = 1469598103934665603ull;
+            for (std::size_t ly = 0; ly < l.dims.layers; ++ly) {
+                const memory::BlockPool& p = gen.block_pool(ly);
+                const std::size_t n = static_cast<std::size_t>(p.total_blocks()) * p.block_elements();
+                std::vector<std::uint16_t> host(n);
+                for (const std::uint16_t* pool : {p.key_cache(), p.value_cache()}) {
+                    if (skv_memcpy_d2h(host.data(), pool, n * 2, nullptr) != SKV_OK)
+                        throw std::runtime_error(skv_last_error());
+                    for (std::uint16_t v : host)
+                        for (int b = 0; b < 2; ++b) hsh = (hsh ^ ((v >> (8 * b)) & 0xFFu)) * 1099511628211ull;
+                }
+            }
+            return hsh;
+        };
+        std::uint64_t before = 0;
+        if (a.check_pools) {
+            for (std::size_t ly = 0; ly < l.dims.layers; ++ly) {
+                const memory::BlockPool& p = gen.block_pool(ly);
+                const std::size_t n = static_cast<std::size_t>(p.total_blocks()) * p.block_elements();
+                if (skv_fill_normal_bf16(const_cast<std::uint16_t*>(p.key_cache()), n, 7 + 2 * ly, 0, nullptr) ||
+                    skv_fill_normal_bf16(const_cast<std::uint16_t*>(p.value_cache()), n, 8 + 2 * ly, 0, nullptr))
+                    throw std::runtime_error(skv_last_error());
+            }
+            before = pools_hash();
+        }
+        std::vector<int> pools_unchanged;
+        std::vector<std::size_t> blocks_visited;
         std::vector<int> out;
         std::vector<std::vector<int>> runs, tables;
         std::vector<double> gen_ms;
@@ -238,6 +269,8 @@ int cmd_generate(int argc, char** argv) {
                 for (int b = 0; b < 4; ++b) hsh = (hsh ^ ((bits >> (8 * b)) & 0xFFu)) * 1099511628211ull;
             }
             logit_hashes.push_back(hsh);
+            if (a.check_pools) pools_unchanged.push_back(pools_hash() == before ? 1 : 0);
+            blocks_visited.push_back(gen.block(0).last_attention_blocks_visited());
         }
         std::printf("{\"ok\": true, \"runs\": [");
         for (std::size_t r = 0; r < runs.size(); ++r) {
@@ -256,6 +289,10 @@ int cmd_generate(int argc, char** argv) {
         std::printf("], \"logits_fnv\": [");
         for (std::size_t r = 0; r < logit_hashes.size(); ++r)
             std::printf("%s\"%016llx\"", r ? ", " : "", static_cast<unsigned long long>(logit_hashes[r]));
+        std::printf("], \"pools_unchanged\": [");
+        for (std::size_t r = 0; r < pools_unchanged.size(); ++r) std::printf("%s%d", r ? ", " : "", pools_unchanged[r]);
+        std::printf("], \"blocks_visited\": [");
+        for (std::size_t r = 0; r < blocks_visited.size(); ++r) std::printf("%s%zu", r ? ", " : "", blocks_visited[r]);
         std::printf("], \"tokens\": [");
         for (std::size_t i = 0; i < out.size(); ++i) std::printf("%s%d", i ? ", " : "", out[i]);
         std::printf("], \"load_ms\": %.3f, \"payload_bytes\": %zu, \"decode_ms\": %.3f, \"init_ms\": %.3f, "

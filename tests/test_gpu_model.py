@@ -351,20 +351,79 @@ def test_generate_repeatable_and_errors(gpu, ckpt_dir):
     assert res["tokens"] == [3, gen[0]]
 
 
-def test_parity_diagnostic_reports_attention(gpu, ckpt_dir):
-    """STRATAKV_PARITY=1: every layer's paged attention on the first token is
-    compared with a host double-precision restatement and reported on stderr
-    (src/models/transformer_block.cpp:63-80 prints the same line format)."""
+def _parity_run(path, max_new, prompt):
+    env = dict(os.environ, STRATAKV_PARITY="1")
+    p = subprocess.run([TOOL, "generate", path, str(max_new), "-1", "--", *map(str, prompt)], stdout=subprocess.PIPE,
+                       stderr=subprocess.PIPE, text=True, timeout=600, env=env)
+    res = json.loads(p.stdout.strip().splitlines()[-1])
+    assert p.returncode == 0 and res["ok"], p.stderr
+    lines = p.stderr.splitlines()
+    ops = {}
+    for line in lines:
+        if line.startswith("[PARITY L0] "):
+            name, rest = line[len("[PARITY L0] "):].split(": max_diff = ")
+            ops[name] = float(rest.split(",")[0])
+    layers = {}
+    for line in lines:
+        if line.startswith("[PARITY pos=") and " layer=" in line:
+            head, val = line.split("] max_diff = ")
+            pos, layer = head[len("[PARITY pos="):].split(" layer=")
+            layers[(int(pos), int(layer))] = float(val)
+    final = [line for line in lines if line.startswith("[PARITY FINAL] lm_head logits")]
+    return res, ops, layers, final
+
+
+@pytest.mark.parametrize("prompt_len", [1, 3])
+def test_parity_diagnostic_reports_every_layer(gpu, ckpt_dir, prompt_len):
+    """STRATAKV_PARITY=1 (src/generation/generator.cpp:33-36, 581-613): every
+    layer at every position against the host model of the layer, in the
+    reference's line format.
+    * layer 0's ops on the first token (the values the fused kernels leave in
+      memory), the embedding bit-exact;
+    * one line per position and layer, for the prompt (one step, or the
+      prompt pass over 3 rows) and every decode step that ran;
+    * the final logits the first token is chosen from, same argmax.
+    The host model keeps K/V rounded to bf16 like the pools, so the
+    differences are the fp32 arithmetic's: bounded here by 1e-3 of the
+    values' scale (a dropped term or a wrong position errs by O(1))."""
     golden = _golden("mini")
     path = _checkpoint("mini", ckpt_dir, golden)
-    env = dict(os.environ, STRATAKV_PARITY="1")
-    p = subprocess.run([TOOL, "generate", path, "4", "-1", "--", "5"], stdout=subprocess.PIPE,
-                       stderr=subprocess.PIPE, text=True, timeout=600, env=env)
-    assert p.returncode == 0 and json.loads(p.stdout.strip().splitlines()[-1])["ok"], p.stderr
-    diffs = [float(line.split("max_diff = ")[1].split(",")[0]) for line in p.stderr.splitlines()
-             if line.startswith("[PARITY L0] paged_attention: max_diff = ")]
-    assert len(diffs) == golden["checkpoint"]["layers"], p.stderr
-    assert max(diffs) < 1e-5, diffs
+    prompt = golden["prompt"][:prompt_len]
+    res, ops, layers, final = _parity_run(path, 4, prompt)
+    L = golden["checkpoint"]["layers"]
+    assert set(ops) == {"embedding", "rope_q", "rope_k", "v_proj", "paged_attention", "out_proj + residual",
+                        "swiglu"}, ops
+    assert ops["embedding"] == 0.0, ops
+    assert max(ops.values()) < 1e-3, ops
+    positions = len(res["tokens"]) - 1        # the prompt and every generated token but the last
+    assert sorted(layers) == [(p, l) for p in range(positions) for l in range(L)], sorted(layers)
+    assert max(layers.values()) < 1e-3, layers
+    assert len(final) == 1, final
+    ga, ca = (int(final[0].split(name + " = ")[1].split(",")[0]) for name in ("gpu_argmax", "cpu_argmax"))
+    assert ga == ca, final[0]
+    # The diagnostic turns graph replay off; the tokens are those of a plain run.
+    plain = tool("generate", path, 4, -1, "--", *prompt)
+    assert res["tokens"] == plain["tokens"]
+
+
+def test_generate_leaves_the_pools_unchanged(gpu, ckpt_dir):
+    """The reference's SequenceGuard puts every pool back after generate
+    (src/generation/generator.cpp:347-371, 639): with every K/V pool filled
+    with random bf16 first, the pools hash the same after each of two
+    generations (graph replay and step by step), and the attention of the
+    last step read the blocks of the whole context."""
+    golden = _golden("mini")
+    path = _checkpoint("mini", ckpt_dir, golden)
+    prompt = golden["prompt"]
+    for extra in ([], ["--eager"]):
+        res = tool("generate", path, 40, -1, "--check-pools", "--repeat", 2, *extra, "--", *prompt)
+        assert res["ok"], res
+        assert res["pools_unchanged"] == [1, 1], res
+        positions = len(res["tokens"]) - 1
+        want = -(-positions // 16)
+        # Replayed steps leave the count of the prompt's prefill_into / forward_into.
+        assert res["blocks_visited"][1] == (-(-len(prompt) // 16) if res["replayed"][1] else want), res
+        assert res["replayed"][1] == (0 if extra else res["replayed"][1])
 
 
 def test_consecutive_generations_use_the_same_blocks(gpu, ckpt_dir):
