@@ -14,14 +14,17 @@
 //   head); wavefront w owns rows 32w..32w+31 as two 16-row column groups.
 //   Every K/V byte staged in LDS serves all 256 rows.
 // * Keys are walked 64 at a time (four 16-token blocks) up to the tile's last
-//   position, through two LDS buffers: the next step's K/V are loaded into
-//   registers while the current step is computed, then stored into the other
-//   buffer; one barrier per step.  K rows are unpadded, each 16-byte chunk c
-//   of row r stored at chunk position c ^ (r % chunks per row); V rows are
-//   padded by 32 bytes.  Both make the operand reads below conflict-free (a
-//   16-byte padding of K had left half of the K reads' LDS cycles in bank
-//   conflicts).  The heaviest tiles (the latest tokens of each sequence) are
-//   scheduled first.
+//   position, through two LDS buffers, one barrier per step.  While the
+//   current step is computed, the next step's K rows go straight from memory
+//   into the other buffer (buffer_load_dwordx4 ... lds: no registers, no LDS
+//   store instruction) and its V rows into registers, converted to fp16 and
+//   stored after the compute.  K rows are unpadded, each 16-byte chunk c of
+//   row r stored at chunk position c ^ (r % chunks per row) (the DMA writes
+//   lane i's 16 bytes at position i, so lane i loads the chunk that belongs
+//   there); V rows are padded by 32 bytes.  Both make the operand reads below
+//   conflict-free (a 16-byte padding of K had left half of the K reads' LDS
+//   cycles in bank conflicts).  The heaviest tiles (the latest tokens of each
+//   sequence) are scheduled first.
 // * The step loop keeps its K/V loads in flight through the compute: they are
 //   unconditional buffer loads through a per-(wavefront, block) descriptor that
 //   spans exactly the block's existing rows (rows past the context and absent
@@ -159,6 +162,21 @@ struct PrefillLds {
         return row * KRS + (c ^ (row & (HD / 8 - 1))) * 16;
     }
 };
+
+// 16 bytes per lane from a buffer straight into LDS (buffer_load_dwordx4 ...
+// lds): lane i writes bytes [16 i, 16 i + 16) after `lds_base` (wave-uniform).
+// The host pass of the compiler has no form of this builtin, so its call sits
+// in the device pass only.
+// s_waitcnt operand for vmcnt(0) alone (gfx9 encoding: expcnt 7 and lgkmcnt 15
+// are their "don't wait" values): the wave's LDS DMA has landed.
+constexpr int kWaitVmcnt0 = 0x0F70;
+
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds_base, int voffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds_base, 16, voffset, 0,
+                                             0, 0);
+#endif
+}
 
 typedef short v4s_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -384,7 +402,17 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
         row_w[u] = 8 * (wv & 1) + u * (64 / CH) + lane / CH;   // row within the block
         voff_w[u] = static_cast<int>(row_w[u] * row_bytes + (lane % CH) * 16);
     }
-    auto load_step = [&](int s, u32x4_t (&kr)[LOADS], u32x4_t (&vr)[LOADS]) {
+    // K goes straight into LDS buffer `buf` (buffer_load ... lds): lane i of
+    // pass u writes the 16 bytes at LDS row lr0 + i / CH, chunk position
+    // i % CH, so it loads the block row's chunk (i % CH) ^ (row % CH) -- the
+    // swizzled layout, realised through the source addresses.
+    int kvoff_w[LOADS];
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+        const int lr = 16 * blk_w + row_w[u];
+        kvoff_w[u] = static_cast<int>(row_w[u] * row_bytes + (((lane % CH) ^ (lr & (CH - 1))) * 16));
+    }
+    auto load_step = [&](int s, int buf, u32x4_t (&vr)[LOADS]) {
         const int slot = 4 * s + blk_w - tb;
         const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(off_lo, slot))) |
                              static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(off_hi, slot))) << 32;
@@ -393,11 +421,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
             const_cast<unsigned char*>(reinterpret_cast<const unsigned char*>(kbase)) + off, 0, nrec, 0x00020000);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<unsigned char*>(reinterpret_cast<const unsigned char*>(vbase)) + off, 0, nrec, 0x00020000);
+        unsigned char* kb = lds + buf * Lds::BUF;
 #pragma unroll
         for (int u = 0; u < LOADS; ++u) {
-            kr[u] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, voff_w[u], 0, 0));
-            vr[u] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff_w[u], 0, 0));
+            const int lr0 = 16 * blk_w + 8 * (wv & 1) + u * (64 / CH);   // first LDS row of this pass
+            lds_dma16(rk, kb + lr0 * Lds::KRS, kvoff_w[u]);
         }
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u)
+            vr[u] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff_w[u], 0, 0));
     };
     // Rows of keys that do not exist are stored as zeros (V must not carry
     // NaN from unused slots into 0 * V).
@@ -405,13 +437,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
     // keep an absolute error below 2^-25); vmax tracks the largest |V| this
     // thread stored.
     float vmax = 0.0f;
-    auto store_step = [&](int buf, const u32x4_t (&kr)[LOADS], const u32x4_t (&vr)[LOADS]) {
+    auto store_step = [&](int buf, const u32x4_t (&vr)[LOADS]) {
         unsigned char* kb = lds + buf * Lds::BUF;
         unsigned char* vb = kb + Lds::KB;
 #pragma unroll
         for (int u = 0; u < LOADS; ++u) {
             const int lr = 16 * blk_w + row_w[u], lc = lane % CH;
-            *reinterpret_cast<u32x4_t*>(kb + Lds::k_chunk(lr, lc)) = kr[u];
             u32x4_t w;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -432,20 +463,21 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
     float lsum[2] = {0.0f, 0.0f};          // this lane's share of each row's denominator
 
     const int nsteps = cdiv(keys_end, KS);
-    u32x4_t kr[LOADS], vr[LOADS];
+    u32x4_t vr[LOADS];
     uint32_t nib_cur = 0, nib_next = 0;   // blocks of the current and next step that exist
     if (nsteps > 0) {
         nib_cur = step_nib(0);
-        load_step(0, kr, vr);
-        store_step(0, kr, vr);
+        load_step(0, 0, vr);
+        store_step(0, vr);
     }
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);   // this wave's K rows are in LDS
     __syncthreads();
     for (int st = 0; st < nsteps; ++st) {
         const int cur = st & 1;
         if (st + 1 < nsteps) {   // in flight during compute
             window(st + 1);
             nib_next = step_nib(st + 1);
-            load_step(st + 1, kr, vr);
+            load_step(st + 1, cur ^ 1, vr);
         }
         const unsigned char* kb = lds + cur * Lds::BUF;
         const unsigned char* vb = kb + Lds::KB;
@@ -550,7 +582,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_mfma_kernel(Prefil
             }
         }
 
-        if (st + 1 < nsteps) store_step(cur ^ 1, kr, vr);
+        if (st + 1 < nsteps) store_step(cur ^ 1, vr);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);   // the next step's K rows are in LDS
         __syncthreads();
         nib_cur = nib_next;
     }
