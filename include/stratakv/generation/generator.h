@@ -109,10 +109,6 @@ public:
     // step-by-step launches.  On by default; false runs every step eagerly.
     void set_graph_replay(bool enabled);
     bool graph_replay() const noexcept { return graph_replay_; }
-    // Replayed steps run each layer's attention and o_proj + residual as one
-    // launch where the geometry allows (TransformerBlock::
-    // set_fold_output_projection); the same bits either way.  On by default.
-    void set_fold_output_projection(bool enabled);
     // Whether the last generate call replayed its steps from a graph.
     bool last_generation_replayed() const noexcept { return last_replayed_; }
     // The logits left by the last generate call (those of the last token's

@@ -59,11 +59,6 @@ public:
     // Stream for the device work of forward_into (a hipStream_t; nullptr =
     // the default stream).
     void set_stream(void* stream) noexcept { stream_ = stream; }
-    // forward_into_at folds o_proj + residual into the attention launch where
-    // it can (on by default); false keeps them separate launches.  No
-    // counterpart in the reference.
-    void set_fold_output_projection(bool enabled) noexcept { fold_output_projection_ = enabled; }
-    bool fold_output_projection() const noexcept { return fold_output_projection_; }
 
     // GPU tensors: allocates the result and runs forward_into.  CPU tensors:
     // the reference's CPU path, not provided by this build (throws).
@@ -127,9 +122,6 @@ public:
     // same kernels as forward_into on bf16 or fp32 output-major weights, so with
     // equal inputs the outputs are equal to forward_into's bits whenever the
     // attention takes the same path (a table capacity of at most 16 blocks).
-    // Where skv_paged_decode_append_oproj has a kernel for the geometry (and
-    // fold_output_projection() is on), the attention and o_proj + residual run
-    // as that one launch, with the bits of the two launches.
     // Returns false, having launched nothing, when a projection's weights are
     // not in the fused kernels' layout (forward_into then runs separate kernels).
     // No counterpart in the reference.
@@ -170,7 +162,6 @@ private:
     layers::Linear down_proj_;
     bool last_pass_prefill_ = false;   // which scratch parity_row reads
     void* stream_ = nullptr;
-    bool fold_output_projection_ = true;
     // Persistent GPU scratchpads, allocated by to(Device::GPU) and reused by
     // every forward_into; a block serves one request at a time.
     std::optional<Tensor> normalized_input_workspace_;

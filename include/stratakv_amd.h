@@ -214,31 +214,6 @@ int skv_paged_decode_append_noalloc(const void* q, int q_dtype,
                                     int num_q_heads, int num_kv_heads, int head_dim,
                                     int block_size, float scale, float* out, void* stream);
 
-/* One sequence's decode attention with the output projection and its
- * residual add folded into the same launch:
- *   context = skv_paged_decode_append(q, k_new, v_new, ..., num_seqs = 1)
- *   out     = context W_o + o_bias + residual      (out may alias residual)
- * with both results bit-identical to those two calls (skv_paged_decode_append
- * with fp32 q and fp32 k_new / v_new, then skv_linear_residual_f32 with
- * in_dim = num_q_heads * head_dim, out_dim = hidden) on the same stream, and
- * the new K/V row stored as they store it.  context_len is a device int.
- * Returns SKV_ERR_UNSUPPORTED, launching nothing, unless: block_size 16,
- * head_dim 64, (num_q_heads, num_kv_heads) = (32, 4) or (8, 2),
- * max_blocks <= 16, bf16 output-major W_o rows (o_stride_k == 1,
- * o_stride_n >= in_dim, 16-byte aligned rows) and 512 <= in_dim <= 2048, with
- * 16-byte aligned q, k_new, v_new and context; callers then make the two
- * calls.
- * Replaces: paged_attention_decode_cuda followed by the o_proj
- * Linear::forward_into and add_inplace_cuda in forward_into
- * (src/models/transformer_block.cpp:511-541). */
-int skv_paged_decode_append_oproj(const float* q, const float* k_new, const float* v_new,
-                                  uint16_t* k_pool, uint16_t* v_pool, int64_t total_blocks,
-                                  const int32_t* block_table, int max_blocks, const int32_t* context_len,
-                                  int num_q_heads, int num_kv_heads, int head_dim, int block_size,
-                                  float scale, const void* o_weight, int o_dtype, int64_t o_stride_k,
-                                  int64_t o_stride_n, const float* o_bias, const float* residual,
-                                  int hidden, float* context, float* out, void* stream);
-
 /* Chunked prefill attention over the paged cache.  The query rows
  * seq_offsets[b] .. seq_offsets[b+1]-1 of q ([num_tokens][num_q_heads][head_dim],
  * q_dtype) are sequence b's chunk: the last n_b positions of its

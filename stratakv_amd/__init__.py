@@ -91,10 +91,7 @@ _PROTOS = {
                                        _i32, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _sz, _vp]),
     "skv_paged_decode_append_noalloc": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _i32,
                                                _vp, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _vp]),
-    "skv_paged_decode_append_oproj": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _vp, _i32, _vp, _i32, _i32, _i32,
-                                             _i32, _f32, _vp, _i32, _i64, _i64, _vp, _vp, _i32, _vp, _vp,
-                                             _vp]),
-    "skv_paged_attention_decode_append":(_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _vp,
+    "skv_paged_attention_decode_append": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _vp,
                                                  _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz,
                                                  _vp]),
     "skv_paged_prefill": (_i32, [_vp, _i32, _vp, _vp, _i64, _vp, _i32, _vp, _vp, _i32, _i32, _i32,

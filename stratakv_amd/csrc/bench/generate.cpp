@@ -6,12 +6,10 @@
 // Weights: bf16 N(0, 0.02) generated on the device from a seed (norm gammas
 // 1.0), or a safetensors checkpoint loaded with io::load_safetensors_device
 // (then the load is timed too).  Prints one JSON line.
-//   bench_generate [--checkpoint PATH] [--repeat N] [--new N] [--prompt N] [--eager] [--unfolded]
+//   bench_generate [--checkpoint PATH] [--repeat N] [--new N] [--prompt N] [--eager]
 // --prompt N: N prompt tokens (the 16 below, then ids from a fixed 32-bit LCG)
 // instead of 16, to time the prompt pass on long prompts.  --eager: every decode
 // step launched one kernel at a time (Generator::set_graph_replay(false)).
-// --unfolded: replayed steps keep attention and o_proj + residual as separate
-// launches (Generator::set_fold_output_projection(false)).
 // Also reported: the process's first generation (first_call_ms) and, for a
 // prompt one token shorter than any run before, its first and second
 // generation of one token (unseen_length_*_ms).
@@ -84,7 +82,7 @@ int main(int argc, char** argv) {
     try {
         std::string checkpoint;
         int repeat = 5, n_new = 128, n_prompt = 16;
-        bool eager = false, unfolded = false;
+        bool eager = false;
         for (int i = 1; i < argc; ++i) {
             const std::string a = argv[i];
             if (a == "--checkpoint" && i + 1 < argc) checkpoint = argv[++i];
@@ -92,7 +90,6 @@ int main(int argc, char** argv) {
             else if (a == "--new" && i + 1 < argc) n_new = std::max(1, std::atoi(argv[++i]));
             else if (a == "--prompt" && i + 1 < argc) n_prompt = std::max(1, std::atoi(argv[++i]));
             else if (a == "--eager") eager = true;
-            else if (a == "--unfolded") unfolded = true;
         }
         int devices = 0;
         if (skv_device_count(&devices) != SKV_OK || devices == 0) {
@@ -113,7 +110,6 @@ int main(int argc, char** argv) {
         generation::GeneratorConfig cfg(kHidden, kInter, kHeads, kKv, kLayers, 1024, 16, kVocab, -1);
         generation::Generator gen(cfg, std::move(weights));
         if (eager) gen.set_graph_replay(false);
-        if (unfolded) gen.set_fold_output_projection(false);
         // 16 prompt ids as numpy default_rng(42).integers(0, 32000, 16).
         std::vector<int> prompt = {2856, 24766, 20946, 14044, 13856, 27475, 2750, 22315,
                                    6447, 3013,  16847, 31219, 23544, 24356, 22959, 25154};
@@ -151,12 +147,12 @@ int main(int argc, char** argv) {
                     "\"decode_tokens_per_s\": %.2f, \"init_ms\": %.2f, \"load_ms\": %.2f, "
                     "\"load_payload_bytes\": %zu, \"load_decode_ms\": %.2f, \"checkpoint\": %s, \"repeat\": %d, "
                     "\"graph_replay\": %s, \"first_call_ms\": %.4f, \"unseen_length_first_ms\": %.4f, "
-                    "\"unseen_length_second_ms\": %.4f, \"oproj_folded\": %s}\n",
+                    "\"unseen_length_second_ms\": %.4f}\n",
                     kLayers, prompt.size(), out.size() - prompt.size(), ms,
                     (out.size() - prompt.size()) / (ms / 1e3), ms1, per_token, 1e3 / per_token,
                     gen.initialization_ms(), load_ms, bd.payload_bytes, bd.tensor_decode_ms,
                     checkpoint.empty() ? "false" : "true", repeat, replayed ? "true" : "false", first_call_ms,
-                    unseen_first_ms, unseen_second_ms, unfolded ? "false" : "true");
+                    unseen_first_ms, unseen_second_ms);
         return 0;
     } catch (const std::exception& e) {
         std::fprintf(stderr, "bench_generate: %s\n", e.what());

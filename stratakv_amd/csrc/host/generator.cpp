@@ -277,12 +277,6 @@ void Generator::set_graph_replay(bool enabled) {
     }
 }
 
-void Generator::set_fold_output_projection(bool enabled) {
-    (void)skv_stream_synchronize(stream_);
-    release_step_graph();  // captured with the other setting
-    for (auto& b : blocks_) b.set_fold_output_projection(enabled);
-}
-
 void Generator::release_step_graph() noexcept {
     if (step_graph_) (void)skv_graph_destroy(step_graph_);
     step_graph_ = nullptr;

@@ -198,34 +198,18 @@ bool TransformerBlock::forward_into_at(const Tensor& hidden_states, Tensor& outp
                                        bias_of(wv), hidden, num_heads, num_kv_heads, head_dim, step,
                                        rope_cos_sin, rope_positions, fp(queries), fp(keys), fp(values), s),
                   "forward_into_at: fused rmsnorm + q/k/v + rope");
-    const float scale = 1.0f / std::sqrt(static_cast<float>(head_dim));
-    // The attention with o_proj + residual folded into its launch where the
-    // geometry has a folded kernel (the same bits as the two calls below).
-    const int folded =
-        fold_output_projection_
-            ? skv_paged_decode_append_oproj(cfp(queries), cfp(keys), cfp(values), block_pool.key_cache(),
-                                            block_pool.value_cache(), block_pool.total_blocks(), device_table,
-                                            table_capacity, step + 1, num_heads, num_kv_heads, head_dim,
-                                            block_pool.block_size(), scale, wo.weight().raw_data(), wdtype(wo),
-                                            stride_k(wo), stride_n(wo), bias_of(wo), cfp(hidden_states), hidden,
-                                            fp(context), fp(down), s)
-            : SKV_ERR_UNSUPPORTED;
-    if (folded != SKV_ERR_UNSUPPORTED) {
-        detail::check(folded, "forward_into_at: KV append + paged attention + o_proj + residual");
-    } else {
-        detail::check(skv_paged_decode_append(cfp(queries), SKV_DTYPE_FP32, cfp(keys), cfp(values),
-                                              SKV_DTYPE_FP32, block_pool.key_cache(), block_pool.value_cache(),
-                                              block_pool.total_blocks(), device_table, table_capacity, step + 1,
-                                              1, num_heads, num_kv_heads, head_dim, block_pool.block_size(), scale,
-                                              fp(context), ws.raw_data(), ws.num_elements() * ws.element_size(),
-                                              s),
-                      "forward_into_at: KV append + paged attention");
-        detail::check(skv_linear_residual_f32(cfp(context), wo.weight().raw_data(), wdtype(wo), stride_k(wo),
-                                              stride_n(wo), static_cast<int>(wo.input_dim()),
-                                              static_cast<int>(wo.output_dim()), bias_of(wo),
-                                              cfp(hidden_states), fp(down), s),
-                      "forward_into_at: fused o_proj + residual");
-    }
+    detail::check(skv_paged_decode_append(cfp(queries), SKV_DTYPE_FP32, cfp(keys), cfp(values), SKV_DTYPE_FP32,
+                                          block_pool.key_cache(), block_pool.value_cache(),
+                                          block_pool.total_blocks(), device_table, table_capacity, step + 1, 1,
+                                          num_heads, num_kv_heads, head_dim, block_pool.block_size(),
+                                          1.0f / std::sqrt(static_cast<float>(head_dim)), fp(context),
+                                          ws.raw_data(), ws.num_elements() * ws.element_size(), s),
+                  "forward_into_at: KV append + paged attention");
+    detail::check(skv_linear_residual_f32(cfp(context), wo.weight().raw_data(), wdtype(wo), stride_k(wo),
+                                          stride_n(wo), static_cast<int>(wo.input_dim()),
+                                          static_cast<int>(wo.output_dim()), bias_of(wo), cfp(hidden_states),
+                                          fp(down), s),
+                  "forward_into_at: fused o_proj + residual");
     detail::check(skv_fused_gate_up_swiglu_f32(cfp(down), cfp(norm2_.gamma()), norm2_.epsilon(),
                                                gate_proj_.weight().raw_data(), up_proj_.weight().raw_data(),
                                                wdtype(gate_proj_), stride_k(gate_proj_), stride_n(gate_proj_),

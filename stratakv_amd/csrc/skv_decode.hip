@@ -38,7 +38,6 @@
 //   than 2^8, which after the first blocks is rare; the result is exact since
 //   numerator and denominator share the same reference max.
 #include "skv_append.h"
-#include "skv_gemv.h"
 
 #include <algorithm>
 #include <cmath>
@@ -82,15 +81,6 @@ struct DecodeParams {
     uint16_t* v_pool_w;
     int merge_cw;          // output columns per merge workgroup (a multiple of 64)
     int max_slots;         // (range, head group) pairs the workspace holds partials for
-    // Output projection folded into the attention (FOLD instances, one
-    // sequence): o_y = W out + o_bias + o_residual, W = o_n bf16 rows of
-    // Hq * HD elements, o_row_bytes apart.
-    const void* o_w;
-    int64_t o_row_bytes;
-    const float* o_bias;
-    const float* o_residual;
-    float* o_y;
-    int o_n;
 };
 
 constexpr int kMaxHeadDim = 512;
@@ -248,59 +238,11 @@ __device__ __forceinline__ void store_scaled(float* o, const float* x, float sc)
 // also its register budget (launch bound).
 constexpr int mfma_waves_per_simd(int HD, int G) { return HD == 64 && G < 16 ? 2 : 1; }
 
-// The two output-projection rows of one wavefront of a FOLD workgroup (work
-// item `item`: rows 2 item and 2 item + 1, clamped to the last row; `live`
-// false past the end), with their bias and residual.  start() requests the
-// weight rows; finish() takes the context from LDS and stores y = W ctx +
-// bias + residual with the arithmetic of the separate projection
-// (fused_gemv_kernel's residual mode: PairPrefetch, then (a + bias) + res).
-constexpr int kFoldNU = 4;  // wave-wide weight loads per row requested up front (K <= 2,048 bf16: all)
-
-struct FoldRows {
-    PairPrefetch<true, kFoldNU, true> pf;
-    int ra, rb;
-    bool live;
-    float ba, bb, res_a, res_b;
-
-    __device__ __forceinline__ FoldRows(const DecodeParams& p, int item) {
-        live = 2 * item < p.o_n;
-        ra = min(2 * item, p.o_n - 1);
-        rb = min(ra + 1, p.o_n - 1);
-        ba = p.o_bias != nullptr ? p.o_bias[ra] : 0.0f;
-        bb = p.o_bias != nullptr ? p.o_bias[rb] : 0.0f;
-        res_a = p.o_residual[ra];
-        res_b = p.o_residual[rb];
-    }
-    __device__ __forceinline__ void start(const DecodeParams& p, int K, int lane) {
-        const char* w = static_cast<const char*>(p.o_w);
-        pf = PairPrefetch<true, kFoldNU, true>(w + ra * p.o_row_bytes, w + rb * p.o_row_bytes, K, lane);
-    }
-    __device__ __forceinline__ void finish(const DecodeParams& p, const float* ctx, int K, int lane) {
-        float a, b;
-        pf.finish(ctx, K, lane, a, b);
-        if (lane == 0) {
-            p.o_y[ra] = (a + ba) + res_a;
-            if (rb != ra) p.o_y[rb] = (b + bb) + res_b;
-        }
-    }
-};
-
 // SPLIT: short tables (at most WPW * NBUF blocks per sequence).  Workgroup
 // = one (sequence, kv head) segment; its WPW wavefronts take consecutive
-// sub-ranges ("parts") of at most NBUF blocks, so every K/V load of the
-// segment is in flight at once, and merge their partials through LDS (no
-// merge launch).
-// FOLD_HKV > 0 (with SPLIT; one sequence of FOLD_HKV kv heads): the output
-// projection folded in.  Every workgroup computes the whole context: its
-// WPW / FOLD_HKV wavefronts per kv head take parts sub, sub + WPW / FOLD_HKV,
-// ... of that head, each part computed and the parts merged exactly as SPLIT
-// does (so the context has SPLIT's bits), into LDS; then each wavefront
-// serves two output rows (FoldRows).  The length and the table row are
-// loaded before the weight rows and the K/V blocks after them, so neither
-// wait on the weights, whose stream overlaps the attention.  Workgroup 0
-// writes the context to `out` and stores the appended K/V row; the others
-// substitute that row in registers.
-template <int HD, int G, bool QF32, int WPW, int NBUF, bool SPLIT = false, int FOLD_HKV = 0>
+// sub-ranges of at most NBUF blocks, so every K/V load of the segment is in
+// flight at once, and merge their partials through LDS (no merge launch).
+template <int HD, int G, bool QF32, int WPW, int NBUF, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_mfma_kernel(DecodeParams p) {
     constexpr int BS = 16;
     constexpr int CH = HD / 8;      // 16-byte chunks per row
@@ -310,10 +252,6 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
     constexpr int QP = QF32 ? 2 : 1;
     static_assert(CH * RPI == 64 && RPI * TPL == BS && NMF * 4 == CH, "lane layout");
     static_assert(G >= 1 && G <= 16, "group size");
-    constexpr bool FOLD = FOLD_HKV > 0;
-    static_assert(!FOLD || (SPLIT && QF32 && WPW % FOLD_HKV == 0), "fold layout");
-    constexpr int SUBS = FOLD ? WPW / FOLD_HKV : WPW;      // stride of a wavefront's parts
-    constexpr int NSLOT = (FOLD ? FOLD_HKV : 1) * WPW;     // SPLIT: part slots (WPW per kv head)
 
     // Per-wavefront LDS: the WPW wavefronts of a workgroup serve the same
     // range for WPW consecutive kv heads and only meet at the work split.
@@ -321,9 +259,8 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
     __shared__ u32x4_t k_all[WPW][BS * CH];  // one block of K for this kv head, swizzled
     __shared__ float p_all[WPW][BS * 16];    // probabilities [token][head]
     __shared__ float h_all[WPW][2][16];      // per-head (sum, max) at the end of a segment
-    __shared__ float part_acc[SPLIT ? NSLOT : 1][SPLIT ? G * HD : 1];  // SPLIT: the parts' partials
-    __shared__ float part_ml[SPLIT ? NSLOT : 1][2][16];
-    __shared__ float ctx_s[FOLD ? FOLD_HKV * G * HD : 1];              // FOLD: the context
+    __shared__ float part_acc[SPLIT ? WPW : 1][SPLIT ? G * HD : 1];  // SPLIT: per-wave partials
+    __shared__ float part_ml[SPLIT ? WPW : 1][2][16];
 
     const int wv = WPW == 1 ? 0 : __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
@@ -335,9 +272,8 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
     auto swz = [](int row) { return CH == 16 ? row : ((row >> 1) & 7); };
     const int Hkv = p.Hkv;
     const int w = blockIdx.x * WPW + wv;    // Hkv % WPW == 0: one range per workgroup
-    const int kvh = FOLD ? wv / SUBS : (SPLIT ? static_cast<int>(blockIdx.x % Hkv) : w % Hkv);
+    const int kvh = SPLIT ? static_cast<int>(blockIdx.x % Hkv) : w % Hkv;
     const int range = w / Hkv;
-    const int seq = FOLD ? 0 : static_cast<int>(blockIdx.x / Hkv);  // SPLIT's sequence
 
     // SPLIT: the workgroup names its sequence, so the sequence's whole table
     // row (max_blocks <= 64 entries, one per lane) is loaded beside the
@@ -345,11 +281,9 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
     // dependent load (lengths and table together) instead of two.
     int trow = 0;
     if constexpr (SPLIT) {
-        const int64_t row = static_cast<int64_t>(seq) * p.max_blocks;
+        const int64_t row = static_cast<int64_t>(blockIdx.x / Hkv) * p.max_blocks;
         trow = p.tables[row + std::min(lane, p.max_blocks - 1)];
     }
-    // FOLD: the length here, with the table row (one sequence; no prefix scan).
-    const int fold_len = FOLD ? seq_len(p, 0) : 0;
     // Query chunks of head kvh * G + t (lanes t < G; zero for padded heads),
     // as loaded.  SPLIT knows its sequence here, so its queries are requested
     // with the table row and arrive by the split's barrier (one dependent
@@ -374,59 +308,33 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
             }
         }
     };
-    if constexpr (SPLIT) load_q_raw(seq);
+    if constexpr (SPLIT) load_q_raw(static_cast<int>(blockIdx.x / Hkv));
 
-    // FOLD: this wavefront's output rows (bias and residual first, then the
-    // weight rows, all in flight through the attention).
-    const int fold_k = p.Hq * HD;
-    auto fold_rows = [&]() {
-        if constexpr (FOLD) {
-            FoldRows fr(p, blockIdx.x * WPW + wv);
-            fr.start(p, fold_k, lane);
-            return fr;
-        } else {
-            return 0;
-        }
-    }();
-
-    // Flattened block bounds of sequence bb: the prefix in LDS, or (FOLD,
-    // one sequence) [0, its blocks) from the length loaded above.
-    const int fold_nb = fold_len <= 0 ? 0 : std::min(cdiv(fold_len, p.bs), p.max_blocks);
-    auto seg_begin = [&](int bb) {
-        if constexpr (FOLD) return 0;
-        else return P_s[bb];
-    };
-    auto seg_end = [&](int bb) {
-        if constexpr (FOLD) return fold_nb;
-        else return P_s[bb + 1];
-    };
-
-    const WorkSplit split = FOLD ? WorkSplit{0, 0, 0, 0, 0} : build_split(p, P_s, !SPLIT);
+    const WorkSplit split = build_split(p, P_s, !SPLIT);
     if (!SPLIT && range >= split.used) return;
     const int64_t row_stride = static_cast<int64_t>(Hkv) * HD;
     const int block_bytes = static_cast<int>(BS * row_stride * 2);
     int range_lo = SPLIT ? 0 : split.lo(range);
     int range_hi = SPLIT ? 0 : split.lo(range + 1);
     int b = 0;
-    int part = FOLD ? wv % SUBS : wv;  // SPLIT: this wavefront's (first) part
     if constexpr (SPLIT) {
-        // Part `part`: blocks [part * NBUF, part * NBUF + NBUF) of the segment.
-        b = seq;
-        range_lo = std::min(seg_begin(b) + part * NBUF, seg_end(b));
-        range_hi = std::min(range_lo + NBUF, seg_end(b));
+        // Wavefront wv: blocks [wv * NBUF, wv * NBUF + NBUF) of the segment.
+        b = static_cast<int>(blockIdx.x / Hkv);
+        range_lo = std::min(P_s[b] + wv * NBUF, P_s[b + 1]);
+        range_hi = std::min(range_lo + NBUF, P_s[b + 1]);
     }
     int pos = range_lo;
-    int end = SPLIT ? range_hi : std::min(range_hi, split.total);
+    const int end = SPLIT ? range_hi : std::min(range_hi, split.total);
     if (!SPLIT) b = find_seq(P_s, p.B, pos);
     const int h0 = kvh * G;
 
     while (!SPLIT || pos < end) {
-        const int seg_lo = seg_begin(b), seg_hi = seg_end(b);
+        const int seg_lo = P_s[b], seg_hi = P_s[b + 1];
         const int nb = seg_hi - seg_lo;
         const int k0 = pos - seg_lo;
         const int stop = std::min(end, seg_hi);
         const int kb1 = stop - seg_lo;
-        const int L = FOLD ? fold_len : seq_len(p, b);
+        const int L = seq_len(p, b);
         const int Leff = std::min(L, nb * BS);
         const int32_t* table = p.tables + static_cast<int64_t>(b) * p.max_blocks;
 
@@ -638,7 +546,7 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
             }
         }
 
-        if (kb_new >= 0 && r == r_new && (!FOLD || blockIdx.x == 0)) {  // fused append: store the new row
+        if (kb_new >= 0 && r == r_new) {  // fused append: store the new row
             *reinterpret_cast<u32x4_t*>(p.k_pool_w + new_dst) = knew;
             *reinterpret_cast<u32x4_t*>(p.v_pool_w + new_dst) = vnew;
         }
@@ -677,12 +585,11 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
             if (final_out) {
                 store_scaled<VPH>(p.out + (static_cast<int64_t>(b) * p.Hq + h0 + g) * HD + d0, x,
                                   lsum > 0.0f ? 1.0f / lsum : 0.0f);
-            } else if constexpr (SPLIT) {  // the part's LDS slot
-                const int slot = (FOLD ? kvh * WPW : 0) + part;
-                store_scaled<VPH>(&part_acc[slot][g * HD + d0], x, 1.0f);
+            } else if constexpr (SPLIT) {  // this wavefront's LDS slot
+                store_scaled<VPH>(&part_acc[wv][g * HD + d0], x, 1.0f);
                 if (owns_ml) {
-                    part_ml[slot][0][g] = h_s[1][g];
-                    part_ml[slot][1][g] = lsum;
+                    part_ml[wv][0][g] = h_s[1][g];
+                    part_ml[wv][1][g] = lsum;
                 }
             } else {  // workspace slot, merged by decode_merge_kernel
                 store_scaled<VPH>(p.ws_acc + (prow * G + g) * HD + d0, x, 1.0f);
@@ -693,12 +600,6 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
 
         wave_lds_sync();
 
-        if constexpr (FOLD) {  // this wavefront's next part of its kv head
-            part += SUBS;
-            pos = std::min(seg_begin(b) + part * NBUF, seg_end(b));
-            end = std::min(pos + NBUF, seg_end(b));
-            continue;
-        }
         pos = stop;
         if (SPLIT || pos >= end) break;
         do {
@@ -706,33 +607,7 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
         } while (P_s[b + 1] == P_s[b]);
     }
 
-    if constexpr (FOLD) {
-        // SPLIT's merge for every kv head, into the context in LDS (zeros for
-        // an empty sequence); workgroup 0 also writes it out.  Then the
-        // output rows of every wavefront.
-        const int nw = std::min(WPW, cdiv(fold_nb, NBUF));
-        __syncthreads();
-        for (int col = threadIdx.x; col < FOLD_HKV * G * HD; col += 64 * WPW) {
-            const int hk = col / (G * HD), hc = col - hk * (G * HD), g = hc / HD;
-            const float (*ml)[2][16] = part_ml + hk * WPW;
-            const float (*pa)[G * HD] = part_acc + hk * WPW;
-            float M = -INFINITY;
-            for (int u = 0; u < nw; ++u) M = fmaxf(M, ml[u][0][g]);
-            float L = 0.0f, A = 0.0f;
-            if (M != -INFINITY) {
-                for (int u = 0; u < nw; ++u) {
-                    const float wgt = fast_exp2(ml[u][0][g] - M);
-                    L = fmaf(wgt, ml[u][1][g], L);
-                    A = fmaf(wgt, pa[u][hc], A);
-                }
-            }
-            const float o = nw > 0 && L > 0.0f ? A / L : 0.0f;
-            ctx_s[col] = o;
-            if (blockIdx.x == 0) p.out[col] = o;
-        }
-        __syncthreads();
-        if (fold_rows.live) fold_rows.finish(p, ctx_s, fold_k, lane);
-    } else if constexpr (SPLIT) {
+    if constexpr (SPLIT) {
         // Merge the WPW sub-range partials of the segment (wavefronts past the
         // segment's last sub-range hold none):
         //   out = sum_w acc_w 2^(m_w - M) / sum_w l_w 2^(m_w - M),  M = max_w m_w.
@@ -1306,19 +1181,6 @@ int launch_mfma(const DecodeParams& p, hipStream_t s) {
     return set_error(SKV_ERR_UNSUPPORTED, "no MFMA decode kernel for head_dim %d, group %d", p.HD, G);
 }
 
-// The attention with the output projection folded in: workgroups of 8
-// wavefronts, two output rows per wavefront.  Instances for the geometries
-// of the decoders this build runs (head_dim 64; 8 query heads per kv head
-// over 4 kv heads, 4 per kv head over 2); others return false.
-bool launch_fold(const DecodeParams& p, hipStream_t s) {
-    const int G = p.Hq / p.Hkv;
-    const unsigned groups = static_cast<unsigned>(cdiv(cdiv(p.o_n, 2), 8));
-    if (p.HD == 64 && G == 8 && p.Hkv == 4) decode_mfma_kernel<64, 8, true, 8, 2, true, 4><<<groups, 512, 0, s>>>(p);
-    else if (p.HD == 64 && G == 4 && p.Hkv == 2) decode_mfma_kernel<64, 4, true, 8, 2, true, 2><<<groups, 512, 0, s>>>(p);
-    else return false;
-    return true;
-}
-
 // The load-pattern calibration on the grid the MFMA decode kernel (bf16
 // queries, stream-K mode) would be launched with for the same geometry.
 template <int HD, int G>
@@ -1602,42 +1464,6 @@ extern "C" int skv_paged_decode_append_noalloc(const void* q, int q_dtype, const
     void* ws = nullptr;
     if (int rc = scratch_for_current_device(&ws)) return rc;
     return run_decode(p, q_dtype, ws, kScratchBytes, static_cast<hipStream_t>(stream), slots);
-}
-
-extern "C" int skv_paged_decode_append_oproj(const float* q, const float* k_new, const float* v_new,
-                                             uint16_t* k_pool, uint16_t* v_pool, int64_t total_blocks,
-                                             const int32_t* block_table, int max_blocks, const int32_t* context_len,
-                                             int num_q_heads, int num_kv_heads, int head_dim, int block_size,
-                                             float scale, const void* o_weight, int o_dtype, int64_t o_stride_k,
-                                             int64_t o_stride_n, const float* o_bias, const float* residual,
-                                             int hidden, float* context, float* out, void* stream) {
-    const char* fn = "skv_paged_decode_append_oproj";
-    DecodeParams p;
-    if (int rc = fill_decode_append(p, fn, q, SKV_DTYPE_FP32, k_new, v_new, SKV_DTYPE_FP32, k_pool, v_pool,
-                                    total_blocks, block_table, max_blocks, context_len, 1, num_q_heads,
-                                    num_kv_heads, head_dim, block_size, scale, context))
-        return rc;
-    SKV_REQUIRE(o_weight && residual && out && hidden > 0, "%s: invalid output projection pointers or sizes", fn);
-    SKV_REQUIRE(o_dtype == SKV_DTYPE_BF16 || o_dtype == SKV_DTYPE_FP32, "%s: unknown weight dtype %d", fn, o_dtype);
-    // The fold computes what skv_paged_decode_append's short-table kernel and
-    // skv_linear_residual_f32's one-row kernel compute, and runs only where
-    // those two would take exactly those kernels.
-    const int K = num_q_heads * head_dim;
-    const bool fits = mfma_path_ok(p, SKV_DTYPE_FP32) && aligned16(k_new) && aligned16(v_new) &&
-                      max_blocks <= 8 * 2 && o_dtype == SKV_DTYPE_BF16 && o_stride_k == 1 && o_stride_n >= K &&
-                      aligned16(o_weight) && (o_stride_n * 2) % 16 == 0 && K >= 512 && K <= 2048;
-    if (!fits)
-        return set_error(SKV_ERR_UNSUPPORTED, "%s: no folded kernel for this geometry or weight layout", fn);
-    p.o_w = o_weight;
-    p.o_row_bytes = o_stride_n * 2;
-    p.o_bias = o_bias;
-    p.o_residual = residual;
-    p.o_y = out;
-    p.o_n = hidden;
-    if (!launch_fold(p, static_cast<hipStream_t>(stream)))
-        return set_error(SKV_ERR_UNSUPPORTED, "%s: no folded kernel for head_dim %d, %d query heads over %d kv heads",
-                         fn, head_dim, num_q_heads, num_kv_heads);
-    return check_launch("decode_mfma_kernel (output projection folded)");
 }
 
 extern "C" size_t skv_paged_attention_decode_workspace_bytes(int num_q_heads, int num_kv_heads,

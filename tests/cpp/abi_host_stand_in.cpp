@@ -161,8 +161,6 @@ size_t skv_paged_attention_decode_workspace_bytes(int, int, int) { return 0; }
 
 int skv_paged_decode_append(const void*, int, const void*, const void*, int, uint16_t*, uint16_t*, int64_t, const int32_t*, int, const int32_t*, int, int, int, int, int, float, float*, void*, size_t, void*) { return fail("skv_paged_decode_append: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
-int skv_paged_decode_append_oproj(const float*, const float*, const float*, uint16_t*, uint16_t*, int64_t, const int32_t*, int, const int32_t*, int, int, int, int, float, const void*, int, int64_t, int64_t, const float*, const float*, int, float*, float*, void*) { return fail("skv_paged_decode_append_oproj: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
-
 int skv_paged_prefill(const void*, int, const uint16_t*, const uint16_t*, int64_t, const int32_t*, int, const int32_t*, const int32_t*, int, int, int, int, int, int, float, float*, void*) { return fail("skv_paged_prefill: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }
 
 int skv_rmsnorm_f32(const float*, float*, const float*, int, int, float, void*) { return fail("skv_rmsnorm_f32: no GPU in the host-only build", SKV_ERR_UNSUPPORTED); }

@@ -165,7 +165,6 @@ struct GenArgs {
     long long seed = -1;  // >= 0: Generator::seed_sampler
     int first_max = -1;   // >= 0: max_new of the first call (later calls use MAX_NEW)
     bool eager = false;   // Generator::set_graph_replay(false)
-    bool unfolded = false;   // Generator::set_fold_output_projection(false)
     bool check_pools = false;   // fill the pools with a pattern, report whether generate leaves them unchanged
     std::vector<int> tokens;
 };
@@ -187,7 +186,6 @@ GenArgs parse_gen(int first, int argc, char** argv) {
         else if (s == "--seed") a.seed = std::stoll(argv[++i]);
         else if (s == "--first-max") a.first_max = std::stoi(argv[++i]);
         else if (s == "--eager") a.eager = true;
-        else if (s == "--unfolded") a.unfolded = true;
         else if (s == "--check-pools") a.check_pools = true;
     }
     for (; i < argc; ++i) a.tokens.push_back(std::stoi(argv[i]));
@@ -223,7 +221,6 @@ int cmd_generate(int argc, char** argv) {
         generation::Generator gen(cfg, std::move(l.weights));
         if (a.seed >= 0) gen.seed_sampler(static_cast<std::uint32_t>(a.seed));
         if (a.eager) gen.set_graph_replay(false);
-        if (a.unfolded) gen.set_fold_output_projection(false);
         // FNV-1a over every layer's K and V pool bytes.
         auto pools_hash = [&]() {
             std::uint64_t hsh = 1469598103934665603ull;

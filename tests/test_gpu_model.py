@@ -515,24 +515,6 @@ def test_graph_replay_matches_eager(gpu, ckpt_dir, max_new):
     assert g["logits_fnv"] == e["logits_fnv"] and len(set(g["logits_fnv"])) == 1
 
 
-@pytest.mark.timeout(400)  # the tinyllama checkpoint is written first when no earlier test wrote it
-@pytest.mark.parametrize("name,max_new", [("small", 240), ("tinyllama", 128)])
-def test_folded_output_projection_matches_separate_launches(gpu, ckpt_dir, name, max_new):
-    """Replayed steps whose attention and o_proj + residual run as one launch
-    (skv_paged_decode_append_oproj, both geometries it has kernels for) give
-    the tokens, block tables and last logits (bits) of replayed steps with
-    the two launches, and of step-by-step launches."""
-    path, _ = make_checkpoint.ensure(name, ckpt_dir)
-    prompt = [3, 141, 59, 265, 358, 979, 323, 846, 264, 338, 327, 950, 288, 419, 716, 939]
-    runs = {mode: tool("generate", path, max_new, -1, *flags, "--", *prompt)
-            for mode, flags in (("folded", []), ("unfolded", ["--unfolded"]), ("eager", ["--eager"]))}
-    assert all(r["ok"] for r in runs.values()), runs
-    assert runs["folded"]["replayed"] == runs["unfolded"]["replayed"] == [1]
-    for mode in ("unfolded", "eager"):
-        for key in ("runs", "tables", "logits_fnv"):
-            assert runs["folded"][key] == runs[mode][key], (mode, key)
-
-
 def test_graph_replay_past_the_short_table_limit_runs_eagerly(gpu, ckpt_dir):
     path = _small(ckpt_dir)
     g = tool("generate", path, 241, -1, "--", *range(1, 17))   # 257 tokens: 17 blocks
