@@ -81,6 +81,7 @@ struct DecodeParams {
     uint16_t* v_pool_w;
     int merge_cw;          // output columns per merge workgroup (a multiple of 64)
     int max_slots;         // (range, head group) pairs the workspace holds partials for
+    int seg_cost;          // stream-K: blocks' worth of time charged per segment start (see WorkSplit)
 };
 
 constexpr int kMaxHeadDim = 512;
@@ -112,6 +113,16 @@ __device__ __forceinline__ int seq_blocks(const DecodeParams& p, int b) {
 // the segment starts strictly inside the range (then it is the range's last
 // segment), 0 otherwise (the range's first segment).
 //
+// A segment start costs a wavefront about a memory round trip more than a
+// block (finalising the previous segment, then the new segment's queries and
+// table entries before its first K/V loads): per-wave timestamps of cfg3 on
+// MI355X showed the ranges that cross a segment boundary ending ~4.3 us (~3.4
+// blocks' time) after the others, and making most of the last ones.  So the
+// split is over a "virtual" space in which every non-empty segment occupies
+// seg_cost empty slots before its blocks: P_s holds that prefix, segment b's
+// blocks sit at [seg_first(b), P_s[b + 1]), and a range that covers a segment
+// start gets seg_cost fewer blocks.  The merge kernel reads the same prefix.
+//
 // Ranges [0, half) hold `per` blocks and ranges [half, used) `per_b`.  The
 // split is even (half = used, per_b = per) unless the grid is paired: two
 // workgroups per CU, two wavefronts per SIMD, where the second half of the
@@ -122,6 +133,7 @@ __device__ __forceinline__ int seq_blocks(const DecodeParams& p, int b) {
 // times the blocks of the second.
 // ---------------------------------------------------------------------------
 constexpr int kPairShare = 24;
+constexpr int kSegmentCost = 4;  // seg_cost of the MFMA kernel's stream-K split
 
 struct WorkSplit {
     int total, per, used, half, per_b;
@@ -150,6 +162,7 @@ __device__ WorkSplit build_split(const DecodeParams& p, int* P_s, bool stream_k)
                     for (int64_t i = lane; i < row; i += 64) o[i] = 0.0f;
                 }
             }
+            if (v > 0) v += p.seg_cost;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const int u = __shfl_up(v, o, 64);
@@ -190,6 +203,12 @@ __device__ WorkSplit build_split(const DecodeParams& p, int* P_s, bool stream_k)
         }
     }
     return ws;
+}
+
+// Position of segment b's first block: past its seg_cost empty slots, unless
+// it has no blocks.
+__device__ __forceinline__ int seg_first(const int* P, int b, int seg_cost) {
+    return P[b] + (P[b + 1] > P[b] ? seg_cost : 0);
 }
 
 // Sequence owning flattened block `pos`: P[b] <= pos < P[b+1].
@@ -329,7 +348,11 @@ __global__ __launch_bounds__(64 * WPW, mfma_waves_per_simd(HD, G)) void decode_m
     const int h0 = kvh * G;
 
     while (!SPLIT || pos < end) {
-        const int seg_lo = P_s[b], seg_hi = P_s[b + 1];
+        const int seg_lo = SPLIT ? P_s[b] : seg_first(P_s, b, p.seg_cost), seg_hi = P_s[b + 1];
+        if (!SPLIT) {  // the range may start among, or end within, the segment's empty slots
+            if (end <= seg_lo) break;
+            pos = std::max(pos, seg_lo);
+        }
         const int nb = seg_hi - seg_lo;
         const int k0 = pos - seg_lo;
         const int stop = std::min(end, seg_hi);
@@ -671,7 +694,9 @@ __global__ __launch_bounds__(64 * WPW) void block_stream_checksum_kernel(DecodeP
     const int lane_off_b = static_cast<int>((r * row_stride + static_cast<int64_t>(kvh) * HD + c * 8) * 2);
 
     while (true) {
-        const int seg_lo = P_s[b], seg_hi = P_s[b + 1];
+        const int seg_lo = seg_first(P_s, b, p.seg_cost), seg_hi = P_s[b + 1];
+        if (end <= seg_lo) break;
+        pos = std::max(pos, seg_lo);
         const int k0 = pos - seg_lo;
         const int stop = std::min(end, seg_hi);
         const int kb1 = stop - seg_lo;
@@ -964,7 +989,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
     split.half = p.plan[3];
     split.per_b = p.plan[4];
     const int32_t* P = p.plan + 5;
-    const int lo = P[b], hi = P[b + 1];
+    const int lo = seg_first(P, b, p.seg_cost), hi = P[b + 1];
     float* out0 = p.out + (static_cast<int64_t>(b) * p.Hq + grp * NH) * HD;
     if (lo == hi) return;  // no context: zeroed by the attention kernel
     const int r0 = split.range_of(lo), r1 = split.range_of(hi - 1);
@@ -1110,7 +1135,7 @@ bool paired_grid(const DecodeParams& p, int waves, int max_per_simd) {
 // batches and short contexts launch a small grid) and no more than the
 // workspace has partial slots for.
 int decode_ranges(const DecodeParams& p, int waves) {
-    const int64_t max_work = static_cast<int64_t>(p.B) * p.max_blocks;
+    const int64_t max_work = static_cast<int64_t>(p.B) * (p.max_blocks + p.seg_cost);
     return static_cast<int>(std::max<int64_t>(
         1, std::min<int64_t>({waves / p.Hseg, cdiv<int64_t>(max_work, p.min_per), p.max_slots / p.Hseg})));
 }
@@ -1151,7 +1176,7 @@ int launch_pair(K kern, int wpw, int max_per_simd, DecodeParams p, hipStream_t s
 //   of 8 KiB, 1 wavefront per SIMD; head_dim 64: 3 blocks of 4 KiB, 2 per
 //   SIMD).  More requests in flight than that lowers the achieved rate.
 template <int HD, int G, bool QF32>
-int launch_mfma_shape(const DecodeParams& p, hipStream_t s) {
+int launch_mfma_shape(DecodeParams p, hipStream_t s) {
     constexpr int NB = HD == 64 ? 3 : 2;
     constexpr int PER_SIMD = mfma_waves_per_simd(HD, G);
     const char* name = "decode_mfma_kernel";
@@ -1165,6 +1190,7 @@ int launch_mfma_shape(const DecodeParams& p, hipStream_t s) {
         decode_mfma_kernel<HD, G, QF32, 8, 2, true><<<groups, 512, lds, s>>>(p);
         return check_launch(name);
     }
+    p.seg_cost = kSegmentCost;
     if (p.Hkv % 4 == 0) return launch_pair(decode_mfma_kernel<HD, G, QF32, 4, NB>, 4, PER_SIMD, p, s, name);
     if (p.Hkv % 2 == 0) return launch_pair(decode_mfma_kernel<HD, G, QF32, 2, NB>, 2, PER_SIMD, p, s, name);
     return launch_pair(decode_mfma_kernel<HD, G, QF32, 1, NB>, 1, PER_SIMD, p, s, name);
@@ -1188,6 +1214,7 @@ int launch_checksum_shape(DecodeParams p, uint32_t* sums, hipStream_t s) {
     constexpr int NB = HD == 64 ? 3 : 2;
     constexpr int PER_SIMD = mfma_waves_per_simd(HD, G);
     const size_t lds = sizeof(int) * (static_cast<size_t>(p.B) + 1);
+    p.seg_cost = kSegmentCost;
     auto go = [&](auto decode_kern, auto sum_kern, int wpw) {
         const int waves = resident_waves(decode_kern, wpw, lds, PER_SIMD);
         p.ranges = decode_ranges(p, waves);
@@ -1264,10 +1291,12 @@ int run_decode(DecodeParams p, int q_dtype, void* workspace, size_t workspace_by
                          "decode workspace of %zu bytes is smaller than the %zu required",
                          workspace_bytes, w.total);
     // Flattened (sequence, block) indices are int32 on the device.
-    const long long flat_bound = static_cast<long long>(std::min(p.B, kMaxBatchPerLaunch)) * p.max_blocks;
+    const long long flat_bound =
+        static_cast<long long>(std::min(p.B, kMaxBatchPerLaunch)) * (static_cast<long long>(p.max_blocks) + kSegmentCost);
     if (flat_bound >= (1ll << 30))
         return set_error(SKV_ERR_UNSUPPORTED,
-                         "batch x table width = %lld exceeds the 2^30 work index range", flat_bound);
+                         "batch x (table width + %d) = %lld exceeds the 2^30 work index range", kSegmentCost,
+                         flat_bound);
     const size_t q_elem = q_dtype == SKV_DTYPE_FP32 ? 4 : 2;
     const int B = p.B;
     for (int b0 = 0; b0 < B; b0 += kMaxBatchPerLaunch) {
