@@ -45,6 +45,23 @@ def test_batched_geometries(gpu, geom, q_dtype):
     _check(gpu, case, f"geom={geom} q={q_dtype}")
 
 
+@pytest.mark.parametrize("B", [64, 3000])
+@pytest.mark.parametrize("geom", [TL, L3], ids=["tl", "l3"])
+def test_many_short_segments_with_empty_ones(gpu, geom, B):
+    """Stream-K over short segments (1-5 blocks, a fifth of the sequences
+    empty) in tables wider than the short-table limit.  The split puts empty
+    slots before every segment's blocks, so ranges begin and end among them.
+    At B=64 the ranges are 4 slots wide: some hold no block at all, and one
+    segment is cut by several ranges."""
+    Hq, Hkv, hd = geom
+    rng = np.random.default_rng(B + hd)
+    lens = rng.integers(1, 80, B).astype(np.int32)
+    lens[rng.random(B) < 0.2] = 0
+    case = make_case(B, Hq, Hkv, hd, 16, lens, layout="random", seed=B, extra_cols=20)
+    assert case["tables"].shape[1] > 16   # the stream-K kernel, not the short-table one
+    _check(gpu, case, f"short segments geom={geom} B={B}")
+
+
 @pytest.mark.parametrize("layout", ["sequential", "round_robin", "random"])
 def test_table_layouts(gpu, layout):
     Hq, Hkv, hd = L3
