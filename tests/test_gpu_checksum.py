@@ -75,6 +75,18 @@ def test_many_short_sequences(gpu):
     run(gpu, 32, 4, 64, lens, max_blocks=5, total=4000, seed=9, bad_entries=50)
 
 
+@pytest.mark.parametrize("B", [64, 2000])
+def test_short_and_empty_segments_ranges_among_segment_slots(gpu, B):
+    # The split charges every non-empty segment a few empty slots before its
+    # blocks: with 1-5 block segments and a fifth of the sequences empty,
+    # range boundaries fall among those slots (at B=64 the ranges are 4 slots
+    # wide, some hold no block); every block is still read exactly once.
+    rng = np.random.default_rng(B)
+    lens = rng.integers(1, 80, size=B)
+    lens[rng.random(B) < 0.2] = 0
+    run(gpu, 32, 4, 64, lens, max_blocks=25, total=6000, seed=B, bad_entries=B // 20)
+
+
 def test_rejects_other_geometries(gpu):
     skv = gpu
     buf = skv.DeviceBuffer(1 << 16)
