@@ -122,3 +122,33 @@ def test_positions_outside_table_are_not_written(gpu):
     gk, gv, rk, rv = _run(gpu, k_new, v_new, 8, bs, Hkv, hd, tables, [0, 10], 20)
     _bits_equal(gk, rk, "K")
     _bits_equal(gv, rv, "V")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_ragged_appends(gpu, seed):
+    """Seeded random cases: kv geometry (odd head dims included), batch, each
+    sequence's start position and token count (ragged offsets, some empty),
+    bf16 or fp32 source, and tables with entries outside the pool."""
+    rng = np.random.default_rng(700 + seed)
+    Hkv, hd = [(4, 64), (8, 128), (2, 96), (3, 20), (1, 128), (8, 64)][rng.integers(0, 6)]
+    bs = 16
+    B = int(rng.integers(1, 9))
+    counts = rng.choice([0, 1, 2, 15, 16, 17, 40, 100], B).astype(np.int32)
+    starts = rng.choice([0, 1, 15, 16, 17, 100, 255], B).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    lens = np.maximum(starts + counts, 1)
+    total = sum(-(-int(L) // bs) for L in lens) + 9
+    tables = make_tables(lens, bs, total, "random", rng, extra_cols=int(rng.integers(0, 3)))
+    for _ in range(int(rng.integers(0, 4))):    # entries outside the pool: those rows are skipped
+        tables[rng.integers(0, B), rng.integers(0, tables.shape[1])] = int(rng.choice([-1, total, total + 5]))
+    rows = max(int(offsets[-1]), 1)
+    if rng.random() < 0.5:
+        k_new = rng.standard_normal((rows, Hkv * hd), dtype=np.float32)
+        v_new = rng.standard_normal((rows, Hkv * hd), dtype=np.float32)
+    else:
+        k_new = rng.integers(0, 0x10000, size=(rows, Hkv * hd), dtype=np.uint16)
+        v_new = rng.integers(0, 0x10000, size=(rows, Hkv * hd), dtype=np.uint16)
+    gk, gv, rk, rv = _run(gpu, k_new, v_new, total, bs, Hkv, hd, tables, starts, int(max(counts.max(), 1)),
+                          offsets=offsets)
+    _bits_equal(gk, rk, f"seed {seed} K")
+    _bits_equal(gv, rv, f"seed {seed} V")
